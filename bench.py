@@ -1,0 +1,236 @@
+"""OpWorks-on-MI355X benchmark driver (one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+
+A "step" is one pass of the hot path over one batch of synthetic input already
+resident in HBM. Timing uses HIP events recorded on the stream the kernels are
+launched on, bracketed by a device synchronize on both sides; the average
+launch duration is K events apart divided by K. Working sets smaller than
+512 MiB are rotated over several buffer sets so the 256 MB Infinity Cache
+cannot serve them.
+
+`value` is the headline workload's throughput; every measured workload also
+appears under `components` with its own roofline. `cpu_baseline` times the CPU
+oracle (the restatement of the reference kernels) on a bounded sample on this
+host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+import opworks_amd as ow  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+BF16_PEAK_TFLOPS = 2500.0
+SEED = 1234
+METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
+
+
+def cpu_threads() -> int:
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+class Timer:
+    """K launches between two events on `stream`, synchronized on both sides."""
+
+    def __init__(self, stream):
+        self.stream = stream
+        self.t0, self.t1 = ow.Event(), ow.Event()
+
+    def run(self, fn, steps: int, warmup: int) -> float:
+        for i in range(warmup):
+            fn(i)
+        ow.check(ow.lib().opw_device_synchronize())
+        self.t0.record(self.stream)
+        for i in range(steps):
+            fn(i)
+        self.t1.record(self.stream)
+        self.t1.synchronize()
+        ow.check(ow.lib().opw_device_synchronize())
+        return self.t0.elapsed_ms(self.t1) / steps
+
+
+def roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) -> dict:
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+# ------------------------------------------------------------------ workloads
+def wl_map(stream, steps, warmup):
+    """Config 2a: ScaleAdd(alpha=2.5) over n = 2^28 fp32; 12 B/element."""
+    n = 1 << 28
+    a, b, c = (ow.DeviceBuffer.empty(n) for _ in range(3))
+    ow.fill_uniform(a, SEED, 0, -1.0, 1.0, stream=stream)
+    ow.fill_uniform(b, SEED, 1, -1.0, 1.0, stream=stream)
+    ms = Timer(stream).run(lambda i: ow.ops.map_scale_add(a, b, c, n, 2.5, stream=stream), steps, warmup)
+    nbytes = 12 * n
+    gbs = nbytes / ms / 1e6
+    return {"workload": "map_scale_add_n2^28", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
+            "kernel": "map_pack_kernel", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+
+
+def wl_reduce(stream, steps, warmup):
+    """Config 2b: Sum over n = 2^28 fp32 (partial + final launch); 4 B/element."""
+    n = 1 << 28
+    c = ow.DeviceBuffer.empty(n)
+    ow.fill_uniform(c, SEED, 2, -1.0, 1.0, stream=stream)
+    out = ow.DeviceBuffer.empty(1)
+    ws = ow.DeviceBuffer.empty(ow.ops.reduction_workspace_size(n))
+    ms = Timer(stream).run(lambda i: ow.ops.reduce(c, out, n, "sum", ws, stream=stream), steps, warmup)
+    nbytes = 4 * n
+    gbs = nbytes / ms / 1e6
+    return {"workload": "reduce_sum_n2^28", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
+            "kernel": "reduce_partial_kernel+reduce_final_kernel", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+
+
+def _rotating(rows, cols, sets, fill):
+    xs, ys = [], []
+    for k in range(sets):
+        x = ow.DeviceBuffer.empty(rows * cols)
+        fill(x, k)
+        xs.append(x)
+        ys.append(ow.DeviceBuffer.empty(rows * cols))
+    return xs, ys
+
+
+def wl_softmax(stream, steps, warmup):
+    """Config 1: softmax rows=4096, cols=1024, x = 4*N(0,1); 8 B/element; 16 rotating buffer pairs (1 GiB)."""
+    rows, cols, sets = 4096, 1024, 16
+    xs, ys = _rotating(rows, cols, sets, lambda x, k: ow.fill_normal(x, SEED, 100 + k, 0.0, 4.0, stream=stream))
+    ms = Timer(stream).run(lambda i: ow.ops.softmax(xs[i % sets], ys[i % sets], rows, cols, stream=stream),
+                           steps, warmup)
+    nbytes = 8 * rows * cols
+    gbs = nbytes / ms / 1e6
+    return {"workload": "softmax_4096x1024", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
+            "kernel": "softmax_rows_reg_kernel<1,4>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+
+
+def wl_rmsnorm(stream, steps, warmup):
+    """Config 2c: RMSNorm rows=8192, cols=2048, eps=1e-5, gamma ~ U[0.5,1.5]; 4 rotating pairs (1 GiB)."""
+    rows, cols, sets = 8192, 2048, 4
+    xs, ys = _rotating(rows, cols, sets, lambda x, k: ow.fill_normal(x, SEED, 200 + k, 0.0, 1.0, stream=stream))
+    w = ow.DeviceBuffer.empty(cols)
+    ow.fill_uniform(w, SEED, 210, 0.5, 1.5, stream=stream)
+    ms = Timer(stream).run(lambda i: ow.ops.rms_norm(xs[i % sets], w, ys[i % sets], rows, cols, 1e-5, stream=stream),
+                           steps, warmup)
+    nbytes = 8 * rows * cols + 4 * cols
+    gbs = nbytes / ms / 1e6
+    return {"workload": "rms_norm_8192x2048", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
+            "kernel": "rms_norm_reg_kernel<1,8>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+
+
+WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm}
+HEADLINE = "map"
+
+
+# --------------------------------------------------------------- CPU baseline
+def cpu_baseline(name: str) -> dict:
+    """Times the oracle on a bounded sample of the same workload on this host."""
+    from tests import oracle as orc
+
+    threads = cpu_threads()
+    orc.set_threads(threads)
+    if name == "map":
+        n = 1 << 26
+        a = orc.fill_uniform(n, SEED, 0, -1, 1, mt=True)
+        b = orc.fill_uniform(n, SEED, 1, -1, 1, mt=True)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            orc.map_scale_add(a, b, 2.5, mt=True)
+            reps += 1
+            if time.perf_counter() - t0 > 10.0 or reps >= 200:
+                break
+        dt = (time.perf_counter() - t0) / reps
+        return {"value": round(12 * n / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": f"oracle orc_map_scale_add_mt over n=2^26 (768 MiB), {reps} reps, ~10 s"}
+    if name == "reduce":
+        n = 1 << 24
+        x = orc.fill_uniform(n, SEED, 2, -1, 1, mt=True)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 3.0:
+            orc.reduce(x, "sum")
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        return {"value": round(4 * n / dt / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"oracle orc_reduce (reference order, single thread) over n=2^24, {reps} reps"}
+    if name == "softmax":
+        rows, cols = 1024, 1024
+        x = orc.fill_normal(rows * cols, SEED, 100, 0, 4, mt=True)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 3.0:
+            orc.softmax_rows(x, rows, cols)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        return {"value": round(8 * rows * cols / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": f"oracle orc_softmax_rows, 1024 of the 4096 rows, {reps} reps"}
+    if name == "rmsnorm":
+        rows, cols = 2048, 2048
+        x = orc.fill_normal(rows * cols, SEED, 200, 0, 1, mt=True)
+        w = orc.fill_uniform(cols, SEED, 210, 0.5, 1.5)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 3.0:
+            orc.rms_norm_rows(x, w, rows, cols, 1e-5)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        return {"value": round(8 * rows * cols / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": f"oracle orc_rms_norm_rows, 2048 of the 8192 rows, {reps} reps"}
+    return {}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="all", help="all | " + " | ".join(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the path has no multi-GPU component; see DESIGN.md for how it would shard)", file=sys.stderr)
+        return 2
+    names = list(WORKLOADS) if args.workload == "all" else args.workload.split(",")
+    headline = HEADLINE if HEADLINE in names else names[0]
+    stream = ow.Stream()
+    results = {}
+    for name in names:
+        results[name] = WORKLOADS[name](stream.handle, args.steps, args.warmup)
+        print(f"[bench] {name}: {results[name]['value']:.1f} {results[name]['unit']} "
+              f"({results[name]['ms']:.4f} ms/step)", file=sys.stderr, flush=True)
+    head = results[headline]
+    line = {
+        "metric": METRIC,
+        "value": round(head["value"], 2),
+        "unit": head["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (counter-based seeded generator, seed 1234, resident in HBM)",
+        "config": {"workload": head["workload"], "device": ow.device_name()},
+        "roofline": head["roofline"],
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(headline),
+        "components": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                       for k, v in results.items()},
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,85 @@
+/* C ABI of libopworks_amd.so: the fixed-function operators of the OpWorks hot
+ * path, plus the device-memory, stream and event plumbing a host without HIP
+ * headers (ctypes, cgo, JNI) needs to drive them.
+ *
+ * Conventions (all functions):
+ *  - plain pointers and sizes; `stream` is a hipStream_t passed as void*
+ *    (NULL = the legacy default stream, as in the reference's C++ API);
+ *  - operator entry points enqueue asynchronously and return 0, or -1 after a
+ *    contract violation (the reference throws std::invalid_argument there:
+ *    include/core/cuda_utils.cuh:29-49); the message is then available from
+ *    opw_last_error() on the calling thread. No C++ exception crosses the ABI.
+ *  - HIP runtime failures abort the process, as OPWORKS_CUDA_CHECK does in the
+ *    reference (include/core/cuda_utils.cuh:13-21).
+ *  - sizes follow the reference: nonnegative int, at most INT_MAX elements.
+ */
+#ifndef OPWORKS_OPS_H
+#define OPWORKS_OPS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *opw_last_error(void);
+
+/* ---- device plumbing (reference: include/core/device_buffer.cuh:12-67) ---- */
+int opw_device_count(int *count);
+int opw_set_device(int device);
+int opw_device_name(char *out, int out_len);
+int opw_device_cu_count(int *cus);
+int opw_malloc(void **ptr, size_t bytes);
+int opw_free(void *ptr);
+/* Blocking copies on `stream` (DeviceBuffer::from_host / to_host semantics). */
+int opw_memcpy_htod(void *dst, const void *src, size_t bytes, void *stream);
+int opw_memcpy_dtoh(void *dst, const void *src, size_t bytes, void *stream);
+int opw_memcpy_dtod(void *dst, const void *src, size_t bytes, void *stream);
+int opw_memset(void *dst, int value, size_t bytes, void *stream);
+int opw_stream_create(void **stream);
+int opw_stream_destroy(void *stream);
+/* reference: synchronize(stream), include/core/cuda_utils.cuh:100-102 */
+int opw_stream_synchronize(void *stream);
+int opw_device_synchronize(void);
+int opw_event_create(void **event);
+int opw_event_destroy(void *event);
+int opw_event_record(void *event, void *stream);
+int opw_event_synchronize(void *event);
+int opw_event_elapsed_ms(void *start, void *stop, float *ms);
+
+/* ---- seeded synthetic inputs (counter-based; bit-identical to the CPU
+ * restatement in oracle/, so the checker regenerates the same arrays) ---- */
+int opw_fill_uniform_f32(float *dst, int64_t n, uint64_t seed, uint64_t stream_id, float lo, float hi, void *stream);
+int opw_fill_normal_f32(float *dst, int64_t n, uint64_t seed, uint64_t stream_id, float mean, float stddev,
+                        void *stream);
+
+/* ---- map (reference: ops::map, include/ops/elementwise.cuh:68-77) ----
+ * Exact in-place use is allowed, partial overlap is not. n == 0 is a no-op. */
+/* out[i] = fmaf(alpha, a[i], b[i])  — README ScaleAdd functor (README.md:78-83) under nvcc's FMA contraction */
+int opw_map_scale_add_f32(const float *a, const float *b, float *out, int n, float alpha, void *stream);
+/* out[i] = a[i] + b[i]  — framework.cu Add / tests/integration/vector_add.cu:7-11 */
+int opw_map_add_f32(const float *a, const float *b, float *out, int n, void *stream);
+/* out[i] = factor * in[i]  — framework.cu Scale */
+int opw_map_scale_f32(const float *in, float *out, int n, float factor, void *stream);
+/* out[i] = fmaxf(in[i], 0)  — tests/integration/relu.cu:7-10 */
+int opw_map_relu_f32(const float *in, float *out, int n, void *stream);
+
+/* ---- reduce (reference: ops::reduce<Op>, include/ops/reduction.cuh:34-67) ---- */
+int opw_reduction_workspace_size(int n);
+/* op: 0 = sum, 1 = max, 2 = product. workspace == NULL selects the
+ * stream-ordered-allocation convenience overload. */
+int opw_reduce_f32(const float *in, float *out, int n, int op, float *workspace, int workspace_size, void *stream);
+
+/* ---- rows (reference: include/ops/softmax.cuh:36-43, layer_norm.cuh:38-47, rms_norm.cuh:31-40) ---- */
+int opw_softmax_f32(const float *in, float *out, int rows, int cols, void *stream);
+int opw_layer_norm_f32(const float *in, float *out, const float *gamma, const float *beta, int rows, int cols,
+                       float eps, void *stream);
+int opw_rms_norm_f32(const float *x, const float *weight, float *out, int rows, int cols, float eps, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OPWORKS_OPS_H */

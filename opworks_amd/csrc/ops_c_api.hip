@@ -1,0 +1,329 @@
+// extern "C" operator surface of libopworks_amd.so (declared in
+// include/opworks_ops.h). Each entry point validates through the same
+// opworks::ops function a C++ caller would use, then enqueues.
+
+#include <hip/hip_runtime.h>
+
+#include "../include/core/random.hpp"
+#include "../include/ops/elementwise.hpp"
+#include "../include/ops/layer_norm.hpp"
+#include "../include/ops/reduction.hpp"
+#include "../include/ops/rms_norm.hpp"
+#include "../include/ops/softmax.hpp"
+#include "c_api_common.hpp"
+
+using opworks::capi::guard;
+
+namespace {
+
+hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+struct ScaleAdd {
+    float alpha;
+    __device__ float operator()(float a, float b) const { return fmaf(alpha, a, b); }
+};
+struct Add {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct Scale {
+    float factor;
+    __device__ float operator()(float x) const { return factor * x; }
+};
+struct Relu {
+    __device__ float operator()(float x) const { return fmaxf(x, 0.f); }
+};
+struct Sum {
+    static __device__ float identity() { return 0.f; }
+    static __device__ float combine(float a, float b) { return a + b; }
+};
+struct Max {
+    static __device__ float identity() { return -INFINITY; }
+    static __device__ float combine(float a, float b) { return fmaxf(a, b); }
+};
+struct Product {
+    static __device__ float identity() { return 1.f; }
+    static __device__ float combine(float a, float b) { return a * b; }
+};
+
+__global__ void __launch_bounds__(256) fill_uniform_kernel(float *dst, int64_t n, uint64_t key, float lo, float hi) {
+    OPWORKS_GRID_LOOP(i, n) { dst[i] = opworks::rng::uniform(key, static_cast<uint64_t>(i), lo, hi); }
+}
+__global__ void __launch_bounds__(256) fill_normal_kernel(float *dst, int64_t n, uint64_t key, float mean, float sd) {
+    OPWORKS_GRID_LOOP(i, n) { dst[i] = opworks::rng::normal(key, static_cast<uint64_t>(i), mean, sd); }
+}
+
+int fill_grid(int64_t n) {
+    const int64_t cap = static_cast<int64_t>(opworks::detail::cu_count()) * 16;
+    const int64_t need = opworks::detail::blocks_for64(n, 256);
+    return static_cast<int>(need < cap ? need : cap);
+}
+
+template <typename Op> void reduce_dispatch(const float *in, float *out, int n, float *ws, int ws_size, hipStream_t s) {
+    if (ws)
+        opworks::ops::reduce<Op>(in, out, n, opworks::DeviceSpan<float>(ws, ws_size), s);
+    else
+        opworks::ops::reduce<Op>(in, out, n, s);
+}
+
+} // namespace
+
+extern "C" {
+
+const char *opw_last_error(void) { return opworks::capi::last_error().c_str(); }
+
+int opw_device_count(int *count) {
+    return guard([&] {
+        opworks::detail::require(count != nullptr, "null count pointer");
+        OPWORKS_HIP_CHECK(hipGetDeviceCount(count));
+        return 0;
+    });
+}
+
+int opw_set_device(int device) {
+    return guard([&] {
+        OPWORKS_HIP_CHECK(hipSetDevice(device));
+        return 0;
+    });
+}
+
+int opw_device_name(char *out, int out_len) {
+    return guard([&] {
+        opworks::detail::require(out != nullptr && out_len > 0, "null name buffer");
+        int dev = 0;
+        OPWORKS_HIP_CHECK(hipGetDevice(&dev));
+        hipDeviceProp_t prop;
+        OPWORKS_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
+        std::snprintf(out, static_cast<size_t>(out_len), "%s (%s)", prop.name, prop.gcnArchName);
+        return 0;
+    });
+}
+
+int opw_device_cu_count(int *cus) {
+    return guard([&] {
+        opworks::detail::require(cus != nullptr, "null pointer");
+        *cus = opworks::detail::cu_count();
+        return 0;
+    });
+}
+
+int opw_malloc(void **ptr, size_t bytes) {
+    return guard([&] {
+        opworks::detail::require(ptr != nullptr, "null output pointer");
+        *ptr = nullptr;
+        if (bytes)
+            OPWORKS_HIP_CHECK(hipMalloc(ptr, bytes));
+        return 0;
+    });
+}
+
+int opw_free(void *ptr) {
+    return guard([&] {
+        if (ptr)
+            OPWORKS_HIP_CHECK(hipFree(ptr));
+        return 0;
+    });
+}
+
+int opw_memcpy_htod(void *dst, const void *src, size_t bytes, void *stream) {
+    return guard([&] {
+        opworks::detail::require(bytes == 0 || (dst && src), "null copy pointer");
+        if (bytes) {
+            OPWORKS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, as_stream(stream)));
+            opworks::synchronize(as_stream(stream));
+        }
+        return 0;
+    });
+}
+
+int opw_memcpy_dtoh(void *dst, const void *src, size_t bytes, void *stream) {
+    return guard([&] {
+        opworks::detail::require(bytes == 0 || (dst && src), "null copy pointer");
+        if (bytes) {
+            OPWORKS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, as_stream(stream)));
+            opworks::synchronize(as_stream(stream));
+        }
+        return 0;
+    });
+}
+
+int opw_memcpy_dtod(void *dst, const void *src, size_t bytes, void *stream) {
+    return guard([&] {
+        opworks::detail::require(bytes == 0 || (dst && src), "null copy pointer");
+        if (bytes)
+            OPWORKS_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)));
+        return 0;
+    });
+}
+
+int opw_memset(void *dst, int value, size_t bytes, void *stream) {
+    return guard([&] {
+        opworks::detail::require(bytes == 0 || dst, "null memset pointer");
+        if (bytes)
+            OPWORKS_HIP_CHECK(hipMemsetAsync(dst, value, bytes, as_stream(stream)));
+        return 0;
+    });
+}
+
+int opw_stream_create(void **stream) {
+    return guard([&] {
+        opworks::detail::require(stream != nullptr, "null stream pointer");
+        hipStream_t s;
+        OPWORKS_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+        *stream = s;
+        return 0;
+    });
+}
+
+int opw_stream_destroy(void *stream) {
+    return guard([&] {
+        if (stream)
+            OPWORKS_HIP_CHECK(hipStreamDestroy(as_stream(stream)));
+        return 0;
+    });
+}
+
+int opw_stream_synchronize(void *stream) {
+    return guard([&] {
+        opworks::synchronize(as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_device_synchronize(void) {
+    return guard([&] {
+        OPWORKS_HIP_CHECK(hipDeviceSynchronize());
+        return 0;
+    });
+}
+
+int opw_event_create(void **event) {
+    return guard([&] {
+        opworks::detail::require(event != nullptr, "null event pointer");
+        hipEvent_t e;
+        OPWORKS_HIP_CHECK(hipEventCreate(&e));
+        *event = e;
+        return 0;
+    });
+}
+
+int opw_event_destroy(void *event) {
+    return guard([&] {
+        if (event)
+            OPWORKS_HIP_CHECK(hipEventDestroy(static_cast<hipEvent_t>(event)));
+        return 0;
+    });
+}
+
+int opw_event_record(void *event, void *stream) {
+    return guard([&] {
+        opworks::detail::require(event != nullptr, "null event");
+        OPWORKS_HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(event), as_stream(stream)));
+        return 0;
+    });
+}
+
+int opw_event_synchronize(void *event) {
+    return guard([&] {
+        opworks::detail::require(event != nullptr, "null event");
+        OPWORKS_HIP_CHECK(hipEventSynchronize(static_cast<hipEvent_t>(event)));
+        return 0;
+    });
+}
+
+int opw_event_elapsed_ms(void *start, void *stop, float *ms) {
+    return guard([&] {
+        opworks::detail::require(start && stop && ms, "null event or output");
+        OPWORKS_HIP_CHECK(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
+        return 0;
+    });
+}
+
+int opw_fill_uniform_f32(float *dst, int64_t n, uint64_t seed, uint64_t stream_id, float lo, float hi, void *stream) {
+    return guard([&] {
+        opworks::detail::require(n >= 0 && (n == 0 || dst), "fill requires a buffer and a nonnegative size");
+        if (n)
+            opworks::launch_async(as_stream(stream), fill_uniform_kernel, fill_grid(n), 256, dst, n,
+                                  opworks::rng::stream_key(seed, stream_id), lo, hi);
+        return 0;
+    });
+}
+
+int opw_fill_normal_f32(float *dst, int64_t n, uint64_t seed, uint64_t stream_id, float mean, float stddev,
+                        void *stream) {
+    return guard([&] {
+        opworks::detail::require(n >= 0 && (n == 0 || dst), "fill requires a buffer and a nonnegative size");
+        if (n)
+            opworks::launch_async(as_stream(stream), fill_normal_kernel, fill_grid(n), 256, dst, n,
+                                  opworks::rng::stream_key(seed, stream_id), mean, stddev);
+        return 0;
+    });
+}
+
+int opw_map_scale_add_f32(const float *a, const float *b, float *out, int n, float alpha, void *stream) {
+    return guard([&] {
+        opworks::ops::map(a, b, out, n, ScaleAdd{alpha}, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_map_add_f32(const float *a, const float *b, float *out, int n, void *stream) {
+    return guard([&] {
+        opworks::ops::map(a, b, out, n, Add{}, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_map_scale_f32(const float *in, float *out, int n, float factor, void *stream) {
+    return guard([&] {
+        opworks::ops::map(in, out, n, Scale{factor}, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_map_relu_f32(const float *in, float *out, int n, void *stream) {
+    return guard([&] {
+        opworks::ops::map(in, out, n, Relu{}, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_reduction_workspace_size(int n) {
+    return guard([&] { return opworks::ops::reduction_workspace_size(n); });
+}
+
+int opw_reduce_f32(const float *in, float *out, int n, int op, float *workspace, int workspace_size, void *stream) {
+    return guard([&] {
+        hipStream_t s = as_stream(stream);
+        switch (op) {
+        case 0: reduce_dispatch<Sum>(in, out, n, workspace, workspace_size, s); break;
+        case 1: reduce_dispatch<Max>(in, out, n, workspace, workspace_size, s); break;
+        case 2: reduce_dispatch<Product>(in, out, n, workspace, workspace_size, s); break;
+        default: throw std::invalid_argument("unknown reduction op (0 sum, 1 max, 2 product)");
+        }
+        return 0;
+    });
+}
+
+int opw_softmax_f32(const float *in, float *out, int rows, int cols, void *stream) {
+    return guard([&] {
+        opworks::ops::softmax(in, out, rows, cols, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_layer_norm_f32(const float *in, float *out, const float *gamma, const float *beta, int rows, int cols,
+                       float eps, void *stream) {
+    return guard([&] {
+        opworks::ops::layer_norm(in, out, gamma, beta, rows, cols, eps, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_rms_norm_f32(const float *x, const float *weight, float *out, int rows, int cols, float eps, void *stream) {
+    return guard([&] {
+        opworks::ops::rms_norm(x, weight, out, rows, cols, eps, as_stream(stream));
+        return 0;
+    });
+}
+
+} // extern "C"

@@ -1,0 +1,87 @@
+#pragma once
+
+// ops::rms_norm — row-wise RMSNorm (reference: include/ops/rms_norm.cuh:9-40).
+// Per row: ss = sum(x^2); inv = rsqrtf(ss/cols + eps); out = x * inv * weight.
+
+#include "rowwise_kernels.hpp"
+
+namespace opworks::detail {
+
+template <int kW, int kV>
+__global__ __launch_bounds__(RowShape<kW>::kBlock) void rms_norm_reg_kernel(const float *__restrict__ x,
+                                                                             const float *__restrict__ weight,
+                                                                             float *__restrict__ out, int rows,
+                                                                             int cols, float eps) {
+    const RowPos p = row_position<kW>(rows);
+    const int n4 = cols / 4;
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(x + p.row * cols);
+    f32x4 v[kV];
+    float local = 0.f;
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+        const int q = pack_index<kW>(p, k);
+        if (p.active && q < n4) {
+            v[k] = src[q];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                local = fmaf(v[k][j], v[k][j], local);
+        }
+    }
+    const float inv = rsqrtf(row_combine<kW>(wave::sum(local), p, wave::Add{}) / cols + eps);
+    const f32x4 *w4 = reinterpret_cast<const f32x4 *>(weight);
+    f32x4 *dst = reinterpret_cast<f32x4 *>(out + p.row * cols);
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+        const int q = pack_index<kW>(p, k);
+        if (p.active && q < n4) {
+            const f32x4 w = w4[q];
+            f32x4 r;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                r[j] = v[k][j] * inv * w[j];
+            __builtin_nontemporal_store(r, dst + q);
+        }
+    }
+}
+
+static __global__ void __launch_bounds__(kThreads)
+    rms_norm_stream_kernel(const float *__restrict__ x, const float *__restrict__ weight, float *__restrict__ out,
+                           int cols, float eps) {
+    const float *row_in = x + static_cast<int64_t>(blockIdx.x) * cols;
+    float *row_out = out + static_cast<int64_t>(blockIdx.x) * cols;
+    float local = 0.f;
+    OPWORKS_BLOCK_LOOP(j, cols) {
+        const float v = row_in[j];
+        local = fmaf(v, v, local);
+    }
+    const float inv = rsqrtf(block_reduce_all<ReduceSum>(local) / cols + eps);
+    OPWORKS_BLOCK_LOOP(j, cols) { row_out[j] = row_in[j] * inv * weight[j]; }
+}
+
+} // namespace opworks::detail
+
+namespace opworks::ops {
+
+// RMSNorm over the last dim of a rows x cols matrix (no mean subtraction).
+inline void rms_norm(const float *x, const float *weight, float *out, int rows, int cols, float eps,
+                     hipStream_t stream = nullptr) {
+    detail::validate_matrix(rows, cols);
+    if (rows == 0)
+        return;
+    detail::require(cols > 0, "rms_norm requires positive columns for nonempty rows");
+    detail::require(x && weight && out, "rms_norm requires non-null pointers");
+    detail::require(eps > 0.f, "rms_norm epsilon must be positive");
+    const bool packed = detail::aligned16(x) && detail::aligned16(weight) && detail::aligned16(out);
+    const detail::RowPlan plan = detail::plan_row(cols, packed);
+    if (plan.waves == 0) {
+        launch_async(stream, detail::rms_norm_stream_kernel, rows, kThreads, x, weight, out, cols, eps);
+        return;
+    }
+    detail::dispatch_row_plan(plan, [&](auto w, auto v) {
+        constexpr int kW = decltype(w)::value, kV = decltype(v)::value;
+        launch_async(stream, detail::rms_norm_reg_kernel<kW, kV>, detail::row_grid<kW>(rows),
+                     detail::RowShape<kW>::kBlock, x, weight, out, rows, cols, eps);
+    });
+}
+
+} // namespace opworks::ops

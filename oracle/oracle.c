@@ -1,0 +1,311 @@
+/* OpWorks CPU oracle — TEST INFRASTRUCTURE ONLY (see oracle.h). */
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define REF_THREADS 256   /* kThreads, include/core/config.cuh:15-17,56 */
+#define REF_WARP 32       /* kWarpSize, include/core/config.cuh:46 */
+#define REF_MAX_PARTIALS 1024 /* kMaxThreadsPerBlock, include/core/config.cuh:47 */
+
+/* ------------------------------------------------------------------ threads */
+static int g_threads = 1;
+void orc_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+int orc_get_threads(void) { return g_threads; }
+
+typedef void (*range_fn)(void *ctx, int64_t begin, int64_t end);
+struct range_job {
+    range_fn fn;
+    void *ctx;
+    int64_t begin, end;
+};
+static void *range_worker(void *p) {
+    struct range_job *j = (struct range_job *)p;
+    j->fn(j->ctx, j->begin, j->end);
+    return NULL;
+}
+/* Splits [0, n) into g_threads contiguous chunks. */
+static void parallel_for(int64_t n, range_fn fn, void *ctx) {
+    int t = g_threads;
+    if (t <= 1 || n < 2) {
+        fn(ctx, 0, n);
+        return;
+    }
+    if (t > n)
+        t = (int)n;
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * t);
+    struct range_job *jobs = (struct range_job *)malloc(sizeof(struct range_job) * t);
+    for (int i = 0; i < t; ++i) {
+        jobs[i].fn = fn;
+        jobs[i].ctx = ctx;
+        jobs[i].begin = n * i / t;
+        jobs[i].end = n * (i + 1) / t;
+        pthread_create(&th[i], NULL, range_worker, &jobs[i]);
+    }
+    for (int i = 0; i < t; ++i)
+        pthread_join(th[i], NULL);
+    free(th);
+    free(jobs);
+}
+
+/* ---------------------------------------------------------------------- rng */
+static const uint64_t kGolden = 0x9E3779B97F4A7C15ull;
+static uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+uint64_t orc_stream_key(uint64_t seed, uint64_t stream) { return mix64(seed ^ mix64(stream + kGolden)); }
+static uint64_t draw(uint64_t key, uint64_t i) { return mix64(key + (i + 1) * kGolden); }
+
+void orc_fill_uniform(float *dst, int64_t n, uint64_t seed, uint64_t stream, float lo, float hi) {
+    const uint64_t key = orc_stream_key(seed, stream);
+    for (int64_t i = 0; i < n; ++i) {
+        const float u = (float)(uint32_t)(draw(key, (uint64_t)i) >> 40) * 0x1p-24f;
+        dst[i] = fmaf(u, hi - lo, lo);
+    }
+}
+
+void orc_fill_normal(float *dst, int64_t n, uint64_t seed, uint64_t stream, float mean, float sd) {
+    const uint64_t key = orc_stream_key(seed, stream);
+    for (int64_t i = 0; i < n; ++i) {
+        const uint64_t a = draw(key, 2 * (uint64_t)i), b = draw(key, 2 * (uint64_t)i + 1);
+        const int32_t s = (int32_t)(a >> 40) + (int32_t)((a >> 16) & 0xFFFFFFu) + (int32_t)(b >> 40) +
+                          (int32_t)((b >> 16) & 0xFFFFFFu) - (1 << 25);
+        const float z = (float)s * 0x1.bb67aep-24f;
+        dst[i] = fmaf(z, sd, mean);
+    }
+}
+
+struct fill_ctx {
+    float *dst;
+    uint64_t seed, stream;
+    float p0, p1;
+    int normal;
+};
+/* The generators are counter-based, so a chunk [lo, hi) is filled independently. */
+static void fill_range(void *p, int64_t lo, int64_t hi) {
+    struct fill_ctx *c = (struct fill_ctx *)p;
+    const uint64_t key = orc_stream_key(c->seed, c->stream);
+    for (int64_t i = lo; i < hi; ++i) {
+        if (c->normal) {
+            const uint64_t a = draw(key, 2 * (uint64_t)i), b = draw(key, 2 * (uint64_t)i + 1);
+            const int32_t s = (int32_t)(a >> 40) + (int32_t)((a >> 16) & 0xFFFFFFu) + (int32_t)(b >> 40) +
+                              (int32_t)((b >> 16) & 0xFFFFFFu) - (1 << 25);
+            c->dst[i] = fmaf((float)s * 0x1.bb67aep-24f, c->p1, c->p0);
+        } else {
+            const float u = (float)(uint32_t)(draw(key, (uint64_t)i) >> 40) * 0x1p-24f;
+            c->dst[i] = fmaf(u, c->p1 - c->p0, c->p0);
+        }
+    }
+}
+void orc_fill_uniform_mt(float *dst, int64_t n, uint64_t seed, uint64_t stream, float lo, float hi) {
+    struct fill_ctx c = {dst, seed, stream, lo, hi, 0};
+    parallel_for(n, fill_range, &c);
+}
+void orc_fill_normal_mt(float *dst, int64_t n, uint64_t seed, uint64_t stream, float mean, float sd) {
+    struct fill_ctx c = {dst, seed, stream, mean, sd, 1};
+    parallel_for(n, fill_range, &c);
+}
+
+/* ---------------------------------------------------------------------- map */
+/* README.md:78-83 ScaleAdd `alpha * a + b`; nvcc contracts it to one FMA, and
+ * ops::map applies the functor per element (include/ops/elementwise.cuh:20-35). */
+void orc_map_scale_add(const float *a, const float *b, float *out, int64_t n, float alpha) {
+    for (int64_t i = 0; i < n; ++i)
+        out[i] = fmaf(alpha, a[i], b[i]);
+}
+struct map_ctx {
+    const float *a, *b;
+    float *out;
+    float alpha;
+};
+static void map_range(void *p, int64_t lo, int64_t hi) {
+    struct map_ctx *c = (struct map_ctx *)p;
+    orc_map_scale_add(c->a + lo, c->b + lo, c->out + lo, hi - lo, c->alpha);
+}
+void orc_map_scale_add_mt(const float *a, const float *b, float *out, int64_t n, float alpha) {
+    struct map_ctx c = {a, b, out, alpha};
+    parallel_for(n, map_range, &c);
+}
+
+/* ------------------------------------------------------------------- reduce */
+static float combine(int op, float a, float b) {
+    switch (op) {
+    case 0: return a + b;
+    case 1: return fmaxf(a, b);
+    default: return a * b;
+    }
+}
+static float identity(int op) { return op == 0 ? 0.f : (op == 1 ? -INFINITY : 1.f); }
+
+/* One 32-lane __shfl_down_sync tree (offsets 16..1); lanes whose source is
+ * past the warp keep their own value (include/core/block_reduce.cuh:17-18). */
+static float warp_tree(const float *lanes, int op) {
+    float cur[REF_WARP], nxt[REF_WARP];
+    memcpy(cur, lanes, sizeof(cur));
+    for (int off = REF_WARP / 2; off > 0; off >>= 1) {
+        for (int l = 0; l < REF_WARP; ++l)
+            nxt[l] = combine(op, cur[l], l + off < REF_WARP ? cur[l + off] : cur[l]);
+        memcpy(cur, nxt, sizeof(cur));
+    }
+    return cur[0];
+}
+
+/* block_reduce<Op> (include/core/block_reduce.cuh:11-31): warp trees, lane 0
+ * of each warp to shared[warp], warp 0 re-reduces with missing warps = identity. */
+float orc_block_reduce(const float *vals, int nthreads, int op) {
+    const int nwarps = (nthreads + REF_WARP - 1) / REF_WARP;
+    float shared[REF_MAX_PARTIALS / REF_WARP];
+    for (int w = 0; w < nwarps; ++w)
+        shared[w] = warp_tree(vals + w * REF_WARP, op);
+    float lanes[REF_WARP];
+    for (int l = 0; l < REF_WARP; ++l)
+        lanes[l] = l < nwarps ? shared[l] : identity(op);
+    return warp_tree(lanes, op);
+}
+
+/* reduce_partial_kernel (include/ops/reduction.cuh:9-17) for one block: each
+ * thread combines in[g], in[g+stride], ... in ascending order, then block_reduce. */
+static float partial_block(const float *in, int64_t n, int block, int grid, int op) {
+    float acc[REF_THREADS];
+    const int64_t stride = (int64_t)grid * REF_THREADS;
+    for (int t = 0; t < REF_THREADS; ++t) {
+        float a = identity(op);
+        for (int64_t i = (int64_t)block * REF_THREADS + t; i < n; i += stride)
+            a = combine(op, a, in[i]);
+        acc[t] = a;
+    }
+    return orc_block_reduce(acc, REF_THREADS, op);
+}
+
+/* ops::reduce (include/ops/reduction.cuh:34-54): blocks = min(ceil(n/256), 1024);
+ * one block writes the result directly; otherwise partials, then
+ * reduce_final_kernel (:19-27) with one block of 256 threads. */
+float orc_reduce(const float *in, int n, int op) {
+    int blocks = n / REF_THREADS + (n % REF_THREADS != 0);
+    if (blocks <= 1)
+        return partial_block(in, n, 0, 1, op);
+    if (blocks > REF_MAX_PARTIALS)
+        blocks = REF_MAX_PARTIALS;
+    float *partial = (float *)malloc(sizeof(float) * blocks);
+    for (int b = 0; b < blocks; ++b)
+        partial[b] = partial_block(in, n, b, blocks, op);
+    const float r = partial_block(partial, blocks, 0, 1, op);
+    free(partial);
+    return r;
+}
+
+double orc_sum_f64(const float *in, int64_t n) {
+    double s = 0;
+    for (int64_t i = 0; i < n; ++i)
+        s += in[i];
+    return s;
+}
+double orc_sum_abs_f64(const float *in, int64_t n) {
+    double s = 0;
+    for (int64_t i = 0; i < n; ++i)
+        s += fabs((double)in[i]);
+    return s;
+}
+
+/* --------------------------------------------------------------------- rows */
+/* Per-thread strided partials of one row (OPWORKS_BLOCK_LOOP with 256 threads). */
+#define ROW_THREADS REF_THREADS
+
+/* softmax_rows_kernel (include/ops/softmax.cuh:10-29). */
+static void softmax_row(const float *x, float *y, int cols) {
+    float part[ROW_THREADS];
+    for (int t = 0; t < ROW_THREADS; ++t) {
+        float m = -INFINITY;
+        for (int j = t; j < cols; j += ROW_THREADS)
+            m = fmaxf(m, x[j]);
+        part[t] = m;
+    }
+    const float mx = orc_block_reduce(part, ROW_THREADS, 1);
+    for (int t = 0; t < ROW_THREADS; ++t) {
+        float s = 0.f;
+        for (int j = t; j < cols; j += ROW_THREADS)
+            s += expf(x[j] - mx);
+        part[t] = s;
+    }
+    const float sum = orc_block_reduce(part, ROW_THREADS, 0);
+    for (int j = 0; j < cols; ++j)
+        y[j] = expf(x[j] - mx) / sum;
+}
+
+/* layer_norm_kernel (include/ops/layer_norm.cuh:10-31); `d*d` accumulation and
+ * the final `(x-mean)*rstd*gamma + beta` are FMA-contracted by nvcc. rsqrtf is
+ * restated as 1/sqrtf (CUDA's rsqrtf is not reproduced). */
+static void layer_norm_row(const float *x, float *y, const float *g, const float *b, int cols, float eps) {
+    float part[ROW_THREADS];
+    for (int t = 0; t < ROW_THREADS; ++t) {
+        float s = 0.f;
+        for (int j = t; j < cols; j += ROW_THREADS)
+            s += x[j];
+        part[t] = s;
+    }
+    const float mean = orc_block_reduce(part, ROW_THREADS, 0) / cols;
+    for (int t = 0; t < ROW_THREADS; ++t) {
+        float s = 0.f;
+        for (int j = t; j < cols; j += ROW_THREADS) {
+            const float d = x[j] - mean;
+            s = fmaf(d, d, s);
+        }
+        part[t] = s;
+    }
+    const float rstd = 1.0f / sqrtf(orc_block_reduce(part, ROW_THREADS, 0) / cols + eps);
+    for (int j = 0; j < cols; ++j)
+        y[j] = fmaf((x[j] - mean) * rstd, g[j], b[j]);
+}
+
+/* rms_norm_kernel (include/ops/rms_norm.cuh:9-24); `v*v` accumulation is an FMA. */
+static void rms_norm_row(const float *x, const float *w, float *y, int cols, float eps) {
+    float part[ROW_THREADS];
+    for (int t = 0; t < ROW_THREADS; ++t) {
+        float s = 0.f;
+        for (int j = t; j < cols; j += ROW_THREADS)
+            s = fmaf(x[j], x[j], s);
+        part[t] = s;
+    }
+    const float inv = 1.0f / sqrtf(orc_block_reduce(part, ROW_THREADS, 0) / cols + eps);
+    for (int j = 0; j < cols; ++j)
+        y[j] = x[j] * inv * w[j];
+}
+
+struct row_ctx {
+    const float *in, *p0, *p1;
+    float *out;
+    int cols;
+    float eps;
+    int kind;
+};
+static void rows_range(void *p, int64_t lo, int64_t hi) {
+    struct row_ctx *c = (struct row_ctx *)p;
+    for (int64_t r = lo; r < hi; ++r) {
+        const float *x = c->in + r * c->cols;
+        float *y = c->out + r * c->cols;
+        if (c->kind == 0)
+            softmax_row(x, y, c->cols);
+        else if (c->kind == 1)
+            layer_norm_row(x, y, c->p0, c->p1, c->cols, c->eps);
+        else
+            rms_norm_row(x, c->p0, y, c->cols, c->eps);
+    }
+}
+
+void orc_softmax_rows(const float *in, float *out, int rows, int cols) {
+    struct row_ctx c = {in, NULL, NULL, out, cols, 0.f, 0};
+    parallel_for(rows, rows_range, &c);
+}
+void orc_layer_norm_rows(const float *in, float *out, const float *gamma, const float *beta, int rows, int cols,
+                         float eps) {
+    struct row_ctx c = {in, gamma, beta, out, cols, eps, 1};
+    parallel_for(rows, rows_range, &c);
+}
+void orc_rms_norm_rows(const float *x, const float *w, float *out, int rows, int cols, float eps) {
+    struct row_ctx c = {x, w, NULL, out, cols, eps, 2};
+    parallel_for(rows, rows_range, &c);
+}

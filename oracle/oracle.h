@@ -1,0 +1,68 @@
+/* OpWorks CPU oracle — TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference's algorithms for the operator hot
+ * path (Xavier-86/OpWorks, include/ops/ *.cuh and include/core/block_reduce.cuh),
+ * in the reference's own evaluation order where that order is fixed by the
+ * code. It is the checker for the HIP kernels: only tests/, the smoke() entry
+ * point and bench.py's cpu_baseline leg may load it, and the product path
+ * never calls it.
+ *
+ * Floating-point contraction: the reference is compiled by nvcc with
+ * -fmad=true, which fuses a*b+c into an FMA. This file is compiled with
+ * -ffp-contract=off and writes fmaf() exactly where that fusion is
+ * unambiguous (noted per function); elsewhere results are compared within
+ * the tolerances the tests state.
+ *
+ * Pinning (what checks each function; details in tests/test_oracle.py):
+ *  orc_fill_*            bit-equality with the GPU generator + moments
+ *  orc_map_scale_add     fmaf closed form; framework.cu KATs (Add, Scale)
+ *  orc_reduce            brute-force double sum; framework.cu KATs (ones, empty
+ *                        product); exact tree reproduced by hand on tiny inputs
+ *  orc_softmax_rows      framework.cu:189-195 closed form; sum-to-one, shift
+ *                        invariance
+ *  orc_layer_norm_rows   framework.cu:196-199 closed form; zero mean / unit var
+ *  orc_rms_norm_rows     closed form mean(out^2)=ms/(ms+eps) at gamma=1
+ */
+#ifndef OPWORKS_ORACLE_H
+#define OPWORKS_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* worker threads used by the *_mt entry points (default 1) */
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
+/* seeded synthetic data, restating opworks_amd/include/core/random.hpp */
+uint64_t orc_stream_key(uint64_t seed, uint64_t stream);
+void orc_fill_uniform(float *dst, int64_t n, uint64_t seed, uint64_t stream, float lo, float hi);
+void orc_fill_normal(float *dst, int64_t n, uint64_t seed, uint64_t stream, float mean, float sd);
+void orc_fill_uniform_mt(float *dst, int64_t n, uint64_t seed, uint64_t stream, float lo, float hi);
+void orc_fill_normal_mt(float *dst, int64_t n, uint64_t seed, uint64_t stream, float mean, float sd);
+
+/* map */
+void orc_map_scale_add(const float *a, const float *b, float *out, int64_t n, float alpha);
+void orc_map_scale_add_mt(const float *a, const float *b, float *out, int64_t n, float alpha);
+
+/* block_reduce<Op> of `nthreads` per-thread values (thread 0's result). op: 0 sum, 1 max, 2 product */
+float orc_block_reduce(const float *vals, int nthreads, int op);
+/* ops::reduce<Op> in the reference's launch geometry and order */
+float orc_reduce(const float *in, int n, int op);
+double orc_sum_f64(const float *in, int64_t n);
+double orc_sum_abs_f64(const float *in, int64_t n);
+
+/* row kernels, one reference "block" of 256 threads per row */
+void orc_softmax_rows(const float *in, float *out, int rows, int cols);
+void orc_layer_norm_rows(const float *in, float *out, const float *gamma, const float *beta, int rows, int cols,
+                         float eps);
+void orc_rms_norm_rows(const float *x, const float *w, float *out, int rows, int cols, float eps);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,136 @@
+"""ctypes binding of oracle/liboracle.so — the CPU checker (test infrastructure).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module; the product path never does.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_double, c_float, c_int, c_int64, c_uint64, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+LIB_PATH = ROOT / "oracle" / "liboracle.so"
+
+_lib = None
+_F = POINTER(c_float)
+
+_SIGS = {
+    "orc_set_threads": (None, [c_int]),
+    "orc_get_threads": (c_int, []),
+    "orc_stream_key": (c_uint64, [c_uint64, c_uint64]),
+    "orc_fill_uniform": (None, [_F, c_int64, c_uint64, c_uint64, c_float, c_float]),
+    "orc_fill_normal": (None, [_F, c_int64, c_uint64, c_uint64, c_float, c_float]),
+    "orc_fill_uniform_mt": (None, [_F, c_int64, c_uint64, c_uint64, c_float, c_float]),
+    "orc_fill_normal_mt": (None, [_F, c_int64, c_uint64, c_uint64, c_float, c_float]),
+    "orc_map_scale_add": (None, [_F, _F, _F, c_int64, c_float]),
+    "orc_map_scale_add_mt": (None, [_F, _F, _F, c_int64, c_float]),
+    "orc_block_reduce": (c_float, [_F, c_int, c_int]),
+    "orc_reduce": (c_float, [_F, c_int, c_int]),
+    "orc_sum_f64": (c_double, [_F, c_int64]),
+    "orc_sum_abs_f64": (c_double, [_F, c_int64]),
+    "orc_softmax_rows": (None, [_F, _F, c_int, c_int]),
+    "orc_layer_norm_rows": (None, [_F, _F, _F, _F, c_int, c_int, c_float]),
+    "orc_rms_norm_rows": (None, [_F, _F, _F, c_int, c_int, c_float]),
+}
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m opworks_amd.build oracle`")
+        h = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(h, name, None)
+            if fn is None:
+                continue
+            fn.restype = res
+            fn.argtypes = args
+        _lib = h
+    return _lib
+
+
+def declare(name, restype, argtypes):
+    _SIGS[name] = (restype, argtypes)
+    if _lib is not None:
+        fn = getattr(_lib, name)
+        fn.restype, fn.argtypes = restype, argtypes
+
+
+def fp(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
+    return a.ctypes.data_as(_F)
+
+
+def f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(n)
+
+
+def fill_uniform(n: int, seed: int, stream: int, lo: float, hi: float, mt: bool = False) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    (lib().orc_fill_uniform_mt if mt else lib().orc_fill_uniform)(fp(out), n, seed, stream, lo, hi)
+    return out
+
+
+def fill_normal(n: int, seed: int, stream: int, mean: float, sd: float, mt: bool = False) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    (lib().orc_fill_normal_mt if mt else lib().orc_fill_normal)(fp(out), n, seed, stream, mean, sd)
+    return out
+
+
+def map_scale_add(a, b, alpha: float, mt: bool = False) -> np.ndarray:
+    a, b = f32(a), f32(b)
+    out = np.empty_like(a)
+    (lib().orc_map_scale_add_mt if mt else lib().orc_map_scale_add)(fp(a), fp(b), fp(out), a.size, alpha)
+    return out
+
+
+REDUCE_OPS = {"sum": 0, "max": 1, "product": 2}
+
+
+def block_reduce(vals, op: str = "sum") -> float:
+    v = f32(vals)
+    return lib().orc_block_reduce(fp(v), v.size, REDUCE_OPS[op])
+
+
+def reduce(x, op: str = "sum") -> float:
+    x = f32(x)
+    return lib().orc_reduce(fp(x), x.size, REDUCE_OPS[op])
+
+
+def sum_f64(x) -> float:
+    x = f32(x)
+    return lib().orc_sum_f64(fp(x), x.size)
+
+
+def sum_abs_f64(x) -> float:
+    x = f32(x)
+    return lib().orc_sum_abs_f64(fp(x), x.size)
+
+
+def softmax_rows(x, rows: int, cols: int) -> np.ndarray:
+    x = f32(x)
+    out = np.empty(rows * cols, np.float32)
+    lib().orc_softmax_rows(fp(x), fp(out), rows, cols)
+    return out
+
+
+def layer_norm_rows(x, gamma, beta, rows: int, cols: int, eps: float) -> np.ndarray:
+    x, g, b = f32(x), f32(gamma), f32(beta)
+    out = np.empty(rows * cols, np.float32)
+    lib().orc_layer_norm_rows(fp(x), fp(out), fp(g), fp(b), rows, cols, eps)
+    return out
+
+
+def rms_norm_rows(x, w, rows: int, cols: int, eps: float) -> np.ndarray:
+    x, w = f32(x), f32(w)
+    out = np.empty(rows * cols, np.float32)
+    lib().orc_rms_norm_rows(fp(x), fp(w), fp(out), rows, cols, eps)
+    return out

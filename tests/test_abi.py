@@ -1,0 +1,87 @@
+"""The C-ABI libraries load and export every symbol include/*.h declares, and
+contract violations come back as errors before any device work (no GPU)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+DECL = re.compile(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(opw_\w+|solve)\s*\(", re.M)
+
+
+def declared(header: Path):
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+    return sorted(set(DECL.findall(text)))
+
+
+def test_headers_declare_symbols():
+    assert HEADERS, "no C headers under include/"
+    for h in HEADERS:
+        assert declared(h), h
+
+
+def test_main_library_exports_every_declared_symbol(ow):
+    lib = ow.lib()
+    missing = []
+    for h in HEADERS:
+        if h.name.startswith("opworks_solve"):
+            continue
+        for name in declared(h):
+            if not hasattr(lib, name):
+                missing.append(f"{h.name}:{name}")
+    assert not missing, missing
+
+
+def test_adapters_export_solve():
+    adapters = sorted((ROOT / "opworks_amd" / "lib" / "adapters").glob("libopw_solve_*.so"))
+    hdr = ROOT / "include" / "opworks_solve.h"
+    if not hdr.exists():
+        pytest.skip("no adapters declared yet")
+    names = re.findall(r"libopw_solve_(\w+)\.so", hdr.read_text())
+    assert names
+    built = {p.name for p in adapters}
+    for n in names:
+        assert f"libopw_solve_{n}.so" in built, n
+        assert hasattr(ctypes.CDLL(str(ROOT / "opworks_amd" / "lib" / "adapters" / f"libopw_solve_{n}.so")), "solve")
+
+
+# Contract checks mirror tests/unit/framework.cu:91-106; none reaches the device.
+def test_contracts_reject_before_launch(ow):
+    E = ow.OpworksError
+    ops = ow.ops
+    ops.map_scale_add(None, None, None, 0, 2.5)  # n == 0 is a no-op
+    ops.softmax(None, None, 0, 3)
+    ops.layer_norm(None, None, None, None, 0, 3)
+    with pytest.raises(E, match="nonnegative"):
+        ops.map_scale(None, None, -1, 2.0)
+    with pytest.raises(E, match="non-null"):
+        ops.map_scale(None, None, 1, 2.0)
+    with pytest.raises(E, match="valid input/output"):
+        ops.reduce(None, None, 0)
+    with pytest.raises(E, match="positive columns"):
+        ops.softmax(None, None, 1, 0)
+    with pytest.raises(E, match="nonnegative"):
+        ops.softmax(None, None, -1, 2)
+    with pytest.raises(E, match="positive columns"):
+        ops.layer_norm(None, None, None, None, 1, 0)
+    with pytest.raises(E, match="epsilon"):
+        ops.layer_norm(None, None, None, None, 0, 3, 0.0)
+    with pytest.raises(E, match="epsilon"):
+        ops.layer_norm(None, None, None, None, 0, 3, float("inf"))
+    with pytest.raises(E, match="INT_MAX"):
+        ops.softmax(None, None, 65536, 65536)
+    with pytest.raises(E, match="epsilon"):
+        ops.rms_norm(1, 1, 1, 1, 4, 0.0)
+    with pytest.raises(E, match="unknown reduction"):
+        ow.check(ow.lib().opw_reduce_f32(1, 1, 0, 9, None, 0, None))
+    with pytest.raises(E, match="workspace is too small"):
+        ow.check(ow.lib().opw_reduce_f32(1, 1, 1 << 20, 0, 1, 0, None))
+
+
+def test_workspace_sizes(ow):
+    assert ow.ops.reduction_workspace_size(0) == 0
+    assert ow.ops.reduction_workspace_size(4096) == 0
+    assert ow.ops.reduction_workspace_size(4097) == 2
+    assert ow.ops.reduction_workspace_size(1 << 28) == 1024
