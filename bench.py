@@ -130,7 +130,24 @@ def wl_rmsnorm(stream, steps, warmup):
             "kernel": "rms_norm_reg_kernel<1,8>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
 
 
-WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm}
+def wl_gemm(stream, steps, warmup):
+    """Config 3: C = relu(A @ B + bias), M = N = K = 4096 fp32, A, B ~ N(0, 1/64); 2*4096^3 flop."""
+    n = 4096
+    A, B, C = (ow.DeviceBuffer.empty(n * n) for _ in range(3))
+    bias = ow.DeviceBuffer.empty(n)
+    ow.fill_normal(A, SEED, 300, 0.0, 1.0 / 64, stream=stream)
+    ow.fill_normal(B, SEED, 301, 0.0, 1.0 / 64, stream=stream)
+    ow.fill_uniform(bias, SEED, 302, -0.1, 0.1, stream=stream)
+    lib = ow.lib()
+    ms = Timer(stream).run(lambda i: ow.check(lib.opw_mat_mul_fused_f32(A.ptr, B.ptr, bias.ptr, C.ptr, n, n, n, 0, 1,
+                                                                         stream)), steps, warmup)
+    flop = 2.0 * n ** 3
+    tf = flop / ms / 1e9
+    return {"workload": "gemm_f32_relu_bias_4096^3", "unit": "TFLOP/s", "value": tf, "ms": ms, "flop": flop,
+            "kernel": "gemm_f32_mfma_kernel<kn>", "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma")}
+
+
+WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "gemm": wl_gemm}
 HEADLINE = "map"
 
 

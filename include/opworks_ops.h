@@ -32,6 +32,7 @@ int opw_set_device(int device);
 int opw_device_name(char *out, int out_len);
 int opw_device_cu_count(int *cus);
 int opw_malloc(void **ptr, size_t bytes);
+/* Waits for the device, then frees (blocking like the reference DeviceBuffer destructor). */
 int opw_free(void *ptr);
 /* Blocking copies on `stream` (DeviceBuffer::from_host / to_host semantics). */
 int opw_memcpy_htod(void *dst, const void *src, size_t bytes, void *stream);
@@ -77,6 +78,20 @@ int opw_softmax_f32(const float *in, float *out, int rows, int cols, void *strea
 int opw_layer_norm_f32(const float *in, float *out, const float *gamma, const float *beta, int rows, int cols,
                        float eps, void *stream);
 int opw_rms_norm_f32(const float *x, const float *weight, float *out, int rows, int cols, float eps, void *stream);
+
+/* ---- GEMM (reference: ops::mat_mul, include/ops/matmul.cuh:77-91; names as in
+ * the reference: A is M x N, B is N x K, C is M x K, reduction over N) ---- */
+/* C = A @ B  (PassThrough epilogue). M == 0 or K == 0: no-op; N == 0 writes zeros. */
+int opw_mat_mul_f32(const float *A, const float *B, float *C, int M, int N, int K, void *stream);
+/* C = act(A @ op(B) + bias[K]); op(B) = B (N x K) or, when b_transposed, B^T with B stored K x N;
+ * bias may be NULL; activation 0 none, 1 relu, 2 gelu (erf form). This is what
+ * MatmulBuilder(...).transpose_b().bias().activation() configures (include/builders/matmul.cuh:7-57),
+ * executed as one fused kernel. */
+int opw_mat_mul_fused_f32(const float *A, const float *B, const float *bias, float *C, int M, int N, int K,
+                          int b_transposed, int activation, void *stream);
+/* Y[rows][out] = X[rows][in] @ W[out][in]^T (reference: ops::linear, include/ops/linear.cuh:130-153) */
+int opw_linear_f32(const float *X, const float *W, float *Y, int rows, int in_features, int out_features,
+                   void *stream);
 
 #ifdef __cplusplus
 }

@@ -66,6 +66,10 @@ _SIGNATURES = {
     "opw_softmax_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "opw_layer_norm_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),
     "opw_rms_norm_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),
+    "opw_mat_mul_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "opw_mat_mul_fused_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                      c_void_p]),
+    "opw_linear_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
 }
 
 
@@ -213,7 +217,12 @@ class DeviceView:
 
 
 class DeviceBuffer(DeviceView):
-    """Owning device allocation (the reference's DeviceBuffer / TypedDeviceBuffer)."""
+    """Owning device allocation (the reference's DeviceBuffer / TypedDeviceBuffer).
+
+    Freeing waits for the device (as the reference's cudaFree-based destructor
+    does), but a buffer must still be alive when work that uses it is
+    enqueued: keep a reference, do not pass `DeviceBuffer(...).ptr` of a
+    temporary to an entry point."""
 
     def __init__(self, n: int, dtype=np.float32) -> None:
         if n < 0:
@@ -303,6 +312,20 @@ class _Ops:
 
     def rms_norm(self, x: Ptr, weight: Ptr, out: Ptr, rows: int, cols: int, eps: float, stream=None) -> None:
         check(lib().opw_rms_norm_f32(_p(x), _p(weight), _p(out), rows, cols, eps, _stream(stream)))
+
+    ACTIVATIONS = {"none": 0, "relu": 1, "gelu": 2}
+
+    # Reference names: A is M x N, B is N x K (K x N when b_transposed), C is M x K.
+    def mat_mul(self, A: Ptr, B: Ptr, C: Ptr, M: int, N: int, K: int, stream=None) -> None:
+        check(lib().opw_mat_mul_f32(_p(A), _p(B), _p(C), M, N, K, _stream(stream)))
+
+    def mat_mul_fused(self, A: Ptr, B: Ptr, bias: Ptr, C: Ptr, M: int, N: int, K: int, b_transposed: bool = False,
+                      activation: str = "none", stream=None) -> None:
+        check(lib().opw_mat_mul_fused_f32(_p(A), _p(B), _p(bias), _p(C), M, N, K, int(b_transposed),
+                                          self.ACTIVATIONS[activation], _stream(stream)))
+
+    def linear(self, X: Ptr, W: Ptr, Y: Ptr, rows: int, in_features: int, out_features: int, stream=None) -> None:
+        check(lib().opw_linear_f32(_p(X), _p(W), _p(Y), rows, in_features, out_features, _stream(stream)))
 
 
 ops = _Ops()

@@ -118,8 +118,11 @@ int opw_malloc(void **ptr, size_t bytes) {
 
 int opw_free(void *ptr) {
     return guard([&] {
-        if (ptr)
+        if (ptr) {
+            // Blocking, like the reference DeviceBuffer's cudaFree: queued work may still read ptr.
+            OPWORKS_HIP_CHECK(hipDeviceSynchronize());
             OPWORKS_HIP_CHECK(hipFree(ptr));
+        }
         return 0;
     });
 }

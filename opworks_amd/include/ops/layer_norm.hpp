@@ -22,7 +22,7 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void layer_norm_reg_kernel(
     for (int k = 0; k < kV; ++k) {
         const int q = pack_index<kW>(p, k);
         if (p.active && q < n4) {
-            x[k] = src[q];
+            x[k] = __builtin_nontemporal_load(src + q);
             local += (x[k][0] + x[k][1]) + (x[k][2] + x[k][3]);
         }
     }

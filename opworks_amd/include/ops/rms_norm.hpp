@@ -21,7 +21,7 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void rms_norm_reg_kernel(cons
     for (int k = 0; k < kV; ++k) {
         const int q = pack_index<kW>(p, k);
         if (p.active && q < n4) {
-            v[k] = src[q];
+            v[k] = __builtin_nontemporal_load(src + q);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 local = fmaf(v[k][j], v[k][j], local);

@@ -309,3 +309,110 @@ void orc_rms_norm_rows(const float *x, const float *w, float *out, int rows, int
     struct row_ctx c = {x, w, NULL, out, cols, eps, 2};
     parallel_for(rows, rows_range, &c);
 }
+
+/* --------------------------------------------------------------------- gemm */
+struct mm_ctx {
+    const float *A, *B, *bias;
+    float *out;
+    double *absdot;
+    int M, N, K, act;
+    const int *rows;
+};
+
+static float apply_act(float v, int act) {
+    if (act == 1)
+        return fmaxf(v, 0.f);
+    if (act == 2)
+        return 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+    return v;
+}
+
+static void mm_range(void *p, int64_t lo, int64_t hi) {
+    struct mm_ctx *c = (struct mm_ctx *)p;
+    float *acc = (float *)malloc(sizeof(float) * (size_t)c->K);
+    double *ab = (double *)malloc(sizeof(double) * (size_t)c->K);
+    for (int64_t r = lo; r < hi; ++r) {
+        const int i = c->rows ? c->rows[r] : (int)r;
+        for (int j = 0; j < c->K; ++j) {
+            acc[j] = 0.f;
+            ab[j] = 0.0;
+        }
+        const float *arow = c->A + (int64_t)i * c->N;
+        for (int n = 0; n < c->N; ++n) {
+            const float a = arow[n];
+            const float *brow = c->B + (int64_t)n * c->K;
+            for (int j = 0; j < c->K; ++j) {
+                acc[j] = fmaf(a, brow[j], acc[j]);
+                ab[j] += fabs((double)a * (double)brow[j]);
+            }
+        }
+        for (int j = 0; j < c->K; ++j) {
+            const float v = c->bias ? acc[j] + c->bias[j] : acc[j];
+            c->out[r * c->K + j] = apply_act(v, c->act);
+            if (c->absdot)
+                c->absdot[r * c->K + j] = ab[j] + (c->bias ? fabs((double)c->bias[j]) : 0.0);
+        }
+    }
+    free(acc);
+    free(ab);
+}
+
+/* ops::mat_mul (include/ops/matmul.cuh:11-66) in reference names: A is M x N,
+ * B is N x K (or, with b_transposed, stored K x N), out rows are `rows[0..nrows)`
+ * (all M rows when rows == NULL). Each output is the k-ascending chain
+ * acc = fmaf(a, b, acc) over n = 0..N-1 (nvcc contracts `acc += a*b`), then
+ * v = acc + bias[j] and the activation (0 none, 1 relu, 2 gelu-erf) — the
+ * reference's PassThrough result followed by the host-side bias/ReLU that
+ * MatmulBuilder describes. absdot (optional) receives sum_n |a*b| + |bias|. */
+void orc_mat_mul_rows(const float *A, const float *B, const float *bias, float *out, double *absdot, int M, int N,
+                      int K, const int *rows, int nrows, int b_transposed, int act) {
+    float *bt = NULL;
+    if (b_transposed) {
+        bt = (float *)malloc(sizeof(float) * (size_t)N * (size_t)K);
+        for (int n = 0; n < N; ++n)
+            for (int j = 0; j < K; ++j)
+                bt[(int64_t)n * K + j] = B[(int64_t)j * N + n];
+    }
+    struct mm_ctx c = {A, bt ? bt : B, bias, out, absdot, M, N, K, act, rows};
+    parallel_for(rows ? nrows : M, mm_range, &c);
+    free(bt);
+}
+
+/* gemv_kernel (include/ops/linear.cuh:77-96): y[o] = block_reduce over 256
+ * threads of per-thread partials; with in % 4 == 0 thread t accumulates
+ * local += w.x*x.x + w.y*x.y + w.z*x.z + w.w*x.w over packs t, t+256, ...
+ * The four products are restated as the FMA chain
+ * fmaf(w.w,x.w, fmaf(w.z,x.z, fmaf(w.y,x.y, w.x*x.x))) followed by a plain add
+ * into `local` (one admissible nvcc contraction; results are compared within
+ * tolerance). Otherwise local = fmaf(x[i], w[i], local). */
+struct gemv_ctx {
+    const float *x, *W;
+    float *y;
+    int in;
+};
+static void gemv_range(void *p, int64_t lo, int64_t hi) {
+    struct gemv_ctx *c = (struct gemv_ctx *)p;
+    float part[REF_THREADS];
+    for (int64_t o = lo; o < hi; ++o) {
+        const float *w = c->W + o * c->in;
+        for (int t = 0; t < REF_THREADS; ++t) {
+            float local = 0.f;
+            if (c->in % 4 == 0) {
+                for (int i4 = t; i4 < c->in / 4; i4 += REF_THREADS) {
+                    const float *wv = w + 4 * i4, *xv = c->x + 4 * i4;
+                    const float dot = fmaf(wv[3], xv[3], fmaf(wv[2], xv[2], fmaf(wv[1], xv[1], wv[0] * xv[0])));
+                    local = local + dot;
+                }
+            } else {
+                for (int i = t; i < c->in; i += REF_THREADS)
+                    local = fmaf(c->x[i], w[i], local);
+            }
+            part[t] = local;
+        }
+        c->y[o] = orc_block_reduce(part, REF_THREADS, 0);
+    }
+}
+void orc_gemv(const float *x, const float *W, float *y, int in, int out) {
+    struct gemv_ctx c = {x, W, y, in};
+    parallel_for(out, gemv_range, &c);
+}

@@ -22,6 +22,9 @@
  *                        invariance
  *  orc_layer_norm_rows   framework.cu:196-199 closed form; zero mean / unit var
  *  orc_rms_norm_rows     closed form mean(out^2)=ms/(ms+eps) at gamma=1
+ *  orc_mat_mul_rows      framework.cu:201-221 integer KAT (exact), zero-K case,
+ *                        float64 matmul bound, numpy reference on small shapes
+ *  orc_gemv              float64 dot bound; agrees with orc_mat_mul_rows
  */
 #ifndef OPWORKS_ORACLE_H
 #define OPWORKS_ORACLE_H
@@ -60,6 +63,12 @@ void orc_softmax_rows(const float *in, float *out, int rows, int cols);
 void orc_layer_norm_rows(const float *in, float *out, const float *gamma, const float *beta, int rows, int cols,
                          float eps);
 void orc_rms_norm_rows(const float *x, const float *w, float *out, int rows, int cols, float eps);
+
+/* GEMM in reference names (A: M x N, B: N x K or K x N when b_transposed); see oracle.c */
+void orc_mat_mul_rows(const float *A, const float *B, const float *bias, float *out, double *absdot, int M, int N,
+                      int K, const int *rows, int nrows, int b_transposed, int act);
+/* reference GEMV (rows == 1 path of ops::linear): y[out] = W[out][in] . x */
+void orc_gemv(const float *x, const float *W, float *y, int in, int out);
 
 #ifdef __cplusplus
 }

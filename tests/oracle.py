@@ -34,6 +34,9 @@ _SIGS = {
     "orc_softmax_rows": (None, [_F, _F, c_int, c_int]),
     "orc_layer_norm_rows": (None, [_F, _F, _F, _F, c_int, c_int, c_float]),
     "orc_rms_norm_rows": (None, [_F, _F, _F, c_int, c_int, c_float]),
+    "orc_mat_mul_rows": (None, [_F, _F, _F, _F, POINTER(c_double), c_int, c_int, c_int, POINTER(c_int), c_int,
+                                c_int, c_int]),
+    "orc_gemv": (None, [_F, _F, _F, c_int, c_int]),
 }
 
 
@@ -134,3 +137,30 @@ def rms_norm_rows(x, w, rows: int, cols: int, eps: float) -> np.ndarray:
     out = np.empty(rows * cols, np.float32)
     lib().orc_rms_norm_rows(fp(x), fp(w), fp(out), rows, cols, eps)
     return out
+
+
+ACTS = {"none": 0, "relu": 1, "gelu": 2}
+
+
+def mat_mul_rows(A, B, M, N, K, rows=None, bias=None, b_transposed=False, act="none"):
+    """Reference names: A is M x N, B is N x K (K x N when b_transposed).
+    Returns (out[len(rows) or M, K], absdot float64 of the same shape)."""
+    A, B = f32(A), f32(B)
+    nrows = M if rows is None else len(rows)
+    out = np.empty(nrows * K, np.float32)
+    absdot = np.empty(nrows * K, np.float64)
+    rp = None
+    if rows is not None:
+        rows = np.ascontiguousarray(rows, np.int32)
+        rp = rows.ctypes.data_as(POINTER(c_int))
+    bp = fp(f32(bias)) if bias is not None else None
+    lib().orc_mat_mul_rows(fp(A), fp(B), bp, fp(out), absdot.ctypes.data_as(POINTER(c_double)), M, N, K, rp,
+                           nrows, int(b_transposed), ACTS[act])
+    return out.reshape(nrows, K), absdot.reshape(nrows, K)
+
+
+def gemv(x, W, in_features, out_features):
+    x, W = f32(x), f32(W)
+    y = np.empty(out_features, np.float32)
+    lib().orc_gemv(fp(x), fp(W), fp(y), in_features, out_features)
+    return y

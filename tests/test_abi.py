@@ -82,6 +82,6 @@ def test_contracts_reject_before_launch(ow):
 
 def test_workspace_sizes(ow):
     assert ow.ops.reduction_workspace_size(0) == 0
-    assert ow.ops.reduction_workspace_size(4096) == 0
-    assert ow.ops.reduction_workspace_size(4097) == 2
-    assert ow.ops.reduction_workspace_size(1 << 28) == 1024
+    assert ow.ops.reduction_workspace_size(8192) == 0  # one chunk: single launch
+    assert ow.ops.reduction_workspace_size(8193) == 2
+    assert ow.ops.reduction_workspace_size(1 << 28) == (1 << 28) // 8192

@@ -1,0 +1,102 @@
+"""GPU parity of the fp32 MFMA GEMM (ops::mat_mul, the fused MatmulBuilder
+path, ops::linear incl. the rows == 1 GEMV) against the oracle's k-ascending
+fmaf chains. Bar (north_star): |gpu - ref| <= 1e-4 * (sum_k |a_ik b_kj| + |bias_j|)
+per element, i.e. relative 1e-4 K-scaled. Shapes use the reference's names:
+A is M x N, B is N x K, C is M x K."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+SEED = 1234
+KTOL = 1e-4
+
+
+def upload(ow, arr):
+    return ow.DeviceBuffer.from_host(np.ascontiguousarray(arr, np.float32))
+
+
+def check_kscaled(got, ref, absdot, tol=KTOL, floor=1e-6):
+    err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    bound = tol * absdot + floor
+    worst = float(np.max(err / bound)) if err.size else 0.0
+    assert worst <= 1.0, f"K-scaled error {worst:.3g} x bound"
+
+
+def test_integer_known_answer(ow):
+    # tests/unit/framework.cu:201-218 (3x5x7 integer inputs; exact in fp32)
+    a = np.array([i % 7 - 3 for i in range(15)], np.float32)
+    b = np.array([i % 5 - 2 for i in range(35)], np.float32)
+    c = ow.DeviceBuffer.empty(21)
+    da, db = upload(ow, a), upload(ow, b)  # keep the buffers alive across the launch
+    ow.ops.mat_mul(da, db, c, 3, 5, 7)
+    want = a.reshape(3, 5).astype(np.float64) @ b.reshape(5, 7).astype(np.float64)
+    assert np.array_equal(c.to_host().reshape(3, 7), want.astype(np.float32))
+    # zero reduction dim writes epilogue(0) (framework.cu:219-221)
+    c.copy_from_host(np.full(21, 7.0, np.float32))
+    ow.ops.mat_mul(None, None, c, 3, 0, 7)
+    assert np.all(c.to_host() == 0)
+
+
+SHAPES = [(1, 1, 1), (3, 5, 7), (64, 64, 64), (127, 33, 129), (128, 128, 128), (200, 300, 100), (257, 1000, 515),
+          (512, 2048, 384), (130, 4, 260)]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("b_t", [False, True])
+@pytest.mark.parametrize("act", ["none", "relu", "gelu"])
+def test_fused_matmul_matches_oracle(ow, orc, M, N, K, b_t, act):
+    A = orc.fill_normal(M * N, SEED, 1, 0.0, 1.0)
+    B = orc.fill_normal(N * K, SEED, 2, 0.0, 1.0)
+    bias = orc.fill_uniform(K, SEED, 3, -0.1, 0.1)
+    C = ow.DeviceBuffer.empty(M * K)
+    dA, dB, dbias = upload(ow, A), upload(ow, B), upload(ow, bias)
+    ow.ops.mat_mul_fused(dA, dB, dbias, C, M, N, K, b_transposed=b_t, activation=act)
+    ref, absdot = orc.mat_mul_rows(A, B, M, N, K, bias=bias, b_transposed=b_t, act=act)
+    check_kscaled(C.to_host().reshape(M, K), ref, absdot)
+
+
+@pytest.mark.parametrize("M,N,K", [(5, 7, 9), (129, 130, 131), (256, 512, 128)])
+def test_plain_matmul_and_misaligned(ow, orc, M, N, K):
+    A = orc.fill_normal(M * N + 1, SEED, 4, 0.0, 1.0)
+    B = orc.fill_normal(N * K + 1, SEED, 5, 0.0, 1.0)
+    dA, dB = upload(ow, A), upload(ow, B)
+    C = ow.DeviceBuffer.empty(M * K + 1)
+    # offset by one float: not 16-byte aligned, takes the guarded scalar-load kernel
+    ow.ops.mat_mul(dA.offset(1), dB.offset(1), C.offset(1), M, N, K)
+    ref, absdot = orc.mat_mul_rows(A[1:], B[1:], M, N, K)
+    check_kscaled(C.to_host()[1:].reshape(M, K), ref, absdot)
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", [(1, 2048, 2048), (1, 2048, 512), (1, 8192, 2048), (1, 100, 37),
+                                             (1, 64, 2049), (2, 64, 64), (7, 2048, 3072), (512, 2048, 2048)])
+def test_linear_matches_oracle(ow, orc, rows, in_f, out_f):
+    X = orc.fill_normal(rows * in_f, SEED, 6, 0.0, 1.0)
+    W = orc.fill_normal(out_f * in_f, SEED, 7, 0.0, 0.02)
+    Y = ow.DeviceBuffer.empty(rows * out_f)
+    dX, dW = upload(ow, X), upload(ow, W)
+    ow.ops.linear(dX, dW, Y, rows, in_f, out_f)
+    ref, absdot = orc.mat_mul_rows(X, W, rows, in_f, out_f, b_transposed=True)
+    got = Y.to_host().reshape(rows, out_f)
+    check_kscaled(got, ref, absdot)
+    if rows == 1:  # the reference's own GEMV order agrees too
+        check_kscaled(got[0], orc.gemv(X, W, in_f, out_f), absdot[0])
+
+
+@pytest.mark.slow
+def test_config3_full_size_sampled(ow, orc):
+    """Config 3: C = relu(A @ B + bias), M = N = K = 4096, A, B ~ N(0, 1/64), bias ~ U[-0.1, 0.1];
+    every 32nd row (128 rows x 4096 columns) checked against the oracle."""
+    M = N = K = 4096
+    orc.set_threads(16)
+    dA, dB, dbias, dC = (ow.DeviceBuffer.empty(s) for s in (M * N, N * K, K, M * K))
+    ow.fill_normal(dA, SEED, 300, 0.0, 1.0 / 64)
+    ow.fill_normal(dB, SEED, 301, 0.0, 1.0 / 64)
+    ow.fill_uniform(dbias, SEED, 302, -0.1, 0.1)
+    ow.ops.mat_mul_fused(dA, dB, dbias, dC, M, N, K, activation="relu")
+    A = orc.fill_normal(M * N, SEED, 300, 0.0, 1.0 / 64, mt=True)
+    B = orc.fill_normal(N * K, SEED, 301, 0.0, 1.0 / 64, mt=True)
+    bias = orc.fill_uniform(K, SEED, 302, -0.1, 0.1)
+    rows = np.arange(0, M, 32)
+    ref, absdot = orc.mat_mul_rows(A, B, M, N, K, rows=rows, bias=bias, act="relu")
+    got = dC.to_host().reshape(M, K)[rows]
+    check_kscaled(got, ref, absdot)

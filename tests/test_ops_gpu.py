@@ -88,7 +88,7 @@ def test_map_scale_add_full_size_bit_exact(ow, orc):
 
 
 # -------------------------------------------------------------------- reduce
-@pytest.mark.parametrize("n", [0, 1, 31, 32, 33, 255, 256, 257, 4099, 4097, 100_000, 1 << 20, (1 << 20) + 3])
+@pytest.mark.parametrize("n", [0, 1, 31, 32, 33, 255, 256, 257, 4097, 4099, 8191, 8192, 8193, 16385, 100_000, 1 << 20, (1 << 20) + 3])
 def test_reduce_sum_matches_oracle(ow, orc, n):
     x = orc.fill_normal(max(n, 1), SEED, 20 + n % 97, 0.0, 1.0)[:n]
     dx = upload(ow, x) if n else ow.DeviceBuffer.empty(0)
