@@ -147,7 +147,26 @@ def wl_gemm(stream, steps, warmup):
             "kernel": "gemm_f32_mfma_kernel<kn>", "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma")}
 
 
-WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "gemm": wl_gemm}
+def wl_gemm_bf16(stream, steps, warmup):
+    """Config 3 bf16 variant: relu(A @ W^T + bias), 4096^3, A and W bf16 (RNE-rounded), fp32 accumulate/output."""
+    n = 4096
+    Af, Wf = ow.DeviceBuffer.empty(n * n), ow.DeviceBuffer.empty(n * n)
+    ow.fill_normal(Af, SEED, 300, 0.0, 1.0 / 64, stream=stream)
+    ow.fill_normal(Wf, SEED, 301, 0.0, 1.0 / 64, stream=stream)
+    A, W = ow.DeviceBuffer.empty(n * n, np.uint16), ow.DeviceBuffer.empty(n * n, np.uint16)
+    ow.ops.convert_f32_to_bf16(Af, A, n * n, stream=stream)
+    ow.ops.convert_f32_to_bf16(Wf, W, n * n, stream=stream)
+    bias, C = ow.DeviceBuffer.empty(n), ow.DeviceBuffer.empty(n * n)
+    ow.fill_uniform(bias, SEED, 302, -0.1, 0.1, stream=stream)
+    ms = Timer(stream).run(lambda i: ow.ops.linear_bf16(A, W, bias, C, n, n, n, activation="relu", x_bf16=True,
+                                                        stream=stream), steps, warmup)
+    flop = 2.0 * n ** 3
+    tf = flop / ms / 1e9
+    return {"workload": "gemm_bf16_relu_bias_4096^3", "unit": "TFLOP/s", "value": tf, "ms": ms, "flop": flop,
+            "kernel": "gemm_bf16_mfma_kernel<bf16>", "roofline": roofline(tf, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma")}
+
+
+WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "gemm": wl_gemm, "gemm_bf16": wl_gemm_bf16}
 HEADLINE = "map"
 
 

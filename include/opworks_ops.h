@@ -93,6 +93,17 @@ int opw_mat_mul_fused_f32(const float *A, const float *B, const float *bias, flo
 int opw_linear_f32(const float *X, const float *W, float *Y, int rows, int in_features, int out_features,
                    void *stream);
 
+/* ---- bf16 matrix-core path (reference: ops::linear_mma_bf16, include/ops/linear_mma.cuh:99-115) ----
+ * Y[rows][out] = act(bf16(X)[rows][in] @ W[out][in]^T + bias), fp32 accumulation; W holds bf16 bit
+ * patterns. X is fp32 (rounded to bf16, nearest-even, on load — the reference contract) ... */
+int opw_linear_bf16(const float *X, const uint16_t *W, const float *bias, float *Y, int rows, int in_features,
+                    int out_features, int activation, void *stream);
+/* ... or already bf16. */
+int opw_linear_bf16_bf16(const uint16_t *X, const uint16_t *W, const float *bias, float *Y, int rows,
+                         int in_features, int out_features, int activation, void *stream);
+/* dst[i] = bf16 bits of src[i], round to nearest even (tests/model/ops_test.cu:77-82 recipe) */
+int opw_convert_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

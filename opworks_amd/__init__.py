@@ -70,6 +70,9 @@ _SIGNATURES = {
     "opw_mat_mul_fused_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                       c_void_p]),
     "opw_linear_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "opw_linear_bf16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
+    "opw_linear_bf16_bf16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
+    "opw_convert_f32_to_bf16": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
 }
 
 
@@ -326,6 +329,15 @@ class _Ops:
 
     def linear(self, X: Ptr, W: Ptr, Y: Ptr, rows: int, in_features: int, out_features: int, stream=None) -> None:
         check(lib().opw_linear_f32(_p(X), _p(W), _p(Y), rows, in_features, out_features, _stream(stream)))
+
+    def linear_bf16(self, X: Ptr, W: Ptr, bias: Ptr, Y: Ptr, rows: int, in_features: int, out_features: int,
+                    activation: str = "none", x_bf16: bool = False, stream=None) -> None:
+        fn = lib().opw_linear_bf16_bf16 if x_bf16 else lib().opw_linear_bf16
+        check(fn(_p(X), _p(W), _p(bias), _p(Y), rows, in_features, out_features, self.ACTIVATIONS[activation],
+                 _stream(stream)))
+
+    def convert_f32_to_bf16(self, src: Ptr, dst: Ptr, n: int, stream=None) -> None:
+        check(lib().opw_convert_f32_to_bf16(_p(src), _p(dst), n, _stream(stream)))
 
 
 ops = _Ops()

@@ -416,3 +416,21 @@ void orc_gemv(const float *x, const float *W, float *y, int in, int out) {
     struct gemv_ctx c = {x, W, y, in};
     parallel_for(out, gemv_range, &c);
 }
+
+/* ---------------------------------------------------------------------- bf16 */
+/* Round-to-nearest-even fp32 -> bf16 bits (tests/model/ops_test.cu:77-82
+ * f2bf16_bits) and back: out[i] = float(bf16(in[i])). */
+void orc_round_bf16(const float *in, float *out, uint16_t *bits, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        uint32_t u;
+        memcpy(&u, &in[i], 4);
+        u += 0x7FFFu + ((u >> 16) & 1u);
+        const uint16_t b = (uint16_t)(u >> 16);
+        if (bits)
+            bits[i] = b;
+        if (out) {
+            const uint32_t f = (uint32_t)b << 16;
+            memcpy(&out[i], &f, 4);
+        }
+    }
+}

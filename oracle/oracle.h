@@ -25,6 +25,7 @@
  *  orc_mat_mul_rows      framework.cu:201-221 integer KAT (exact), zero-K case,
  *                        float64 matmul bound, numpy reference on small shapes
  *  orc_gemv              float64 dot bound; agrees with orc_mat_mul_rows
+ *  orc_round_bf16        hand-computed bit patterns incl. ties to even
  */
 #ifndef OPWORKS_ORACLE_H
 #define OPWORKS_ORACLE_H
@@ -69,6 +70,9 @@ void orc_mat_mul_rows(const float *A, const float *B, const float *bias, float *
                       int K, const int *rows, int nrows, int b_transposed, int act);
 /* reference GEMV (rows == 1 path of ops::linear): y[out] = W[out][in] . x */
 void orc_gemv(const float *x, const float *W, float *y, int in, int out);
+
+/* fp32 -> bf16 round-to-nearest-even (bits and/or the rounded float) */
+void orc_round_bf16(const float *in, float *out, uint16_t *bits, int64_t n);
 
 #ifdef __cplusplus
 }

@@ -37,6 +37,7 @@ _SIGS = {
     "orc_mat_mul_rows": (None, [_F, _F, _F, _F, POINTER(c_double), c_int, c_int, c_int, POINTER(c_int), c_int,
                                 c_int, c_int]),
     "orc_gemv": (None, [_F, _F, _F, c_int, c_int]),
+    "orc_round_bf16": (None, [_F, _F, c_void_p, c_int64]),
 }
 
 
@@ -164,3 +165,12 @@ def gemv(x, W, in_features, out_features):
     y = np.empty(out_features, np.float32)
     lib().orc_gemv(fp(x), fp(W), fp(y), in_features, out_features)
     return y
+
+
+def round_bf16(x):
+    """Returns (rounded float32 array, uint16 bf16 bits)."""
+    x = f32(x)
+    out = np.empty_like(x)
+    bits = np.empty(x.size, np.uint16)
+    lib().orc_round_bf16(fp(x), fp(out), bits.ctypes.data, x.size)
+    return out, bits

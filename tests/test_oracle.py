@@ -184,3 +184,34 @@ def test_rms_norm_closed_form(orc):
     w = np.linspace(0.5, 1.5, 8).astype(np.float32)
     y = orc.rms_norm_rows(np.full(8, 0.25, np.float32), w, 1, 8, eps)
     assert framework_close(y, 0.25 / math.sqrt(0.0625 + eps) * w.astype(np.float64))
+
+
+def test_round_bf16_known_bits(orc):
+    # hand-computed: 1.0 -> 0x3F80; 1 + 2^-8 is a tie between 0x3F80 and 0x3F81 -> even 0x3F80;
+    # 1 + 3*2^-8 ties between 0x3F81 and 0x3F82 -> even 0x3F82; 1 + 2^-8 + 2^-20 rounds up -> 0x3F81
+    x = np.array([1.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8, 1 + 2 ** -8 + 2 ** -20, -2.0, 0.0, 3.0e38], np.float32)
+    r, b = orc.round_bf16(x)
+    assert list(b[:6]) == [0x3F80, 0x3F80, 0x3F82, 0x3F81, 0xC000, 0x0000]
+    assert np.array_equal(r.view(np.uint32), b.astype(np.uint32) << 16)
+    # 8 significant bits: relative rounding error at most 2^-8, and it is attained closely
+    z = orc.fill_normal(10000, 8, 0, 0.0, 1.0)
+    rz, _ = orc.round_bf16(z)
+    rel = np.abs(rz - z) / np.abs(z)
+    assert rel.max() <= 2 ** -8 and rel.max() > 2 ** -9
+
+
+def test_mat_mul_oracle_vs_float64(orc):
+    M, N, K = 37, 300, 29
+    A = orc.fill_normal(M * N, 9, 0, 0.0, 1.0)
+    B = orc.fill_normal(N * K, 9, 1, 0.0, 1.0)
+    out, absdot = orc.mat_mul_rows(A, B, M, N, K)
+    ref = A.reshape(M, N).astype(np.float64) @ B.reshape(N, K).astype(np.float64)
+    assert np.max(np.abs(out - ref) / absdot) < 1e-6
+    # transposed storage of B gives the same values; bias + relu applied after the sum
+    bias = orc.fill_uniform(K, 9, 2, -0.1, 0.1)
+    out_t, _ = orc.mat_mul_rows(A, np.ascontiguousarray(B.reshape(N, K).T), M, N, K, bias=bias, b_transposed=True,
+                                act="relu")
+    assert np.array_equal(out_t, np.maximum(out + bias, 0))
+    # the reference GEMV order agrees within the same bound
+    y = orc.gemv(A[:N], np.ascontiguousarray(B.reshape(N, K).T), N, K)
+    assert np.max(np.abs(y - ref[0]) / absdot[0]) < 1e-6
