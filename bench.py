@@ -166,7 +166,49 @@ def wl_gemm_bf16(stream, steps, warmup):
             "kernel": "gemm_bf16_mfma_kernel<bf16>", "roofline": roofline(tf, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma")}
 
 
-WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "gemm": wl_gemm, "gemm_bf16": wl_gemm_bf16}
+def wl_attention(stream, steps, warmup):
+    """Config 4 prefill: causal GQA 32 q / 8 kv heads, D = 64, T = S = 2048, fp32 N(0,1), scale 1/8.
+    Algorithmic flop = 4 * 32 * 64 * (2048 * 2049 / 2) (QK^T and PV over the unmasked triangle)."""
+    T, qh, kvh, D = 2048, 32, 8, 64
+    q, out = ow.DeviceBuffer.empty(qh * T * D), ow.DeviceBuffer.empty(qh * T * D)
+    k, v = ow.DeviceBuffer.empty(kvh * T * D), ow.DeviceBuffer.empty(kvh * T * D)
+    ow.fill_normal(q, SEED, 400, 0.0, 1.0, stream=stream)
+    ow.fill_normal(k, SEED, 401, 0.0, 1.0, stream=stream)
+    ow.fill_normal(v, SEED, 402, 0.0, 1.0, stream=stream)
+    ms = Timer(stream).run(lambda i: ow.ops.attention_prefill(q, k, v, out, T, T, 0, qh, 4, D, T, stream=stream),
+                           steps, warmup)
+    flop = 4.0 * qh * D * (T * (T + 1) / 2)
+    tf = flop / ms / 1e9
+    return {"workload": "attention_prefill_causal_gqa_32q8kv_d64_t2048", "unit": "TFLOP/s", "value": tf, "ms": ms,
+            "flop": flop, "kernel": "attention_prefill_kernel<2,4>",
+            "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma")}
+
+
+def wl_attention_decode(stream, steps, warmup):
+    """Config 4 decode: one query per head against a 2048-entry cache; 8,404,992 algorithmic bytes.
+    The cache is rotated over 32 copies (1 GiB... of K/V) so the Infinity Cache cannot hold it."""
+    qh, kvh, D, L, sets = 32, 8, 64, 2048, 32
+    q, out = ow.DeviceBuffer.empty(qh * D), ow.DeviceBuffer.empty(qh * D)
+    ow.fill_normal(q, SEED, 410, 0.0, 1.0, stream=stream)
+    ks, vs = [], []
+    for i in range(sets):
+        k, v = ow.DeviceBuffer.empty(kvh * L * D), ow.DeviceBuffer.empty(kvh * L * D)
+        ow.fill_normal(k, SEED, 411 + 2 * i, 0.0, 1.0, stream=stream)
+        ow.fill_normal(v, SEED, 412 + 2 * i, 0.0, 1.0, stream=stream)
+        ks.append(k)
+        vs.append(v)
+    ws = ow.DeviceBuffer.empty(ow.ops.attention_decode_workspace_size(qh, L, D))
+    ms = Timer(stream).run(lambda i: ow.ops.attention_decode(q, ks[i % sets], vs[i % sets], out, qh, 4, D, L, L,
+                                                             workspace=ws, stream=stream), steps, warmup)
+    nbytes = 2 * kvh * L * D * 4 + 2 * qh * D * 4
+    gbs = nbytes / ms / 1e6
+    return {"workload": "attention_decode_32q8kv_d64_len2048", "unit": "GB/s", "value": gbs, "ms": ms,
+            "bytes": nbytes, "kernel": "attention_decode_partial_kernel+combine",
+            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+
+
+WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "gemm": wl_gemm, "gemm_bf16": wl_gemm_bf16, "attention": wl_attention,
+             "attention_decode": wl_attention_decode}
 HEADLINE = "map"
 
 

@@ -104,6 +104,24 @@ int opw_linear_bf16_bf16(const uint16_t *X, const uint16_t *W, const float *bias
 /* dst[i] = bf16 bits of src[i], round to nearest even (tests/model/ops_test.cu:77-82 recipe) */
 int opw_convert_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, void *stream);
 
+/* ---- attention over a KV cache (fp32). q_heads/out [num_q_heads][T][head_dim];
+ * caches [num_q_heads/kv_rep][cap][head_dim] with S valid entries; kv head = q head / kv_rep;
+ * query t sits at position q_offset + t and sees keys 0..min(position, S-1); scale 1/sqrt(head_dim). ---- */
+/* Flash causal prefill (reference: ops::attention_prefill_chunked, include/ops/attention_prefill.cuh:164-177;
+ * requires S >= T, q_offset == S - T, head_dim in {16,32,48,64}, cap >= S) */
+int opw_attention_prefill_f32(const float *q_heads, const float *kcache, const float *vcache, float *out, int T, int S,
+                              int q_offset, int num_q_heads, int kv_rep, int head_dim, int cap, void *stream);
+/* One query per head against `len` cache entries (reference: ops::attention_decode,
+ * include/ops/attention_decode.cuh:99-109; q/out [num_q_heads][head_dim], len <= 8192).
+ * Scratch comes from stream-ordered allocation ... */
+int opw_attention_decode_f32(const float *q, const float *kcache, const float *vcache, float *out, int num_q_heads,
+                             int kv_rep, int head_dim, int len, int max_seq, void *stream);
+/* ... or from a caller workspace of opw_attention_decode_workspace_size() floats (no allocation). */
+int opw_attention_decode_workspace_size(int num_q_heads, int max_len, int head_dim);
+int opw_attention_decode_ws_f32(const float *q, const float *kcache, const float *vcache, float *out,
+                                int num_q_heads, int kv_rep, int head_dim, int len, int max_seq, float *workspace,
+                                int workspace_size, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,13 @@ _SIGNATURES = {
     "opw_linear_bf16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
     "opw_linear_bf16_bf16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
     "opw_convert_f32_to_bf16": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
+    "opw_attention_prefill_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                          c_int, c_int, c_void_p]),
+    "opw_attention_decode_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                         c_void_p]),
+    "opw_attention_decode_workspace_size": (c_int, [c_int, c_int, c_int]),
+    "opw_attention_decode_ws_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                            c_void_p, c_int, c_void_p]),
 }
 
 
@@ -335,6 +342,27 @@ class _Ops:
         fn = lib().opw_linear_bf16_bf16 if x_bf16 else lib().opw_linear_bf16
         check(fn(_p(X), _p(W), _p(bias), _p(Y), rows, in_features, out_features, self.ACTIVATIONS[activation],
                  _stream(stream)))
+
+    def attention_prefill(self, q: Ptr, k: Ptr, v: Ptr, out: Ptr, T: int, S: int, q_offset: int, num_q_heads: int,
+                          kv_rep: int, head_dim: int, cap: int, stream=None) -> None:
+        check(lib().opw_attention_prefill_f32(_p(q), _p(k), _p(v), _p(out), T, S, q_offset, num_q_heads, kv_rep,
+                                              head_dim, cap, _stream(stream)))
+
+    def attention_decode(self, q: Ptr, k: Ptr, v: Ptr, out: Ptr, num_q_heads: int, kv_rep: int, head_dim: int,
+                         length: int, max_seq: int, workspace: Ptr = None, workspace_size: int = 0,
+                         stream=None) -> None:
+        if workspace is None:
+            check(lib().opw_attention_decode_f32(_p(q), _p(k), _p(v), _p(out), num_q_heads, kv_rep, head_dim, length,
+                                                 max_seq, _stream(stream)))
+        else:
+            if isinstance(workspace, DeviceView) and workspace_size == 0:
+                workspace_size = workspace.n
+            check(lib().opw_attention_decode_ws_f32(_p(q), _p(k), _p(v), _p(out), num_q_heads, kv_rep, head_dim,
+                                                    length, max_seq, _p(workspace), workspace_size,
+                                                    _stream(stream)))
+
+    def attention_decode_workspace_size(self, num_q_heads: int, max_len: int, head_dim: int) -> int:
+        return check(lib().opw_attention_decode_workspace_size(num_q_heads, max_len, head_dim))
 
     def convert_f32_to_bf16(self, src: Ptr, dst: Ptr, n: int, stream=None) -> None:
         check(lib().opw_convert_f32_to_bf16(_p(src), _p(dst), n, _stream(stream)))

@@ -1,0 +1,48 @@
+// extern "C" attention surface of libopworks_amd.so (include/opworks_ops.h).
+
+#include <hip/hip_runtime.h>
+
+#include "../include/ops/attention.hpp"
+#include "c_api_common.hpp"
+
+using opworks::capi::guard;
+
+extern "C" {
+
+int opw_attention_prefill_f32(const float *q_heads, const float *kcache, const float *vcache, float *out, int T, int S,
+                              int q_offset, int num_q_heads, int kv_rep, int head_dim, int cap, void *stream) {
+    return guard([&] {
+        opworks::ops::attention_prefill(q_heads, kcache, vcache, out, T, S, q_offset, num_q_heads, kv_rep, head_dim,
+                                        cap, static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
+int opw_attention_decode_f32(const float *q, const float *kcache, const float *vcache, float *out, int num_q_heads,
+                             int kv_rep, int head_dim, int len, int max_seq, void *stream) {
+    return guard([&] {
+        opworks::ops::attention_decode(q, kcache, vcache, out, num_q_heads, kv_rep, head_dim, len, max_seq,
+                                       static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
+int opw_attention_decode_workspace_size(int num_q_heads, int max_len, int head_dim) {
+    return guard([&] {
+        opworks::detail::require(num_q_heads > 0 && max_len > 0 && head_dim > 0, "positive shape required");
+        return opworks::ops::attention_decode_workspace_size(num_q_heads, max_len, head_dim);
+    });
+}
+
+int opw_attention_decode_ws_f32(const float *q, const float *kcache, const float *vcache, float *out,
+                                int num_q_heads, int kv_rep, int head_dim, int len, int max_seq, float *workspace,
+                                int workspace_size, void *stream) {
+    return guard([&] {
+        opworks::ops::attention_decode_ws(q, kcache, vcache, out, num_q_heads, kv_rep, head_dim, len, max_seq,
+                                          workspace, workspace_size, nullptr, 0, 0,
+                                          static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
+} // extern "C"

@@ -434,3 +434,137 @@ void orc_round_bf16(const float *in, float *out, uint16_t *bits, int64_t n) {
         }
     }
 }
+
+/* ---------------------------------------------------------------- attention */
+struct attn_ctx {
+    const float *q, *k, *v;
+    float *out;
+    double *bound;
+    int T, S, qh, kv_rep, D, cap;
+    const int *rows;
+    int nrows;
+    float scale;
+};
+
+/* One (head, row) of the explicit path. */
+static void attn_explicit_row(const struct attn_ctx *c, int h, int row, float *scores, float *o, double *b) {
+    const int kvh = h / c->kv_rep;
+    const float *qrow = c->q + ((int64_t)h * c->T + row) * c->D;
+    const float *kh = c->k + (int64_t)kvh * c->cap * c->D;
+    const float *vh = c->v + (int64_t)kvh * c->cap * c->D;
+    /* linear(q_h, k_h): k-ascending fmaf chain over d (linear_kernel, include/ops/linear.cuh:18-73) */
+    for (int j = 0; j < c->S; ++j) {
+        float acc = 0.f;
+        for (int d = 0; d < c->D; ++d)
+            acc = fmaf(qrow[d], kh[(int64_t)j * c->D + d], acc);
+        scores[j] = acc;
+    }
+    /* causal_scale (include/ops/causal_scale.cuh:9-16): col <= S - T + row ? s * scale : -inf */
+    const int qpos = c->S - c->T + row;
+    for (int j = 0; j < c->S; ++j)
+        scores[j] = j <= qpos ? scores[j] * c->scale : -INFINITY;
+    /* softmax over the row (include/ops/softmax.cuh:10-29) */
+    softmax_row(scores, scores, c->S);
+    /* mat_mul(P, v_h): fmaf chain over keys (include/ops/matmul.cuh:11-66) */
+    for (int d = 0; d < c->D; ++d) {
+        float acc = 0.f;
+        double ab = 0.0;
+        for (int j = 0; j < c->S; ++j) {
+            acc = fmaf(scores[j], vh[(int64_t)j * c->D + d], acc);
+            ab += fabs((double)scores[j] * vh[(int64_t)j * c->D + d]);
+        }
+        o[d] = acc;
+        if (b)
+            b[d] = ab;
+    }
+}
+
+static void attn_range(void *p, int64_t lo, int64_t hi) {
+    struct attn_ctx *c = (struct attn_ctx *)p;
+    float *scores = (float *)malloc(sizeof(float) * (size_t)c->S);
+    const int nr = c->rows ? c->nrows : c->T;
+    for (int64_t w = lo; w < hi; ++w) {
+        const int h = (int)(w / nr), ri = (int)(w % nr);
+        const int row = c->rows ? c->rows[ri] : ri;
+        float *o = c->out + ((int64_t)h * nr + ri) * c->D;
+        double *b = c->bound ? c->bound + ((int64_t)h * nr + ri) * c->D : NULL;
+        attn_explicit_row(c, h, row, scores, o, b);
+    }
+    free(scores);
+}
+
+/* Explicit prefill attention, as LlamaModelT::forward runs it for 2 <= rows <=
+ * 2048 (include/models/llama.cuh:246-263): per q head, QK^T by ops::linear,
+ * causal_scale with scale 1/sqrt(D) (llama.cuh:222), row softmax, then P V by
+ * ops::mat_mul. Only rows listed in `rows` (all T when NULL) are produced:
+ * out/bound are [qh][nrows][D]; bound receives sum_key p*|v| per output. */
+void orc_attention_explicit(const float *q, const float *k, const float *v, float *out, double *bound, int T, int S,
+                            int qh, int kv_rep, int D, int cap, const int *rows, int nrows) {
+    struct attn_ctx c = {q, k, v, out, bound, T, S, qh, kv_rep, D, cap, rows, nrows, 1.0f / sqrtf((float)D)};
+    parallel_for((int64_t)qh * (rows ? nrows : T), attn_range, &c);
+}
+
+/* attention_decode_kernel (include/ops/attention_decode.cuh:14-90), one block
+ * of 256 threads per q head: scores[j] = (fmaf chain over d) * scale, block max,
+ * e_j = expf(s_j - max), block sum, inv = 1/sum, per-thread acc[d] =
+ * fmaf(e_j * inv, v_j[d], acc[d]) over keys j = t, t+256, ..., then a 32-lane
+ * shuffle tree per d and a serial sum over the 8 warps. scale = rsqrtf(D),
+ * restated as 1/sqrtf(D) (exact for D = 64). */
+void orc_attention_decode(const float *q, const float *k, const float *v, float *out, int qh, int kv_rep, int D,
+                          int len, int max_seq) {
+    float *scores = (float *)malloc(sizeof(float) * (size_t)len);
+    float *acc = (float *)malloc(sizeof(float) * REF_THREADS * (size_t)D);
+    float part[REF_THREADS];
+    const float scale = 1.0f / sqrtf((float)D);
+    for (int h = 0; h < qh; ++h) {
+        const int kvh = h / kv_rep;
+        const float *kh = k + (int64_t)kvh * max_seq * D;
+        const float *vh = v + (int64_t)kvh * max_seq * D;
+        const float *qv = q + (int64_t)h * D;
+        for (int j = 0; j < len; ++j) {
+            float dot = 0.f;
+            for (int d = 0; d < D; ++d)
+                dot = fmaf(qv[d], kh[(int64_t)j * D + d], dot);
+            scores[j] = dot * scale;
+        }
+        for (int t = 0; t < REF_THREADS; ++t) {
+            float m = -INFINITY;
+            for (int j = t; j < len; j += REF_THREADS)
+                m = fmaxf(m, scores[j]);
+            part[t] = m;
+        }
+        const float mx = orc_block_reduce(part, REF_THREADS, 1);
+        for (int t = 0; t < REF_THREADS; ++t) {
+            float s = 0.f;
+            for (int j = t; j < len; j += REF_THREADS) {
+                const float e = expf(scores[j] - mx);
+                scores[j] = e;
+                s += e;
+            }
+            part[t] = s;
+        }
+        const float inv = 1.f / orc_block_reduce(part, REF_THREADS, 0);
+        for (int t = 0; t < REF_THREADS; ++t) {
+            float *a = acc + (int64_t)t * D;
+            for (int d = 0; d < D; ++d)
+                a[d] = 0.f;
+            for (int j = t; j < len; j += REF_THREADS) {
+                const float p = scores[j] * inv;
+                for (int d = 0; d < D; ++d)
+                    a[d] = fmaf(p, vh[(int64_t)j * D + d], a[d]);
+            }
+        }
+        for (int d = 0; d < D; ++d) {
+            float total = 0.f;
+            for (int w = 0; w < REF_THREADS / REF_WARP; ++w) {
+                float lanes[REF_WARP];
+                for (int l = 0; l < REF_WARP; ++l)
+                    lanes[l] = acc[(int64_t)(w * REF_WARP + l) * D + d];
+                total += warp_tree(lanes, 0);
+            }
+            out[(int64_t)h * D + d] = total;
+        }
+    }
+    free(scores);
+    free(acc);
+}

@@ -26,6 +26,10 @@
  *                        float64 matmul bound, numpy reference on small shapes
  *  orc_gemv              float64 dot bound; agrees with orc_mat_mul_rows
  *  orc_round_bf16        hand-computed bit patterns incl. ties to even
+ *  orc_attention_explicit  float64 softmax-attention on small shapes; one-key
+ *                        rows return v_0 exactly; uniform keys average V
+ *  orc_attention_decode  equals the explicit path's last row (same maths,
+ *                        other order) and the float64 reference
  */
 #ifndef OPWORKS_ORACLE_H
 #define OPWORKS_ORACLE_H
@@ -73,6 +77,12 @@ void orc_gemv(const float *x, const float *W, float *y, int in, int out);
 
 /* fp32 -> bf16 round-to-nearest-even (bits and/or the rounded float) */
 void orc_round_bf16(const float *in, float *out, uint16_t *bits, int64_t n);
+
+/* attention (layouts of include/ops/attention_prefill.cuh:21-24) */
+void orc_attention_explicit(const float *q, const float *k, const float *v, float *out, double *bound, int T, int S,
+                            int qh, int kv_rep, int D, int cap, const int *rows, int nrows);
+void orc_attention_decode(const float *q, const float *k, const float *v, float *out, int qh, int kv_rep, int D,
+                          int len, int max_seq);
 
 #ifdef __cplusplus
 }

@@ -38,6 +38,9 @@ _SIGS = {
                                 c_int, c_int]),
     "orc_gemv": (None, [_F, _F, _F, c_int, c_int]),
     "orc_round_bf16": (None, [_F, _F, c_void_p, c_int64]),
+    "orc_attention_explicit": (None, [_F, _F, _F, _F, POINTER(c_double), c_int, c_int, c_int, c_int, c_int, c_int,
+                                      POINTER(c_int), c_int]),
+    "orc_attention_decode": (None, [_F, _F, _F, _F, c_int, c_int, c_int, c_int, c_int]),
 }
 
 
@@ -174,3 +177,25 @@ def round_bf16(x):
     bits = np.empty(x.size, np.uint16)
     lib().orc_round_bf16(fp(x), fp(out), bits.ctypes.data, x.size)
     return out, bits
+
+
+def attention_explicit(q, k, v, T, S, qh, kv_rep, D, cap, rows=None):
+    """Returns (out [qh][nrows][D], bound float64 of the same shape)."""
+    q, k, v = f32(q), f32(k), f32(v)
+    nrows = T if rows is None else len(rows)
+    out = np.empty(qh * nrows * D, np.float32)
+    bound = np.empty(qh * nrows * D, np.float64)
+    rp = None
+    if rows is not None:
+        rows = np.ascontiguousarray(rows, np.int32)
+        rp = rows.ctypes.data_as(POINTER(c_int))
+    lib().orc_attention_explicit(fp(q), fp(k), fp(v), fp(out), bound.ctypes.data_as(POINTER(c_double)), T, S, qh,
+                                 kv_rep, D, cap, rp, nrows)
+    return out.reshape(qh, nrows, D), bound.reshape(qh, nrows, D)
+
+
+def attention_decode(q, k, v, qh, kv_rep, D, length, max_seq):
+    q, k, v = f32(q), f32(k), f32(v)
+    out = np.empty(qh * D, np.float32)
+    lib().orc_attention_decode(fp(q), fp(k), fp(v), fp(out), qh, kv_rep, D, length, max_seq)
+    return out.reshape(qh, D)

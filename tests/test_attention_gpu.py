@@ -1,0 +1,103 @@
+"""GPU parity of flash prefill and split-KV decode attention against the
+oracle's restatement of the reference's explicit prefill path and decode
+kernel. Bar (north_star rel <= 1e-4): per output |gpu - ref| <= 1e-4 *
+sum_key p*|v| + 1e-6, i.e. relative to the magnitude of the PV sum."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+SEED = 777
+
+
+def upload(ow, arr):
+    return ow.DeviceBuffer.from_host(np.ascontiguousarray(arr, np.float32))
+
+
+def check(got, ref, bound, tol=1e-4):
+    worst = float(np.max(np.abs(got.astype(np.float64) - ref) / (tol * bound + 1e-6)))
+    assert worst <= 1.0, worst
+
+
+def run_prefill(ow, orc, T, S, qh, kv_rep, D, cap, rows=None, data=None):
+    kvh = qh // kv_rep
+    if data is None:
+        q = orc.fill_normal(qh * T * D, SEED, 0, 0.0, 1.0)
+        k = orc.fill_normal(kvh * cap * D, SEED, 1, 0.0, 1.0)
+        v = orc.fill_normal(kvh * cap * D, SEED, 2, 0.0, 1.0)
+    else:
+        q, k, v = data
+    dq, dk, dv = upload(ow, q), upload(ow, k), upload(ow, v)
+    out = ow.DeviceBuffer.empty(qh * T * D)
+    ow.ops.attention_prefill(dq, dk, dv, out, T, S, S - T, qh, kv_rep, D, cap)
+    got = out.to_host().reshape(qh, T, D)
+    ref, bound = orc.attention_explicit(q, k, v, T, S, qh, kv_rep, D, cap, rows=rows)
+    if rows is not None:
+        got = got[:, rows]
+    check(got, ref, bound)
+
+
+@pytest.mark.parametrize("T,S,qh,kv_rep,D,cap", [
+    (1, 1, 4, 4, 64, 1), (2, 2, 4, 4, 64, 8), (31, 31, 4, 4, 64, 31), (32, 32, 4, 4, 64, 32), (33, 33, 4, 4, 64, 40),
+    (100, 100, 8, 4, 64, 128), (257, 257, 32, 4, 64, 300), (64, 200, 8, 4, 64, 256), (1, 77, 4, 4, 64, 80),
+    (96, 96, 4, 1, 64, 96), (96, 96, 4, 2, 32, 96), (80, 80, 8, 8, 64, 80), (70, 70, 16, 16, 64, 70),
+    (65, 65, 6, 3, 48, 65), (65, 65, 2, 2, 16, 65), (130, 130, 12, 12, 64, 130),
+])
+def test_prefill_matches_oracle(ow, orc, T, S, qh, kv_rep, D, cap):
+    run_prefill(ow, orc, T, S, qh, kv_rep, D, cap)
+
+
+def test_prefill_long_lcg_case(ow, orc):
+    """tests/model/ops_test.cu:316-353: L = 2500 with the reference's LCG inputs (seed 42, q then k then v);
+    the reference checks chunked against explicit at NRMSE <= 1e-5. Here: flash vs the explicit restatement
+    on 64 sampled rows of every head, per-element bound."""
+    L, qh, kvh, D = 2500, 32, 8, 64
+    rng = 42
+    mask64 = (1 << 64) - 1
+
+    def draws(n):
+        nonlocal rng
+        out = np.empty(n, np.float32)
+        for i in range(n):
+            rng = (rng * 6364136223846793005 + 1442695040888963407) & mask64
+            out[i] = np.float32(((rng >> 33) & 0xFFFFFF) / 8388608.0 - 1.5)
+        return out
+
+    q = draws(qh * L * D)
+    k = draws(kvh * L * D)
+    v = draws(kvh * L * D)
+    rows = np.linspace(0, L - 1, 64).astype(np.int32)
+    run_prefill(ow, orc, L, L, qh, qh // kvh, D, L, rows=rows, data=(q, k, v))
+
+
+@pytest.mark.slow
+def test_config4_prefill_full_size_sampled(ow, orc):
+    """Config 4: 32 q heads, 8 kv heads, D = 64, T = S = 2048, N(0,1) inputs, scale 1/8."""
+    T, qh, kvh, D = 2048, 32, 8, 64
+    orc.set_threads(16)
+    q = orc.fill_normal(qh * T * D, SEED, 400, 0.0, 1.0, mt=True)
+    k = orc.fill_normal(kvh * T * D, SEED, 401, 0.0, 1.0, mt=True)
+    v = orc.fill_normal(kvh * T * D, SEED, 402, 0.0, 1.0, mt=True)
+    rows = np.concatenate([np.arange(0, 40), np.arange(T - 40, T), np.arange(40, T - 40, 97)]).astype(np.int32)
+    run_prefill(ow, orc, T, T, qh, qh // kvh, D, T, rows=rows, data=(q, k, v))
+
+
+@pytest.mark.parametrize("length,cap", [(1, 1), (2, 8), (63, 64), (64, 64), (65, 128), (767, 1024), (2048, 2048),
+                                        (8192, 8192)])
+@pytest.mark.parametrize("use_ws", [False, True])
+def test_decode_matches_oracle(ow, orc, length, cap, use_ws):
+    qh, kv_rep, D = 32, 4, 64
+    kvh = qh // kv_rep
+    q = orc.fill_normal(qh * D, SEED, 10, 0.0, 1.0)
+    k = orc.fill_normal(kvh * cap * D, SEED, 11, 0.0, 1.0)
+    v = orc.fill_normal(kvh * cap * D, SEED, 12, 0.0, 1.0)
+    dq, dk, dv = upload(ow, q), upload(ow, k), upload(ow, v)
+    out = ow.DeviceBuffer.empty(qh * D)
+    if use_ws:
+        ws = ow.DeviceBuffer.empty(ow.ops.attention_decode_workspace_size(qh, length, D))
+        ow.ops.attention_decode(dq, dk, dv, out, qh, kv_rep, D, length, cap, workspace=ws)
+    else:
+        ow.ops.attention_decode(dq, dk, dv, out, qh, kv_rep, D, length, cap)
+    got = out.to_host().reshape(qh, D)
+    ref = orc.attention_decode(q, k, v, qh, kv_rep, D, length, cap)
+    _, bound = orc.attention_explicit(q, k, v, 1, length, qh, kv_rep, D, cap)
+    check(got, ref, bound[:, 0])

@@ -215,3 +215,60 @@ def test_mat_mul_oracle_vs_float64(orc):
     # the reference GEMV order agrees within the same bound
     y = orc.gemv(A[:N], np.ascontiguousarray(B.reshape(N, K).T), N, K)
     assert np.max(np.abs(y - ref[0]) / absdot[0]) < 1e-6
+
+
+def _np_attention(q, k, v, T, S, qh, kv_rep, D, cap):
+    """float64 textbook causal attention (scripts/llama/export_reference.py:71-84 maths)."""
+    q = q.reshape(qh, T, D).astype(np.float64)
+    k = k.reshape(qh // kv_rep, cap, D)[:, :S].astype(np.float64)
+    v = v.reshape(qh // kv_rep, cap, D)[:, :S].astype(np.float64)
+    out = np.zeros((qh, T, D))
+    for h in range(qh):
+        s = q[h] @ k[h // kv_rep].T / np.sqrt(D)
+        mask = np.arange(S)[None, :] <= (S - T + np.arange(T))[:, None]
+        s = np.where(mask, s, -np.inf)
+        p = np.exp(s - s.max(1, keepdims=True))
+        p /= p.sum(1, keepdims=True)
+        out[h] = p @ v[h // kv_rep]
+    return out
+
+
+@pytest.mark.parametrize("T,S,qh,kv_rep,D,cap", [(5, 5, 4, 2, 16, 5), (17, 40, 8, 4, 64, 48), (64, 64, 2, 1, 32, 64)])
+def test_attention_explicit_vs_float64(orc, T, S, qh, kv_rep, D, cap):
+    q = orc.fill_normal(qh * T * D, 11, 0, 0.0, 1.0)
+    k = orc.fill_normal(qh // kv_rep * cap * D, 11, 1, 0.0, 1.0)
+    v = orc.fill_normal(qh // kv_rep * cap * D, 11, 2, 0.0, 1.0)
+    out, bound = orc.attention_explicit(q, k, v, T, S, qh, kv_rep, D, cap)
+    ref = _np_attention(q, k, v, T, S, qh, kv_rep, D, cap)
+    assert np.max(np.abs(out - ref) / (bound + 1e-12)) < 1e-5
+    # sampled rows equal the full run
+    rows = [0, T - 1]
+    out2, _ = orc.attention_explicit(q, k, v, T, S, qh, kv_rep, D, cap, rows=rows)
+    assert np.array_equal(out2, out[:, rows])
+
+
+def test_attention_special_cases(orc):
+    # a query that sees one key returns that key's value row exactly
+    T = S = 3
+    D = 16
+    q = orc.fill_normal(T * D, 12, 0, 0.0, 1.0)
+    k = orc.fill_normal(S * D, 12, 1, 0.0, 1.0)
+    v = orc.fill_normal(S * D, 12, 2, 0.0, 1.0)
+    out, _ = orc.attention_explicit(q, k, v, T, S, 1, 1, D, S)
+    assert np.array_equal(out[0, 0], v[:D])
+    # identical keys: softmax is uniform and the output is the mean of the visible values
+    k_same = np.tile(k[:D], S)
+    out, _ = orc.attention_explicit(q, k_same, v, T, S, 1, 1, D, S)
+    assert np.allclose(out[0, 2], v.reshape(S, D).mean(0), atol=1e-6)
+
+
+@pytest.mark.parametrize("length", [1, 7, 256, 300])
+def test_attention_decode_equals_last_row(orc, length):
+    qh, kv_rep, D, cap = 8, 4, 64, 320
+    q = orc.fill_normal(qh * D, 13, 0, 0.0, 1.0)
+    k = orc.fill_normal(qh // kv_rep * cap * D, 13, 1, 0.0, 1.0)
+    v = orc.fill_normal(qh // kv_rep * cap * D, 13, 2, 0.0, 1.0)
+    dec = orc.attention_decode(q, k, v, qh, kv_rep, D, length, cap)
+    # the decode query is the prefill row at position length - 1 (T = 1, S = length)
+    exp_, bound = orc.attention_explicit(q, k, v, 1, length, qh, kv_rep, D, cap)
+    assert np.max(np.abs(dec - exp_[:, 0]) / (bound[:, 0] + 1e-12)) < 1e-5
