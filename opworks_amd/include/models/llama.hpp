@@ -1,0 +1,612 @@
+#pragma once
+
+// Llama-3.x decoder on MI355X, fp32 weights (reference: include/models/llama.cuh:43-293).
+//
+// Same model-level contract as the reference's LlamaModelT / LlamaSession:
+// load (pack or seeded random init), create_session(max_seq <= 8192),
+// prefill (fresh session, returns the first generated token), decode_step
+// (appends one token, returns the next), is_eos, last_logits,
+// copy_last_logits, hidden_state, debug_prefill. K is cached post-RoPE, V as
+// projected; the LM head is the tied embedding applied to the last row.
+//
+// MI355X layout of the weights in HBM (differs from the HF layout on purpose):
+//  * wqkv  [(qh + 2 kvh) D][H]  q, k and v rows concatenated: one GEMV/GEMM;
+//  * wgu   [2 I][H]             gate_i and up_i rows interleaved, so one wave's
+//                               rows give silu(gate) * up directly;
+//  * wo [H][qh D], wdown [H][I], embed [V][H] as in HF.
+// Decode is one captured HIP graph per session (5 kernels per layer + LM head);
+// prefill runs the MFMA GEMMs with fused residual / SwiGLU epilogues and the
+// flash attention kernel.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <functional>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../core/hip_utils.hpp"
+#include "../core/random.hpp"
+#include "../core/typed_device_buffer.hpp"
+#include "../ops/attention.hpp"
+#include "../ops/gemm_f32.hpp"
+#include "../ops/rms_norm.hpp"
+#include "../runtime/model_config.hpp"
+#include "../runtime/pack_reader.hpp"
+#include "llama_kernels.hpp"
+
+namespace opworks {
+
+namespace llama_detail {
+
+// Stream ids of the seeded random initialisation (see random.hpp). Logical
+// tensors are generated in the HF layout: element (o, i) of a [out][in]
+// projection is draw o * in + i of its stream.
+constexpr uint64_t kStreamEmbed = 1;
+constexpr uint64_t kStreamFinalNorm = 2;
+inline uint64_t layer_stream(int layer, int which) { return 64 + 16 * static_cast<uint64_t>(layer) + which; }
+enum LayerTensor { kQ = 0, kK = 1, kV = 2, kO = 3, kGate = 4, kUp = 5, kDown = 6, kInNorm = 7, kPostNorm = 8 };
+
+// dst[(r * row_stride + row_offset) * cols + c] = N(mean, sd) draw r * cols + c
+__global__ __launch_bounds__(256) static void fill_rows_normal_kernel(float *dst, int64_t rows, int cols,
+                                                                      int row_stride, int row_offset, uint64_t key,
+                                                                      float mean, float sd) {
+    OPWORKS_GRID_LOOP(i, rows * cols) {
+        const int64_t r = i / cols, c = i % cols;
+        dst[(r * row_stride + row_offset) * cols + c] = rng::normal(key, static_cast<uint64_t>(i), mean, sd);
+    }
+}
+__global__ __launch_bounds__(256) static void fill_uniform_kernel(float *dst, int64_t n, uint64_t key, float lo,
+                                                                  float hi) {
+    OPWORKS_GRID_LOOP(i, n) { dst[i] = rng::uniform(key, static_cast<uint64_t>(i), lo, hi); }
+}
+__global__ __launch_bounds__(256) static void fill_const_kernel(float *dst, int64_t n, float v) {
+    OPWORKS_GRID_LOOP(i, n) { dst[i] = v; }
+}
+
+inline int fill_grid(int64_t n) {
+    const int64_t need = detail::blocks_for64(n, 256), cap = 65536;
+    return static_cast<int>(need < cap ? (need > 0 ? need : 1) : cap);
+}
+
+} // namespace llama_detail
+
+// Norm weights of the seeded init: ones (HF init) or U[0.5, 1.5] (exercises gamma in tests).
+enum class NormInit { ones = 0, uniform = 1 };
+
+struct LlamaLayerWeights {
+    TypedDeviceBuffer<float> input_norm, post_norm; // [H]
+    TypedDeviceBuffer<float> wqkv;                  // [(qh + 2 kvh) D][H]
+    TypedDeviceBuffer<float> wo;                    // [H][qh D]
+    TypedDeviceBuffer<float> wgu;                   // [2 I][H], rows gate_0, up_0, gate_1, ...
+    TypedDeviceBuffer<float> wdown;                 // [H][I]
+};
+
+struct LlamaWeights {
+    TypedDeviceBuffer<float> embed;      // [V][H], also the LM head
+    TypedDeviceBuffer<float> final_norm; // [H]
+    TypedDeviceBuffer<float> inv_freq;   // [D/2]
+    std::vector<LlamaLayerWeights> layers;
+};
+
+struct LlamaSession {
+    int max_seq_len = 0;
+    int length = 0; // valid cache entries
+    hipStream_t stream = nullptr;
+    // KV cache: [layer][kvh][cap][D] for K and for V
+    TypedDeviceBuffer<float> kcache, vcache;
+    // decode step
+    TypedDeviceBuffer<float> d_hidden, d_q, d_attn, d_act, logits, attn_partial, lm_best_val;
+    TypedDeviceBuffer<int32_t> lm_best_idx, argmax_out, counters, state_buf, ids;
+    // prefill
+    TypedDeviceBuffer<float> hidden, normed, qkv, q_heads, attn_heads, attn, act;
+    int attn_max_chunks = 0;
+    int lm_grid = 0;
+    llama::StepState *h_state = nullptr; // pinned
+    int32_t *h_token = nullptr;          // pinned
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    int last_prefill_rows = 0;
+
+    LlamaSession() = default;
+    LlamaSession(const LlamaSession &) = delete;
+    LlamaSession &operator=(const LlamaSession &) = delete;
+    ~LlamaSession() {
+        if (graph_exec)
+            (void)hipGraphExecDestroy(graph_exec);
+        if (graph)
+            (void)hipGraphDestroy(graph);
+        if (h_state)
+            (void)hipHostFree(h_state);
+        if (h_token)
+            (void)hipHostFree(h_token);
+        if (stream)
+            (void)hipStreamDestroy(stream);
+    }
+
+    // Reset only invalidates the length; stale cache bytes are never read.
+    void reset() { length = 0; }
+
+    llama::StepState *state() { return reinterpret_cast<llama::StepState *>(state_buf.data()); }
+};
+
+class LlamaModel {
+  public:
+    using Session = LlamaSession;
+    static constexpr int kMaxSeqLen = detail::kAttnDecodeMaxLen; // 8192
+
+    // Loads an OPWPACK1 float32 pack (scripts/llama/pack_format.py layout).
+    static std::unique_ptr<LlamaModel> load(const std::string &pack_path) {
+        PackReader pack(pack_path);
+        if (pack.dtype() != "float32")
+            throw std::runtime_error("this build runs float32 packs only (got " + pack.dtype() + ")");
+        auto m = std::unique_ptr<LlamaModel>(new LlamaModel(ModelConfig::from_manifest(pack.manifest())));
+        m->check_supported();
+        m->allocate();
+        m->upload_pack(pack);
+        return m;
+    }
+
+    // Seeded random weights: projections and embedding ~ N(0, std), norms per NormInit.
+    static std::unique_ptr<LlamaModel> load_random(const ModelConfig &cfg, uint64_t seed, float std,
+                                                   NormInit norms) {
+        auto m = std::unique_ptr<LlamaModel>(new LlamaModel(cfg));
+        m->check_supported();
+        m->allocate();
+        m->init_random(seed, std, norms);
+        return m;
+    }
+
+    const ModelConfig &config() const { return cfg_; }
+    const LlamaWeights &weights() const { return w_; }
+
+    std::unique_ptr<Session> create_session(int max_seq_len) const {
+        if (max_seq_len <= 0 || max_seq_len > kMaxSeqLen)
+            throw std::invalid_argument("max_seq_len must be in (0, 8192]");
+        auto s = std::make_unique<Session>();
+        const int64_t T = max_seq_len, H = cfg_.hidden_size, I = cfg_.intermediate_size;
+        const int64_t kvh = cfg_.num_kv_heads, D = cfg_.head_dim, qh = cfg_.num_q_heads, L = cfg_.num_layers;
+        s->max_seq_len = max_seq_len;
+        OPWORKS_HIP_CHECK(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
+        s->kcache = TypedDeviceBuffer<float>(L * kvh * T * D);
+        s->vcache = TypedDeviceBuffer<float>(L * kvh * T * D);
+        s->d_hidden = TypedDeviceBuffer<float>(H);
+        s->d_q = TypedDeviceBuffer<float>(qh * D);
+        s->d_attn = TypedDeviceBuffer<float>(qh * D);
+        s->d_act = TypedDeviceBuffer<float>(I);
+        s->logits = TypedDeviceBuffer<float>(cfg_.vocab_size);
+        s->attn_max_chunks = static_cast<int>(detail::blocks_for64(T, detail::kAttnChunk));
+        s->attn_partial = TypedDeviceBuffer<float>(qh * s->attn_max_chunks * (D + 2));
+        s->lm_grid = static_cast<int>(detail::blocks_for64(cfg_.vocab_size, llama::kRows * llama::kWavesPerBlock));
+        s->lm_best_val = TypedDeviceBuffer<float>(s->lm_grid);
+        s->lm_best_idx = TypedDeviceBuffer<int32_t>(s->lm_grid);
+        s->argmax_out = TypedDeviceBuffer<int32_t>(1);
+        s->counters = TypedDeviceBuffer<int32_t>(kvh + 1); // [kvh] attention merges, [kvh] LM head
+        s->state_buf = TypedDeviceBuffer<int32_t>(4);
+        s->ids = TypedDeviceBuffer<int32_t>(T);
+        s->hidden = TypedDeviceBuffer<float>(T * H);
+        s->normed = TypedDeviceBuffer<float>(T * H);
+        s->qkv = TypedDeviceBuffer<float>(T * cfg_.qkv_width());
+        s->q_heads = TypedDeviceBuffer<float>(T * qh * D);
+        s->attn_heads = TypedDeviceBuffer<float>(T * qh * D);
+        s->attn = TypedDeviceBuffer<float>(T * qh * D);
+        s->act = TypedDeviceBuffer<float>(T * I);
+        OPWORKS_HIP_CHECK(hipMemsetAsync(s->counters.data(), 0, sizeof(int32_t) * (kvh + 1), s->stream));
+        OPWORKS_HIP_CHECK(hipMemsetAsync(s->state_buf.data(), 0, sizeof(int32_t) * 4, s->stream));
+        OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&s->h_state), sizeof(llama::StepState)));
+        OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&s->h_token), sizeof(int32_t)));
+        synchronize(s->stream);
+        return s;
+    }
+
+    // Runs the prompt, fills the cache, returns the first generated token.
+    int32_t prefill(Session &s, const std::vector<int32_t> &ids) {
+        check_prefill(s, ids);
+        run_prefill(s, ids, nullptr);
+        return s.h_state->next;
+    }
+
+    // Appends `token` at position length and returns the argmax of the next token.
+    int32_t decode_step(Session &s, int32_t token) {
+        if (token < 0 || token >= cfg_.vocab_size)
+            throw std::invalid_argument("token id outside the vocabulary");
+        if (s.length >= s.max_seq_len)
+            throw std::invalid_argument("session capacity exhausted");
+        s.h_state->token = token;
+        s.h_state->pos = s.length;
+        s.h_state->next = -1;
+        OPWORKS_HIP_CHECK(hipMemcpyAsync(s.state(), s.h_state, sizeof(llama::StepState), hipMemcpyHostToDevice,
+                                         s.stream));
+        if (!s.graph_exec)
+            capture_decode_graph(s);
+        OPWORKS_HIP_CHECK(hipGraphLaunch(s.graph_exec, s.stream));
+        OPWORKS_HIP_CHECK(hipMemcpyAsync(s.h_state, s.state(), sizeof(llama::StepState), hipMemcpyDeviceToHost,
+                                         s.stream));
+        synchronize(s.stream);
+        s.length += 1;
+        s.last_prefill_rows = 0;
+        return s.h_state->next;
+    }
+
+    bool is_eos(int32_t token) const {
+        return std::find(cfg_.eos_token_ids.begin(), cfg_.eos_token_ids.end(), token) != cfg_.eos_token_ids.end();
+    }
+
+    std::vector<float> last_logits(Session &s) const {
+        std::vector<float> out(static_cast<size_t>(cfg_.vocab_size));
+        copy_last_logits(s, out.data(), cfg_.vocab_size);
+        return out;
+    }
+
+    void copy_last_logits(Session &s, float *out, int n) const {
+        if (n != cfg_.vocab_size)
+            throw std::invalid_argument("logits buffer must hold vocab_size floats");
+        OPWORKS_HIP_CHECK(hipMemcpyAsync(out, s.logits.data(), sizeof(float) * static_cast<size_t>(n),
+                                         hipMemcpyDeviceToHost, s.stream));
+        synchronize(s.stream);
+    }
+
+    // Residual stream of the last prefill: rows x H.
+    std::vector<float> hidden_state(Session &s, int rows) const {
+        if (rows <= 0 || rows > s.max_seq_len)
+            throw std::invalid_argument("rows outside the session capacity");
+        std::vector<float> out(static_cast<size_t>(rows) * cfg_.hidden_size);
+        OPWORKS_HIP_CHECK(hipMemcpyAsync(out.data(), s.hidden.data(), out.size() * sizeof(float),
+                                         hipMemcpyDeviceToHost, s.stream));
+        synchronize(s.stream);
+        return out;
+    }
+
+    // Like prefill, also returning the residual stream after the embedding and after each layer.
+    std::vector<std::vector<float>> debug_prefill(Session &s, const std::vector<int32_t> &ids) {
+        check_prefill(s, ids);
+        std::vector<std::vector<float>> captures;
+        const int n = static_cast<int>(ids.size());
+        run_prefill(s, ids, [&](int) {
+            std::vector<float> h(static_cast<size_t>(n) * cfg_.hidden_size);
+            const float *src = n == 1 ? s.d_hidden.data() : s.hidden.data();
+            OPWORKS_HIP_CHECK(hipMemcpyAsync(h.data(), src, h.size() * sizeof(float), hipMemcpyDeviceToHost,
+                                             s.stream));
+            synchronize(s.stream);
+            captures.push_back(std::move(h));
+        });
+        return captures;
+    }
+
+  private:
+    explicit LlamaModel(const ModelConfig &cfg) : cfg_(cfg) {}
+
+    ModelConfig cfg_;
+    LlamaWeights w_;
+
+    void check_supported() const {
+        const int H = cfg_.hidden_size, I = cfg_.intermediate_size;
+        if (H % 256 != 0 || H / 256 > 16 || (H / 256 & (H / 256 - 1)) != 0)
+            throw std::runtime_error("hidden_size must be 256 * {1,2,4,8,16}");
+        if (I % 1024 != 0 || I / 1024 > 16 || (I / 1024 & (I / 1024 - 1)) != 0)
+            throw std::runtime_error("intermediate_size must be 1024 * {1,2,4,8,16}");
+        if (cfg_.head_dim != 64 && cfg_.head_dim != 32)
+            throw std::runtime_error("head_dim must be 32 or 64");
+        if (cfg_.kv_rep() > 16)
+            throw std::runtime_error("at most 16 query heads per kv head");
+    }
+
+    void check_prefill(Session &s, const std::vector<int32_t> &ids) const {
+        for (int32_t id : ids)
+            if (id < 0 || id >= cfg_.vocab_size)
+                throw std::invalid_argument("token id outside the vocabulary");
+        if (ids.empty())
+            throw std::invalid_argument("prefill requires at least one token");
+        if (static_cast<int>(ids.size()) > s.max_seq_len)
+            throw std::invalid_argument("prompt exceeds the session capacity");
+        if (s.length != 0)
+            throw std::invalid_argument("prefill requires a fresh session (reset first)");
+    }
+
+    void allocate() {
+        const int64_t H = cfg_.hidden_size, I = cfg_.intermediate_size, V = cfg_.vocab_size;
+        w_.embed = TypedDeviceBuffer<float>(V * H);
+        w_.final_norm = TypedDeviceBuffer<float>(H);
+        w_.inv_freq = TypedDeviceBuffer<float>::from_host(cfg_.rope_inv_freq());
+        w_.layers.resize(static_cast<size_t>(cfg_.num_layers));
+        for (auto &l : w_.layers) {
+            l.input_norm = TypedDeviceBuffer<float>(H);
+            l.post_norm = TypedDeviceBuffer<float>(H);
+            l.wqkv = TypedDeviceBuffer<float>(int64_t(cfg_.qkv_width()) * H);
+            l.wo = TypedDeviceBuffer<float>(H * cfg_.q_width());
+            l.wgu = TypedDeviceBuffer<float>(2 * I * H);
+            l.wdown = TypedDeviceBuffer<float>(H * I);
+        }
+    }
+
+    void init_random(uint64_t seed, float sd, NormInit norms) {
+        using namespace llama_detail;
+        const int64_t H = cfg_.hidden_size, I = cfg_.intermediate_size, V = cfg_.vocab_size;
+        const int64_t qw = cfg_.q_width(), kw = cfg_.kv_width();
+        auto rows_fill = [&](float *dst, int64_t rows, int64_t cols, int stride, int offset, uint64_t stream) {
+            launch_async(nullptr, fill_rows_normal_kernel, fill_grid(rows * cols), 256, dst, rows,
+                         static_cast<int>(cols), stride, offset, rng::stream_key(seed, stream), 0.f, sd);
+        };
+        auto norm_fill = [&](float *dst, uint64_t stream) {
+            if (norms == NormInit::ones)
+                launch_async(nullptr, fill_const_kernel, fill_grid(H), 256, dst, H, 1.f);
+            else
+                launch_async(nullptr, fill_uniform_kernel, fill_grid(H), 256, dst, H, rng::stream_key(seed, stream),
+                             0.5f, 1.5f);
+        };
+        rows_fill(w_.embed.data(), V, H, 1, 0, kStreamEmbed);
+        norm_fill(w_.final_norm.data(), kStreamFinalNorm);
+        for (int l = 0; l < cfg_.num_layers; ++l) {
+            LlamaLayerWeights &lw = w_.layers[static_cast<size_t>(l)];
+            rows_fill(lw.wqkv.data(), qw, H, 1, 0, layer_stream(l, kQ));
+            rows_fill(lw.wqkv.data() + qw * H, kw, H, 1, 0, layer_stream(l, kK));
+            rows_fill(lw.wqkv.data() + (qw + kw) * H, kw, H, 1, 0, layer_stream(l, kV));
+            rows_fill(lw.wo.data(), H, qw, 1, 0, layer_stream(l, kO));
+            rows_fill(lw.wgu.data(), I, H, 2, 0, layer_stream(l, kGate));
+            rows_fill(lw.wgu.data(), I, H, 2, 1, layer_stream(l, kUp));
+            rows_fill(lw.wdown.data(), H, I, 1, 0, layer_stream(l, kDown));
+            norm_fill(lw.input_norm.data(), layer_stream(l, kInNorm));
+            norm_fill(lw.post_norm.data(), layer_stream(l, kPostNorm));
+        }
+        synchronize(nullptr);
+    }
+
+    void upload_pack(const PackReader &pack) {
+        const int64_t H = cfg_.hidden_size, I = cfg_.intermediate_size, V = cfg_.vocab_size;
+        const int64_t qw = cfg_.q_width(), kw = cfg_.kv_width();
+        // one pinned staging buffer, sized for the largest tensor
+        int64_t largest = std::max<int64_t>(V * H, I * H);
+        float *stage = nullptr;
+        OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&stage), sizeof(float) * largest));
+        struct Free {
+            float *p;
+            ~Free() { (void)hipHostFree(p); }
+        } guard{stage};
+        auto read = [&](const std::string &name, int64_t numel) {
+            if (pack.meta(name).numel != numel)
+                throw std::runtime_error(name + ": element count mismatch");
+            pack.read_into(name, stage, sizeof(float) * static_cast<size_t>(numel));
+        };
+        auto put = [&](float *dst, int64_t numel) {
+            OPWORKS_HIP_CHECK(hipMemcpy(dst, stage, sizeof(float) * numel, hipMemcpyHostToDevice));
+        };
+        auto put_rows_strided = [&](float *dst, int64_t rows, int64_t cols, int offset) {
+            OPWORKS_HIP_CHECK(hipMemcpy2D(dst + offset * cols, sizeof(float) * 2 * cols, stage, sizeof(float) * cols,
+                                          sizeof(float) * cols, rows, hipMemcpyHostToDevice));
+        };
+        read("model.embed_tokens.weight", V * H);
+        put(w_.embed.data(), V * H);
+        read("model.norm.weight", H);
+        put(w_.final_norm.data(), H);
+        for (int l = 0; l < cfg_.num_layers; ++l) {
+            const std::string p = "model.layers." + std::to_string(l) + ".";
+            LlamaLayerWeights &lw = w_.layers[static_cast<size_t>(l)];
+            read(p + "input_layernorm.weight", H);
+            put(lw.input_norm.data(), H);
+            read(p + "self_attn.q_proj.weight", qw * H);
+            put(lw.wqkv.data(), qw * H);
+            read(p + "self_attn.k_proj.weight", kw * H);
+            put(lw.wqkv.data() + qw * H, kw * H);
+            read(p + "self_attn.v_proj.weight", kw * H);
+            put(lw.wqkv.data() + (qw + kw) * H, kw * H);
+            read(p + "self_attn.o_proj.weight", H * qw);
+            put(lw.wo.data(), H * qw);
+            read(p + "post_attention_layernorm.weight", H);
+            put(lw.post_norm.data(), H);
+            read(p + "mlp.gate_proj.weight", I * H);
+            put_rows_strided(lw.wgu.data(), I, H, 0);
+            read(p + "mlp.up_proj.weight", I * H);
+            put_rows_strided(lw.wgu.data(), I, H, 1);
+            read(p + "mlp.down_proj.weight", H * I);
+            put(lw.wdown.data(), H * I);
+        }
+        if (!pack.has("lm_head.weight"))
+            throw std::runtime_error("pack has neither lm_head.weight nor a tying alias");
+        if (pack.meta("lm_head.weight").offset != pack.meta("model.embed_tokens.weight").offset)
+            throw std::runtime_error("untied lm_head.weight is not supported (Llama-3.2 ties it to the embedding)");
+    }
+
+    float *layer_k(Session &s, int l) const {
+        return s.kcache.data() + int64_t(l) * cfg_.num_kv_heads * s.max_seq_len * cfg_.head_dim;
+    }
+    float *layer_v(Session &s, int l) const {
+        return s.vcache.data() + int64_t(l) * cfg_.num_kv_heads * s.max_seq_len * cfg_.head_dim;
+    }
+
+    // ---- decode step (one token at state.pos) -----------------------------
+    template <int kV, int kV2> void enqueue_decode_layer(Session &s, int l) const {
+        const int H = cfg_.hidden_size, I = cfg_.intermediate_size, D = cfg_.head_dim;
+        const int qh = cfg_.num_q_heads, kvh = cfg_.num_kv_heads;
+        const int qkv_waves = (qh + 2 * kvh) * (D / 4);
+        hipStream_t st = s.stream;
+        const LlamaLayerWeights &lw = w_.layers[static_cast<size_t>(l)];
+        llama::QkvArgs qa{};
+        qa.hidden_in = l == 0 ? nullptr : s.d_hidden.data();
+        qa.embed = w_.embed.data();
+        qa.hidden_out = s.d_hidden.data();
+        qa.gamma = lw.input_norm.data();
+        qa.wqkv = lw.wqkv.data();
+        qa.inv_freq = w_.inv_freq.data();
+        qa.q_out = s.d_q.data();
+        qa.kcache = layer_k(s, l);
+        qa.vcache = layer_v(s, l);
+        qa.state = s.state();
+        qa.eps = cfg_.rms_norm_eps;
+        qa.qh = qh;
+        qa.kvh = kvh;
+        qa.D = D;
+        qa.cap = s.max_seq_len;
+        launch_async(st, llama::qkv_rope_kernel<kV>, detail::blocks_for64(qkv_waves, llama::kWavesPerBlock),
+                     llama::kBlock, qa);
+        llama::DecodeAttnArgs aa{};
+        aa.q = s.d_q.data();
+        aa.kcache = layer_k(s, l);
+        aa.vcache = layer_v(s, l);
+        aa.out = s.d_attn.data();
+        aa.partial = s.attn_partial.data();
+        aa.counters = reinterpret_cast<unsigned *>(s.counters.data());
+        aa.state = s.state();
+        aa.kv_rep = cfg_.kv_rep();
+        aa.D = D;
+        aa.cap = s.max_seq_len;
+        aa.max_chunks = s.attn_max_chunks;
+        aa.scale = 1.f / std::sqrt(static_cast<float>(D));
+        launch_async(st, llama::decode_attention_kernel, dim3(kvh, s.attn_max_chunks), cfg_.kv_rep() * kWaveSize, aa);
+        launch_async(st, llama::gemv_residual_kernel<kV>,
+                     detail::blocks_for64(detail::blocks_for64(H, llama::kRows), llama::kWavesPerBlock), llama::kBlock,
+                     lw.wo.data(), s.d_attn.data(), s.d_hidden.data(), H);
+        launch_async(st, llama::swiglu_gemv_kernel<kV>,
+                     detail::blocks_for64(detail::blocks_for64(I, llama::kRows / 2), llama::kWavesPerBlock),
+                     llama::kBlock, s.d_hidden.data(), lw.post_norm.data(), cfg_.rms_norm_eps, lw.wgu.data(),
+                     s.d_act.data(), I);
+        launch_async(st, llama::down_residual_kernel<kV2>, detail::blocks_for64(H, llama::kRows), llama::kBlock,
+                     lw.wdown.data(), s.d_act.data(), s.d_hidden.data(), H);
+    }
+
+    // All layers then the LM head; `hook(l)` (debug only) runs after layer l.
+    void enqueue_decode(Session &s, const std::function<void(int)> &hook = nullptr) const {
+        dispatch_widths([&](auto v, auto v2) {
+            constexpr int kV = decltype(v)::value, kV2 = decltype(v2)::value;
+            for (int l = 0; l < cfg_.num_layers; ++l) {
+                enqueue_decode_layer<kV, kV2>(s, l);
+                if (hook)
+                    hook(l);
+            }
+            enqueue_lm_head<kV>(s, s.d_hidden.data());
+        });
+    }
+
+    template <int kV> void enqueue_lm_head(Session &s, const float *hidden_row) const {
+        llama::LmHeadArgs la{};
+        la.hidden_row = hidden_row;
+        la.gamma = w_.final_norm.data();
+        la.embed = w_.embed.data();
+        la.logits = s.logits.data();
+        la.best_val = s.lm_best_val.data();
+        la.best_idx = s.lm_best_idx.data();
+        la.counter = reinterpret_cast<unsigned *>(s.counters.data() + cfg_.num_kv_heads);
+        la.state = s.state();
+        la.argmax_out = s.argmax_out.data();
+        la.eps = cfg_.rms_norm_eps;
+        la.vocab = cfg_.vocab_size;
+        launch_async(s.stream, llama::lm_head_argmax_kernel<kV>, s.lm_grid, llama::kBlock, la);
+    }
+
+    template <typename F> void dispatch_widths(F &&f) const {
+        const int v = cfg_.hidden_size / 256, v2 = cfg_.intermediate_size / 1024;
+        auto with_v2 = [&](auto vt) {
+            switch (v2) {
+            case 1: f(vt, detail::IntTag<1>{}); break;
+            case 2: f(vt, detail::IntTag<2>{}); break;
+            case 4: f(vt, detail::IntTag<4>{}); break;
+            case 8: f(vt, detail::IntTag<8>{}); break;
+            case 16: f(vt, detail::IntTag<16>{}); break;
+            default: throw std::runtime_error("unsupported intermediate_size");
+            }
+        };
+        switch (v) {
+        case 1: with_v2(detail::IntTag<1>{}); break;
+        case 2: with_v2(detail::IntTag<2>{}); break;
+        case 4: with_v2(detail::IntTag<4>{}); break;
+        case 8: with_v2(detail::IntTag<8>{}); break;
+        case 16: with_v2(detail::IntTag<16>{}); break;
+        default: throw std::runtime_error("unsupported hidden_size");
+        }
+    }
+
+    void capture_decode_graph(Session &s) const {
+        OPWORKS_HIP_CHECK(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
+        try {
+            enqueue_decode(s);
+        } catch (...) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(s.stream, &g);
+            if (g)
+                (void)hipGraphDestroy(g);
+            throw;
+        }
+        OPWORKS_HIP_CHECK(hipStreamEndCapture(s.stream, &s.graph));
+        OPWORKS_HIP_CHECK(hipGraphInstantiate(&s.graph_exec, s.graph, nullptr, nullptr, 0));
+    }
+
+    // ---- prefill -------------------------------------------------------------
+    void run_prefill(Session &s, const std::vector<int32_t> &ids, const std::function<void(int)> &hook) {
+        const int n = static_cast<int>(ids.size());
+        if (n == 1) { // one row: the decode kernels (the reference's rows == 1 path)
+            s.h_state->token = ids[0];
+            s.h_state->pos = 0;
+            s.h_state->next = -1;
+            OPWORKS_HIP_CHECK(hipMemcpyAsync(s.state(), s.h_state, sizeof(llama::StepState),
+                                             hipMemcpyHostToDevice, s.stream));
+            if (hook) {
+                run_decode_layers_with_hook(s, hook);
+            } else {
+                if (!s.graph_exec)
+                    capture_decode_graph(s);
+                OPWORKS_HIP_CHECK(hipGraphLaunch(s.graph_exec, s.stream));
+            }
+        } else {
+            OPWORKS_HIP_CHECK(hipMemcpyAsync(s.ids.data(), ids.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice,
+                                             s.stream));
+            s.h_state->pos = n; // the next decode position
+            OPWORKS_HIP_CHECK(hipMemcpyAsync(s.state(), s.h_state, sizeof(llama::StepState),
+                                             hipMemcpyHostToDevice, s.stream));
+            enqueue_prefill(s, n, hook);
+        }
+        OPWORKS_HIP_CHECK(hipMemcpyAsync(s.h_state, s.state(), sizeof(llama::StepState), hipMemcpyDeviceToHost,
+                                         s.stream));
+        synchronize(s.stream);
+        s.length = n;
+        s.last_prefill_rows = n;
+    }
+
+    // Single-row prefill with per-layer captures: the decode kernels launched eagerly.
+    void run_decode_layers_with_hook(Session &s, const std::function<void(int)> &hook) {
+        // Layer 0's first kernel writes the embedding row into the residual stream;
+        // copy it beforehand so the "after embedding" capture sees it.
+        const int H = cfg_.hidden_size;
+        OPWORKS_HIP_CHECK(hipMemcpyAsync(s.d_hidden.data(), w_.embed.data() + int64_t(s.h_state->token) * H,
+                                         sizeof(float) * H, hipMemcpyDeviceToDevice, s.stream));
+        hook(-1);
+        enqueue_decode(s, hook);
+    }
+
+    void enqueue_prefill(Session &s, int n, const std::function<void(int)> &hook) {
+        const int H = cfg_.hidden_size, I = cfg_.intermediate_size, D = cfg_.head_dim;
+        const int qh = cfg_.num_q_heads, kvh = cfg_.num_kv_heads, qkvw = cfg_.qkv_width();
+        hipStream_t st = s.stream;
+        launch_async(st, llama::embedding_kernel, detail::stream_grid(int64_t(n) * H / 4), 256, w_.embed.data(),
+                     s.ids.data(), s.hidden.data(), n, H);
+        if (hook)
+            hook(-1);
+        for (int l = 0; l < cfg_.num_layers; ++l) {
+            const LlamaLayerWeights &lw = w_.layers[static_cast<size_t>(l)];
+            ops::rms_norm(s.hidden.data(), lw.input_norm.data(), s.normed.data(), n, H, cfg_.rms_norm_eps, st);
+            detail::gemm_f32_launch<detail::BLayout::nk>(s.normed.data(), lw.wqkv.data(), nullptr, s.qkv.data(), n,
+                                                         qkvw, H, detail::IdentityEpilogue{}, st);
+            launch_async(st, llama::rope_split_kernel, detail::stream_grid(int64_t(n) * (qh + 2 * kvh) * (D / 2)),
+                         256, s.qkv.data(), w_.inv_freq.data(), s.q_heads.data(), layer_k(s, l), layer_v(s, l), n, qh,
+                         kvh, D, s.max_seq_len, 0);
+            ops::attention_prefill(s.q_heads.data(), layer_k(s, l), layer_v(s, l), s.attn_heads.data(), n, n, 0, qh,
+                                   cfg_.kv_rep(), D, s.max_seq_len, st);
+            launch_async(st, llama::merge_heads_kernel, detail::stream_grid(int64_t(n) * qh * D), 256,
+                         s.attn_heads.data(), s.attn.data(), n, qh, D);
+            detail::gemm_f32_launch<detail::BLayout::nk, detail::IdentityEpilogue, detail::GemmStore::residual>(
+                s.attn.data(), lw.wo.data(), nullptr, s.hidden.data(), n, H, qh * D, detail::IdentityEpilogue{}, st);
+            ops::rms_norm(s.hidden.data(), lw.post_norm.data(), s.normed.data(), n, H, cfg_.rms_norm_eps, st);
+            detail::gemm_f32_launch<detail::BLayout::nk, detail::IdentityEpilogue, detail::GemmStore::swiglu>(
+                s.normed.data(), lw.wgu.data(), nullptr, s.act.data(), n, 2 * I, H, detail::IdentityEpilogue{}, st);
+            detail::gemm_f32_launch<detail::BLayout::nk, detail::IdentityEpilogue, detail::GemmStore::residual>(
+                s.act.data(), lw.wdown.data(), nullptr, s.hidden.data(), n, H, I, detail::IdentityEpilogue{}, st);
+            if (hook)
+                hook(l);
+        }
+        dispatch_widths([&](auto v, auto) { enqueue_lm_head<decltype(v)::value>(s, s.hidden.data() + int64_t(n - 1) * H); });
+    }
+};
+
+} // namespace opworks

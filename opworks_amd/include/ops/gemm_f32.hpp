@@ -47,6 +47,13 @@ struct IdentityEpilogue {
     __device__ float operator()(float x) const { return x; }
 };
 
+// How the epilogue writes C (all modes apply epi(acc + bias[col]) first):
+//  store    C[row][col] = v
+//  residual C[row][col] += v                     (C holds the residual stream)
+//  swiglu   columns (2i, 2i+1) hold (gate_i, up_i): C[row][i] = silu(gate) * up,
+//           C is N/2 wide; silu(g) = g / (1 + expf(-g)).
+enum class GemmStore { store, residual, swiglu };
+
 // Maps the dispatch-order workgroup id to a (tile_m, tile_n) pair: a band of
 // consecutive tiles per XCD (dispatch is round-robin over XCDs), then
 // group-of-8-rows ordering inside the band.
@@ -72,7 +79,7 @@ template <BLayout kB, bool kVec> struct GemmF32Tiles {
     static constexpr int kStage = kA + kB_;
 };
 
-template <BLayout kB, bool kVec, typename Epi>
+template <BLayout kB, bool kVec, typename Epi, GemmStore kStore = GemmStore::store>
 __global__ __launch_bounds__(kGemmThreads) void gemm_f32_mfma_kernel(const float *__restrict__ A,
                                                                      const float *__restrict__ B,
                                                                      const float *__restrict__ bias,
@@ -211,8 +218,18 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f32_mfma_kernel(const float
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * 64 + bm * 32 + 8 * (r / 4) + 4 * half + (r % 4);
-                if (row < M && col < N)
-                    C[int64_t(row) * N + col] = epi(acc[bm][bn][r] + bv);
+                const float v = epi(acc[bm][bn][r] + bv);
+                if constexpr (kStore == GemmStore::swiglu) {
+                    const float partner = __shfl_xor(v, 1); // lane l ^ 1 holds column col ^ 1
+                    if ((l32 & 1) == 0 && row < M && col + 1 < N)
+                        C[int64_t(row) * (N / 2) + col / 2] = v / (1.f + expf(-v)) * partner;
+                } else if constexpr (kStore == GemmStore::residual) {
+                    if (row < M && col < N)
+                        C[int64_t(row) * N + col] += v;
+                } else {
+                    if (row < M && col < N)
+                        C[int64_t(row) * N + col] = v;
+                }
             }
         }
     }
@@ -223,15 +240,18 @@ inline bool gemm_vec_ok(const void *a, const void *b, int K, int N, BLayout layo
     return aligned && K % 4 == 0 && (layout == BLayout::nk || N % 4 == 0);
 }
 
-// Enqueues C[M][N] = epi(A[M][K] B + bias). K == 0 writes epi(bias or 0).
-template <BLayout kB, typename Epi>
+// Enqueues C[M][N] = epi(A[M][K] B + bias) (written per kStore). K == 0 writes epi(bias or 0).
+template <BLayout kB, typename Epi, GemmStore kStore = GemmStore::store>
 void gemm_f32_launch(const float *A, const float *B, const float *bias, float *C, int M, int N, int K, Epi epi,
                      hipStream_t stream) {
+    require(kStore != GemmStore::swiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
     const int tiles = static_cast<int>(blocks_for64(M, kGemmBM) * blocks_for64(N, kGemmBN));
     if (gemm_vec_ok(A, B, K, N, kB))
-        launch_async(stream, gemm_f32_mfma_kernel<kB, true, Epi>, tiles, kGemmThreads, A, B, bias, C, M, N, K, epi);
+        launch_async(stream, gemm_f32_mfma_kernel<kB, true, Epi, kStore>, tiles, kGemmThreads, A, B, bias, C, M, N, K,
+                     epi);
     else
-        launch_async(stream, gemm_f32_mfma_kernel<kB, false, Epi>, tiles, kGemmThreads, A, B, bias, C, M, N, K, epi);
+        launch_async(stream, gemm_f32_mfma_kernel<kB, false, Epi, kStore>, tiles, kGemmThreads, A, B, bias, C, M, N,
+                     K, epi);
 }
 
 } // namespace opworks::detail

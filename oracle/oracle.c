@@ -568,3 +568,267 @@ void orc_attention_decode(const float *q, const float *k, const float *v, float 
     free(scores);
     free(acc);
 }
+
+/* ------------------------------------------------------------ llama forward */
+/* linear_kernel (include/ops/linear.cuh:18-73) order for rows >= 2: every
+ * output is the k-ascending chain acc = fmaf(x, w, acc). Columns are processed
+ * in blocks of 64 with the weight block transposed into a private buffer. */
+struct lin_ctx {
+    const float *X, *W;
+    float *Y;
+    int rows, in, out;
+};
+#define LIN_BLOCK 64
+static void lin_range(void *p, int64_t lo, int64_t hi) {
+    struct lin_ctx *c = (struct lin_ctx *)p;
+    float *buf = (float *)malloc(sizeof(float) * (size_t)c->in * LIN_BLOCK);
+    float acc[LIN_BLOCK];
+    for (int64_t blk = lo; blk < hi; ++blk) {
+        const int o0 = (int)blk * LIN_BLOCK;
+        const int nb = c->out - o0 < LIN_BLOCK ? c->out - o0 : LIN_BLOCK;
+        for (int j = 0; j < LIN_BLOCK; ++j)
+            for (int n = 0; n < c->in; ++n)
+                buf[(int64_t)n * LIN_BLOCK + j] = j < nb ? c->W[(int64_t)(o0 + j) * c->in + n] : 0.f;
+        for (int r = 0; r < c->rows; ++r) {
+            const float *x = c->X + (int64_t)r * c->in;
+            for (int j = 0; j < LIN_BLOCK; ++j)
+                acc[j] = 0.f;
+            for (int n = 0; n < c->in; ++n) {
+                const float a = x[n];
+                const float *b = buf + (int64_t)n * LIN_BLOCK;
+                for (int j = 0; j < LIN_BLOCK; ++j)
+                    acc[j] = fmaf(a, b[j], acc[j]);
+            }
+            for (int j = 0; j < nb; ++j)
+                c->Y[(int64_t)r * c->out + o0 + j] = acc[j];
+        }
+    }
+    free(buf);
+}
+
+/* ops::linear (include/ops/linear.cuh:130-153): the GEMV order for one row,
+ * the tiled order otherwise. */
+void orc_linear(const float *X, const float *W, float *Y, int rows, int in, int out) {
+    if (rows == 1) {
+        orc_gemv(X, W, Y, in, out);
+        return;
+    }
+    struct lin_ctx c = {X, W, Y, rows, in, out};
+    parallel_for((out + LIN_BLOCK - 1) / LIN_BLOCK, lin_range, &c);
+}
+
+/* ModelConfig::rope_inv_freq (include/runtime/model_config.cuh:68-89): double
+ * arithmetic, with int/float and float-float subexpressions in float as there. */
+void orc_rope_inv_freq(int head_dim, float theta, int llama3, float factor, float low, float high, int orig,
+                       float *out) {
+    const double pi = 3.14159265358979323846;
+    for (int i = 0; i < head_dim / 2; ++i) {
+        double f = 1.0 / pow((double)theta, (2.0 * i) / head_dim);
+        if (llama3) {
+            const double wavelen = 2.0 * pi / f;
+            const double low_wl = (float)orig / low;
+            const double high_wl = (float)orig / high;
+            if (wavelen > low_wl) {
+                f /= factor;
+            } else if (wavelen >= high_wl) {
+                const double smooth = (orig / wavelen - low) / (double)(high - low);
+                f = (1.0 - smooth) * f / factor + smooth * f;
+            }
+        }
+        out[i] = (float)f;
+    }
+}
+
+/* rope_kernel (include/ops/rope.cuh:10-25): pair (i, i + D/2) at position p,
+ * freq = p * inv_freq[i] in float, c = cosf(freq), s = sinf(freq),
+ * lo = a*c - b*s, hi = b*c + a*s. The products are restated with the
+ * contraction lo = fmaf(a, c, -(b*s)), hi = fmaf(b, c, a*s). */
+void orc_rope(float *x, const float *inv_freq, int rows, int heads, int head_dim, int pos_start) {
+    const int half = head_dim / 2;
+    for (int r = 0; r < rows; ++r)
+        for (int h = 0; h < heads; ++h)
+            for (int i = 0; i < half; ++i) {
+                const float freq = (float)(pos_start + r) * inv_freq[i];
+                const float c = cosf(freq), s = sinf(freq);
+                float *p = x + (int64_t)r * heads * head_dim + h * head_dim + i;
+                const float a = p[0], b = p[half];
+                p[0] = fmaf(a, c, -(b * s));
+                p[half] = fmaf(b, c, a * s);
+            }
+}
+
+typedef struct {
+    int L, H, I, qh, kvh, D, V;
+    float eps;
+    float *embed, *final_norm, *inv_freq;
+    float **in_norm, **post_norm, **wq, **wk, **wv, **wo, **wg, **wu, **wd;
+    /* session */
+    int cap, length;
+    float *kc, *vc; /* [L][kvh][cap][D] */
+} orc_llama;
+
+static float *alloc_f(int64_t n) { return (float *)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1)); }
+
+static void fill_norm(float *dst, int64_t n, uint64_t seed, uint64_t stream, int uniform) {
+    if (uniform)
+        orc_fill_uniform(dst, n, seed, stream, 0.5f, 1.5f);
+    else
+        for (int64_t i = 0; i < n; ++i)
+            dst[i] = 1.f;
+}
+
+/* Seeded weights as the runtime's random init creates them (logical HF
+ * tensors; streams: embed 1, final norm 2, layer l base 64 + 16 l: q 0, k 1,
+ * v 2, o 3, gate 4, up 5, down 6, input norm 7, post norm 8). */
+void *orc_llama_create(int L, int H, int I, int qh, int kvh, int D, int V, float eps, float theta, int llama3,
+                       float factor, float low, float high, int orig, uint64_t seed, float sd, int norm_uniform) {
+    orc_llama *m = (orc_llama *)calloc(1, sizeof(orc_llama));
+    m->L = L, m->H = H, m->I = I, m->qh = qh, m->kvh = kvh, m->D = D, m->V = V, m->eps = eps;
+    m->embed = alloc_f((int64_t)V * H);
+    orc_fill_normal_mt(m->embed, (int64_t)V * H, seed, 1, 0.f, sd);
+    m->final_norm = alloc_f(H);
+    fill_norm(m->final_norm, H, seed, 2, norm_uniform);
+    m->inv_freq = alloc_f(D / 2);
+    orc_rope_inv_freq(D, theta, llama3, factor, low, high, orig, m->inv_freq);
+    float ***lists[] = {&m->in_norm, &m->post_norm, &m->wq, &m->wk, &m->wv, &m->wo, &m->wg, &m->wu, &m->wd};
+    for (int k = 0; k < 9; ++k)
+        *lists[k] = (float **)calloc((size_t)L, sizeof(float *));
+    const int64_t qw = (int64_t)qh * D, kw = (int64_t)kvh * D;
+    for (int l = 0; l < L; ++l) {
+        const uint64_t b = 64 + 16 * (uint64_t)l;
+        m->wq[l] = alloc_f(qw * H), orc_fill_normal_mt(m->wq[l], qw * H, seed, b + 0, 0.f, sd);
+        m->wk[l] = alloc_f(kw * H), orc_fill_normal_mt(m->wk[l], kw * H, seed, b + 1, 0.f, sd);
+        m->wv[l] = alloc_f(kw * H), orc_fill_normal_mt(m->wv[l], kw * H, seed, b + 2, 0.f, sd);
+        m->wo[l] = alloc_f((int64_t)H * qw), orc_fill_normal_mt(m->wo[l], (int64_t)H * qw, seed, b + 3, 0.f, sd);
+        m->wg[l] = alloc_f((int64_t)I * H), orc_fill_normal_mt(m->wg[l], (int64_t)I * H, seed, b + 4, 0.f, sd);
+        m->wu[l] = alloc_f((int64_t)I * H), orc_fill_normal_mt(m->wu[l], (int64_t)I * H, seed, b + 5, 0.f, sd);
+        m->wd[l] = alloc_f((int64_t)H * I), orc_fill_normal_mt(m->wd[l], (int64_t)H * I, seed, b + 6, 0.f, sd);
+        m->in_norm[l] = alloc_f(H), fill_norm(m->in_norm[l], H, seed, b + 7, norm_uniform);
+        m->post_norm[l] = alloc_f(H), fill_norm(m->post_norm[l], H, seed, b + 8, norm_uniform);
+    }
+    return m;
+}
+
+void orc_llama_destroy(void *p) {
+    orc_llama *m = (orc_llama *)p;
+    if (!m)
+        return;
+    for (int l = 0; l < m->L; ++l) {
+        free(m->wq[l]), free(m->wk[l]), free(m->wv[l]), free(m->wo[l]), free(m->wg[l]), free(m->wu[l]);
+        free(m->wd[l]), free(m->in_norm[l]), free(m->post_norm[l]);
+    }
+    free(m->wq), free(m->wk), free(m->wv), free(m->wo), free(m->wg), free(m->wu), free(m->wd);
+    free(m->in_norm), free(m->post_norm), free(m->embed), free(m->final_norm), free(m->inv_freq);
+    free(m->kc), free(m->vc);
+    free(m);
+}
+
+/* Raw weight access for tests that write packs: kind 0 embed, 1 final norm,
+ * per layer 2 q, 3 k, 4 v, 5 o, 6 gate, 7 up, 8 down, 9 input norm, 10 post norm. */
+const float *orc_llama_weight(void *p, int kind, int layer) {
+    orc_llama *m = (orc_llama *)p;
+    switch (kind) {
+    case 0: return m->embed;
+    case 1: return m->final_norm;
+    case 2: return m->wq[layer];
+    case 3: return m->wk[layer];
+    case 4: return m->wv[layer];
+    case 5: return m->wo[layer];
+    case 6: return m->wg[layer];
+    case 7: return m->wu[layer];
+    case 8: return m->wd[layer];
+    case 9: return m->in_norm[layer];
+    default: return m->post_norm[layer];
+    }
+}
+
+void orc_llama_reset(void *p, int cap) {
+    orc_llama *m = (orc_llama *)p;
+    free(m->kc), free(m->vc);
+    const int64_t n = (int64_t)m->L * m->kvh * cap * m->D;
+    m->kc = alloc_f(n), m->vc = alloc_f(n);
+    m->cap = cap;
+    m->length = 0;
+}
+
+/* argmax_kernel (include/ops/argmax.cuh:9-51): lowest index on ties, NaN never wins. */
+int orc_argmax(const float *x, int n) {
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = 0; i < n; ++i)
+        if (x[i] > best || (x[i] == best && i < bi))
+            best = x[i], bi = i;
+    return bi;
+}
+
+/* LlamaModelT::forward (include/models/llama.cuh:216-285) for `rows` tokens at
+ * positions [length, length + rows). logits (V floats) of the last row;
+ * captures (optional) receive hidden after the embedding and each layer. */
+static int llama_forward(orc_llama *m, const int *ids, int rows, float *logits, float *captures) {
+    const int H = m->H, I = m->I, D = m->D, qh = m->qh, kvh = m->kvh, rep = qh / kvh;
+    const int pos0 = m->length, S = pos0 + rows;
+    const int64_t qw = (int64_t)qh * D, kw = (int64_t)kvh * D;
+    float *hidden = alloc_f((int64_t)rows * H), *normed = alloc_f((int64_t)rows * H);
+    float *q = alloc_f(rows * qw), *k = alloc_f(rows * kw), *v = alloc_f(rows * kw);
+    float *attn = alloc_f(rows * qw), *gate = alloc_f((int64_t)rows * I), *up = alloc_f((int64_t)rows * I);
+    float *qheads = alloc_f(rows * qw), *aheads = alloc_f(rows * qw);
+    for (int r = 0; r < rows; ++r)
+        memcpy(hidden + (int64_t)r * H, m->embed + (int64_t)ids[r] * H, sizeof(float) * H);
+    if (captures)
+        memcpy(captures, hidden, sizeof(float) * rows * H);
+    for (int l = 0; l < m->L; ++l) {
+        float *kc = m->kc + (int64_t)l * kvh * m->cap * D, *vc = m->vc + (int64_t)l * kvh * m->cap * D;
+        orc_rms_norm_rows(hidden, m->in_norm[l], normed, rows, H, m->eps);
+        orc_linear(normed, m->wq[l], q, rows, H, (int)qw);
+        orc_linear(normed, m->wk[l], k, rows, H, (int)kw);
+        orc_linear(normed, m->wv[l], v, rows, H, (int)kw);
+        orc_rope(q, m->inv_freq, rows, qh, D, pos0);
+        orc_rope(k, m->inv_freq, rows, kvh, D, pos0);
+        for (int r = 0; r < rows; ++r) /* split_heads into the cache (include/ops/split_heads.cuh:9-18) */
+            for (int h = 0; h < kvh; ++h)
+                for (int d = 0; d < D; ++d) {
+                    kc[((int64_t)h * m->cap + pos0 + r) * D + d] = k[(int64_t)r * kw + h * D + d];
+                    vc[((int64_t)h * m->cap + pos0 + r) * D + d] = v[(int64_t)r * kw + h * D + d];
+                }
+        if (rows == 1) {
+            orc_attention_decode(q, kc, vc, attn, qh, rep, D, S, m->cap);
+        } else {
+            for (int r = 0; r < rows; ++r)
+                for (int h = 0; h < qh; ++h)
+                    memcpy(qheads + ((int64_t)h * rows + r) * D, q + (int64_t)r * qw + h * D, sizeof(float) * D);
+            orc_attention_explicit(qheads, kc, vc, aheads, NULL, rows, S, qh, rep, D, m->cap, NULL, 0);
+            for (int r = 0; r < rows; ++r)
+                for (int h = 0; h < qh; ++h)
+                    memcpy(attn + (int64_t)r * qw + h * D, aheads + ((int64_t)h * rows + r) * D, sizeof(float) * D);
+        }
+        orc_linear(attn, m->wo[l], normed, rows, (int)qw, H);
+        for (int64_t i = 0; i < (int64_t)rows * H; ++i) /* add_kernel */
+            hidden[i] = hidden[i] + normed[i];
+        orc_rms_norm_rows(hidden, m->post_norm[l], normed, rows, H, m->eps);
+        orc_linear(normed, m->wg[l], gate, rows, H, I);
+        orc_linear(normed, m->wu[l], up, rows, H, I);
+        for (int64_t i = 0; i < (int64_t)rows * I; ++i) { /* swiglu_kernel (include/ops/swiglu.cuh:7-12) */
+            const float g = gate[i];
+            gate[i] = g / (1.f + expf(-g)) * up[i];
+        }
+        orc_linear(gate, m->wd[l], normed, rows, I, H);
+        for (int64_t i = 0; i < (int64_t)rows * H; ++i)
+            hidden[i] = hidden[i] + normed[i];
+        if (captures)
+            memcpy(captures + (int64_t)(l + 1) * rows * H, hidden, sizeof(float) * rows * H);
+    }
+    orc_rms_norm_rows(hidden + (int64_t)(rows - 1) * H, m->final_norm, normed, 1, H, m->eps);
+    orc_gemv(normed, m->embed, logits, H, m->V);
+    m->length = S;
+    free(hidden), free(normed), free(q), free(k), free(v), free(attn), free(gate), free(up), free(qheads);
+    free(aheads);
+    return orc_argmax(logits, m->V);
+}
+
+int orc_llama_prefill(void *p, const int *ids, int n, float *logits, float *captures) {
+    orc_llama *m = (orc_llama *)p;
+    m->length = 0;
+    return llama_forward(m, ids, n, logits, captures);
+}
+
+int orc_llama_decode(void *p, int token, float *logits) { return llama_forward((orc_llama *)p, &token, 1, logits, NULL); }

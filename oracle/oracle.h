@@ -30,6 +30,13 @@
  *                        rows return v_0 exactly; uniform keys average V
  *  orc_attention_decode  equals the explicit path's last row (same maths,
  *                        other order) and the float64 reference
+ *  orc_linear            agrees with orc_mat_mul_rows (same chain) / orc_gemv
+ *  orc_rope_inv_freq     closed form without scaling; llama3 bands by hand;
+ *                        the reference's own model_config.cuh via oracle/_ref
+ *  orc_rope              position 0 is the identity; pair norms preserved
+ *  orc_argmax            brute force incl. ties, -inf and NaN
+ *  orc_llama_*           float64 numpy forward of a tiny model; KV-cache
+ *                        decode equals full recompute
  */
 #ifndef OPWORKS_ORACLE_H
 #define OPWORKS_ORACLE_H
@@ -83,6 +90,20 @@ void orc_attention_explicit(const float *q, const float *k, const float *v, floa
                             int qh, int kv_rep, int D, int cap, const int *rows, int nrows);
 void orc_attention_decode(const float *q, const float *k, const float *v, float *out, int qh, int kv_rep, int D,
                           int len, int max_seq);
+
+/* Llama forward (include/models/llama.cuh:216-285) on seeded random weights */
+void orc_linear(const float *X, const float *W, float *Y, int rows, int in, int out);
+void orc_rope_inv_freq(int head_dim, float theta, int llama3, float factor, float low, float high, int orig,
+                       float *out);
+void orc_rope(float *x, const float *inv_freq, int rows, int heads, int head_dim, int pos_start);
+int orc_argmax(const float *x, int n);
+void *orc_llama_create(int L, int H, int I, int qh, int kvh, int D, int V, float eps, float theta, int llama3,
+                       float factor, float low, float high, int orig, uint64_t seed, float sd, int norm_uniform);
+void orc_llama_destroy(void *m);
+const float *orc_llama_weight(void *m, int kind, int layer);
+void orc_llama_reset(void *m, int cap);
+int orc_llama_prefill(void *m, const int *ids, int n, float *logits, float *captures);
+int orc_llama_decode(void *m, int token, float *logits);
 
 #ifdef __cplusplus
 }

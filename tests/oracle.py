@@ -41,6 +41,17 @@ _SIGS = {
     "orc_attention_explicit": (None, [_F, _F, _F, _F, POINTER(c_double), c_int, c_int, c_int, c_int, c_int, c_int,
                                       POINTER(c_int), c_int]),
     "orc_attention_decode": (None, [_F, _F, _F, _F, c_int, c_int, c_int, c_int, c_int]),
+    "orc_linear": (None, [_F, _F, _F, c_int, c_int, c_int]),
+    "orc_rope_inv_freq": (None, [c_int, c_float, c_int, c_float, c_float, c_float, c_int, _F]),
+    "orc_rope": (None, [_F, _F, c_int, c_int, c_int, c_int]),
+    "orc_argmax": (c_int, [_F, c_int]),
+    "orc_llama_create": (c_void_p, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_float, c_int,
+                                    c_float, c_float, c_float, c_int, c_uint64, c_float, c_int]),
+    "orc_llama_destroy": (None, [c_void_p]),
+    "orc_llama_weight": (c_void_p, [c_void_p, c_int, c_int]),
+    "orc_llama_reset": (None, [c_void_p, c_int]),
+    "orc_llama_prefill": (c_int, [c_void_p, POINTER(c_int), c_int, _F, _F]),
+    "orc_llama_decode": (c_int, [c_void_p, c_int, _F]),
 }
 
 
@@ -199,3 +210,70 @@ def attention_decode(q, k, v, qh, kv_rep, D, length, max_seq):
     out = np.empty(qh * D, np.float32)
     lib().orc_attention_decode(fp(q), fp(k), fp(v), fp(out), qh, kv_rep, D, length, max_seq)
     return out.reshape(qh, D)
+
+
+def linear(X, W, rows, in_f, out_f):
+    X, W = f32(X), f32(W)
+    Y = np.empty(rows * out_f, np.float32)
+    lib().orc_linear(fp(X), fp(W), fp(Y), rows, in_f, out_f)
+    return Y.reshape(rows, out_f)
+
+
+def rope_inv_freq(head_dim, theta, llama3=False, factor=0.0, low=0.0, high=0.0, orig=0):
+    out = np.empty(head_dim // 2, np.float32)
+    lib().orc_rope_inv_freq(head_dim, theta, int(llama3), factor, low, high, orig, fp(out))
+    return out
+
+
+def rope(x, inv_freq, rows, heads, head_dim, pos_start):
+    x = f32(x).copy()
+    lib().orc_rope(fp(x), fp(f32(inv_freq)), rows, heads, head_dim, pos_start)
+    return x
+
+
+def argmax(x):
+    x = f32(x)
+    return lib().orc_argmax(fp(x), x.size)
+
+
+class Llama:
+    """The oracle's Llama forward on seeded weights (one session)."""
+
+    def __init__(self, cfg: dict, seed: int, sd: float = 0.02, norm_init: str = "ones") -> None:
+        rs = cfg.get("rope_scaling") or {}
+        self.cfg = cfg
+        self.V = cfg["vocab_size"]
+        self.L = cfg["num_hidden_layers"]
+        self.H = cfg["hidden_size"]
+        self.h = lib().orc_llama_create(
+            self.L, self.H, cfg["intermediate_size"], cfg["num_attention_heads"], cfg["num_key_value_heads"],
+            cfg.get("head_dim", self.H // cfg["num_attention_heads"]), self.V, cfg["rms_norm_eps"], cfg["rope_theta"],
+            int(bool(rs)), rs.get("factor", 0.0), rs.get("low_freq_factor", 0.0), rs.get("high_freq_factor", 0.0),
+            rs.get("original_max_position_embeddings", 0), seed, sd, 1 if norm_init == "uniform" else 0)
+
+    def weight(self, kind: int, layer: int, numel: int) -> np.ndarray:
+        p = lib().orc_llama_weight(self.h, kind, layer)
+        return np.ctypeslib.as_array(ctypes.cast(p, POINTER(c_float)), shape=(numel,)).copy()
+
+    def reset(self, cap: int) -> None:
+        lib().orc_llama_reset(self.h, cap)
+
+    def prefill(self, ids, capture: bool = False):
+        ids = np.ascontiguousarray(ids, np.int32)
+        logits = np.empty(self.V, np.float32)
+        caps = np.empty((self.L + 1) * ids.size * self.H, np.float32) if capture else None
+        tok = lib().orc_llama_prefill(self.h, ids.ctypes.data_as(POINTER(c_int)), ids.size, fp(logits),
+                                      fp(caps) if capture else None)
+        if capture:
+            return tok, logits, caps.reshape(self.L + 1, ids.size, self.H)
+        return tok, logits
+
+    def decode(self, token: int):
+        logits = np.empty(self.V, np.float32)
+        tok = lib().orc_llama_decode(self.h, token, fp(logits))
+        return tok, logits
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.orc_llama_destroy(self.h)
+            self.h = None

@@ -1,0 +1,152 @@
+"""Pins the oracle's Llama pieces (no GPU): RoPE frequencies, rotation, argmax
+rules, the tiled/GEMV linear orders, and a whole tiny model against an
+independent float64 numpy forward (textbook maths of
+scripts/llama/export_reference.py:32-88)."""
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+TINY = dict(num_hidden_layers=2, hidden_size=256, intermediate_size=1024, num_attention_heads=4,
+            num_key_value_heads=2, head_dim=64, vocab_size=512, rms_norm_eps=1e-5, rope_theta=500000.0,
+            rope_scaling={"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                          "original_max_position_embeddings": 64})
+
+
+def test_inv_freq_plain_closed_form(orc):
+    got = orc.rope_inv_freq(64, 500000.0)
+    want = np.array([1.0 / 500000.0 ** (2 * i / 64) for i in range(32)]).astype(np.float32)
+    assert np.array_equal(got, want)
+
+
+def test_inv_freq_llama3_bands(orc):
+    base = orc.rope_inv_freq(64, 500000.0).astype(np.float64)
+    got = orc.rope_inv_freq(64, 500000.0, True, 32.0, 1.0, 4.0, 8192).astype(np.float64)
+    wl = 2 * math.pi / base
+    hi_band = wl < 8192 / 4.0
+    lo_band = wl > 8192 / 1.0
+    assert np.array_equal(got[hi_band], base[hi_band].astype(np.float32))     # short wavelengths unchanged
+    assert np.allclose(got[lo_band], base[lo_band] / 32.0, rtol=1e-7)         # long wavelengths / factor
+    mid = ~hi_band & ~lo_band
+    assert mid.any() and np.all(got[mid] <= base[mid] * (1 + 1e-7)) and np.all(got[mid] >= base[mid] / 32 * (1 - 1e-7))
+    # the interpolation weight rises towards the short-wavelength end
+    frac = (got[mid] - base[mid] / 32) / (base[mid] - base[mid] / 32)
+    assert np.all(np.diff(frac) < 0)
+
+
+def test_inv_freq_matches_reference_build(orc):
+    lib = ROOT / "oracle" / "_ref" / "libref_host.so"
+    if not lib.exists():
+        pytest.skip("oracle/_ref not built (the reference sources are absent here)")
+    import ctypes
+    h = ctypes.CDLL(str(lib))
+    h.ref_rope_inv_freq.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_float), ctypes.c_int]
+    h.ref_rope_inv_freq.restype = ctypes.c_int
+    import json
+    for cfg in (TINY, dict(TINY, rope_theta=10000.0, rope_scaling=None),
+                dict(TINY, rope_scaling=dict(TINY["rope_scaling"], factor=8.0, original_max_position_embeddings=8192))):
+        out = np.empty(32, np.float32)
+        manifest = json.dumps({"config": cfg, "eos_token_ids": [1]})
+        assert h.ref_rope_inv_freq(manifest.encode(), out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), 32) == 0
+        rs = cfg.get("rope_scaling") or {}
+        mine = orc.rope_inv_freq(64, cfg["rope_theta"], bool(rs), rs.get("factor", 0.0), rs.get("low_freq_factor", 0.0),
+                                 rs.get("high_freq_factor", 0.0), rs.get("original_max_position_embeddings", 0))
+        assert np.array_equal(out, mine)
+
+
+def test_rope_invariants(orc):
+    inv = orc.rope_inv_freq(64, 500000.0)
+    x = orc.fill_normal(3 * 2 * 64, 21, 0, 0.0, 1.0)
+    y0 = orc.rope(x, inv, 3, 2, 64, 0)
+    # position 0 rotates by angle 0 in every pair
+    assert np.array_equal(y0.reshape(3, 2, 64)[0], x.reshape(3, 2, 64)[0])
+    y = orc.rope(x, inv, 3, 2, 64, 100).reshape(3, 2, 64).astype(np.float64)
+    xr = x.reshape(3, 2, 64).astype(np.float64)
+    norm_x = xr[..., :32] ** 2 + xr[..., 32:] ** 2
+    norm_y = y[..., :32] ** 2 + y[..., 32:] ** 2
+    assert np.allclose(norm_x, norm_y, rtol=1e-5)
+    # closed form of one pair: rotation by (pos * inv_freq) (HF rotate_half convention)
+    r, h, i = 1, 1, 3
+    ang = np.float32(101) * inv[i]
+    a, b = xr[r, h, i], xr[r, h, i + 32]
+    assert abs(y[r, h, i] - (a * math.cos(ang) - b * math.sin(ang))) < 1e-5
+    assert abs(y[r, h, i + 32] - (b * math.cos(ang) + a * math.sin(ang))) < 1e-5
+
+
+def test_argmax_rules(orc):
+    assert orc.argmax([1, 5, 5, 2]) == 1                       # ties -> lowest index
+    assert orc.argmax([np.nan, 1, np.nan, 3]) == 3             # NaN never wins
+    assert orc.argmax([np.nan, np.nan]) == 0x7FFFFFFF          # all NaN
+    assert orc.argmax([-np.inf, -np.inf]) == 0                 # all -inf: lowest index
+    x = orc.fill_normal(10000, 22, 0, 0.0, 1.0)
+    assert orc.argmax(x) == int(np.argmax(x))
+
+
+def test_linear_orders(orc):
+    X = orc.fill_normal(5 * 300, 23, 0, 0.0, 1.0)
+    W = orc.fill_normal(70 * 300, 23, 1, 0.0, 1.0)
+    Y = orc.linear(X, W, 5, 300, 70)
+    ref, _ = orc.mat_mul_rows(X, W, 5, 300, 70, b_transposed=True)
+    assert np.array_equal(Y, ref)  # the same k-ascending chain
+    y1 = orc.linear(X[:300], W, 1, 300, 70)
+    assert np.array_equal(y1[0], orc.gemv(X[:300], W, 300, 70))
+
+
+def _np_forward(model, cfg, ids):
+    """float64 textbook Llama forward (HF semantics) from the oracle's weights."""
+    H, I, V, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"], cfg["num_hidden_layers"]
+    qh, kvh = cfg["num_attention_heads"], cfg["num_key_value_heads"]
+    D = cfg["head_dim"]
+    eps = cfg["rms_norm_eps"]
+    rs = cfg.get("rope_scaling") or {}
+
+    from tests import oracle as orc
+    inv = orc.rope_inv_freq(D, cfg["rope_theta"], bool(rs), rs.get("factor", 0.0), rs.get("low_freq_factor", 0.0),
+                            rs.get("high_freq_factor", 0.0), rs.get("original_max_position_embeddings", 0))
+    w = lambda k, l, n: model.weight(k, l, n).astype(np.float64)
+    T = len(ids)
+    x = w(0, 0, V * H).reshape(V, H)[ids]
+
+    def rms(v, g):
+        return v / np.sqrt((v ** 2).mean(-1, keepdims=True) + eps) * g
+
+    pos = np.arange(T)[:, None] * inv.astype(np.float64)[None, :]
+    cos, sin = np.cos(pos), np.sin(pos)
+
+    def rope(t):  # t [T, heads, D]
+        a, b = t[..., :D // 2], t[..., D // 2:]
+        return np.concatenate([a * cos[:, None] - b * sin[:, None], b * cos[:, None] + a * sin[:, None]], -1)
+
+    for l in range(L):
+        h = rms(x, w(9, l, H))
+        q = rope((h @ w(2, l, qh * D * H).reshape(qh * D, H).T).reshape(T, qh, D))
+        k = rope((h @ w(3, l, kvh * D * H).reshape(kvh * D, H).T).reshape(T, kvh, D))
+        v = (h @ w(4, l, kvh * D * H).reshape(kvh * D, H).T).reshape(T, kvh, D)
+        out = np.zeros((T, qh, D))
+        for hh in range(qh):
+            s = q[:, hh] @ k[:, hh // (qh // kvh)].T / math.sqrt(D)
+            s = np.where(np.tri(T, dtype=bool), s, -np.inf)
+            p = np.exp(s - s.max(1, keepdims=True))
+            out[:, hh] = (p / p.sum(1, keepdims=True)) @ v[:, hh // (qh // kvh)]
+        x = x + out.reshape(T, qh * D) @ w(5, l, H * qh * D).reshape(H, qh * D).T
+        h = rms(x, w(10, l, H))
+        g = h @ w(6, l, I * H).reshape(I, H).T
+        u = h @ w(7, l, I * H).reshape(I, H).T
+        x = x + (g / (1 + np.exp(-g)) * u) @ w(8, l, H * I).reshape(H, I).T
+    return rms(x[-1], w(1, 0, H)) @ w(0, 0, V * H).reshape(V, H).T
+
+
+def test_tiny_model_vs_float64(orc):
+    m = orc.Llama(TINY, 31, norm_init="uniform")
+    m.reset(32)
+    ids = [5, 17, 300, 2, 99, 511, 0]
+    tok, logits = m.prefill(ids)
+    ref = _np_forward(m, TINY, ids)
+    nrmse = np.sqrt(np.mean((logits - ref) ** 2)) / np.sqrt(np.mean(ref ** 2))
+    assert nrmse < 1e-5 and tok == int(np.argmax(ref))
+    # KV-cache decode equals the full recompute of the longer prompt
+    tok2, logits2 = m.decode(tok)
+    ref2 = _np_forward(m, TINY, ids + [tok])
+    assert np.sqrt(np.mean((logits2 - ref2) ** 2)) / np.sqrt(np.mean(ref2 ** 2)) < 1e-5
