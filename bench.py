@@ -207,9 +207,59 @@ def wl_attention_decode(stream, steps, warmup):
             "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
 
 
+def wl_llama(stream, steps, warmup):
+    """Config 5: Llama-3.2-1B architecture, fp32 weights N(0, 0.02) (seeded), RMSNorm gamma = 1, 512
+    uniform-random prompt ids, greedy 256 tokens with the KV cache, no EOS stop. A step is one full
+    generation through the C ABI's greedy loop; value = 255 decode steps / decode wall time (median over
+    steps, after warmup). The roofline is the gate/up GEMV (the largest decode kernel, 134,225,920 B per
+    launch) timed with HIP events on the session stream."""
+    from opworks_amd.llama import LLAMA_3_2_1B, LlamaModel
+    cfg = dict(LLAMA_3_2_1B)
+    model = LlamaModel.load_random(cfg, SEED, 0.02, "ones")
+    sess = model.session(1024)
+    rng = np.random.default_rng(SEED)
+    prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], 512)]
+    new_tokens = 256
+    runs = []
+    for i in range(warmup + steps):
+        sess.reset()
+        toks, pre_ms, dec_ms = sess.generate_greedy(prompt, new_tokens)
+        if i >= warmup:
+            runs.append((pre_ms, dec_ms, toks))
+    dec = sorted(r[1] for r in runs)[len(runs) // 2]
+    pre = sorted(r[0] for r in runs)[len(runs) // 2]
+    tok_s = (new_tokens - 1) / (dec / 1e3)
+    # per-kernel profile of one more decode step at the end of the sequence
+    prof = sess.profile_decode_step(int(runs[-1][2][-1]))
+    H, I, V, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"], cfg["num_hidden_layers"]
+    qkv_w = (cfg["num_attention_heads"] + 2 * cfg["num_key_value_heads"]) * cfg["head_dim"]
+    kernel_bytes = {"qkv_rope": 4 * (qkv_w * H + 2 * H), "o_proj": 4 * (H * H + 3 * H),
+                    "gate_up": 4 * (2 * I * H + 2 * H + I), "down": 4 * (H * I + I + 2 * H),
+                    "lm_head": 4 * (V * H + 2 * H + V)}
+    breakdown = {}
+    for k, ms_list in prof.items():
+        avg = sum(ms_list) / len(ms_list)
+        entry = {"avg_us": round(avg * 1e3, 2), "total_us_per_token": round(sum(ms_list) * 1e3, 1)}
+        if k in kernel_bytes:
+            entry["gbs"] = round(kernel_bytes[k] / (avg * 1e-3) / 1e9, 1)
+        breakdown[k] = entry
+    gu_ms = sum(prof["gate_up"]) / L
+    gu_gbs = kernel_bytes["gate_up"] / (gu_ms * 1e-3) / 1e9
+    weight_bytes = 4 * (V * H + L * (qkv_w * H + H * H + 2 * I * H + H * I) + (2 * L + 1) * H)
+    kv_bytes_avg = 2 * L * cfg["num_key_value_heads"] * cfg["head_dim"] * 4 * (512 + new_tokens / 2)
+    step_gbs = (weight_bytes + kv_bytes_avg) / (dec / (new_tokens - 1) * 1e-3) / 1e9
+    return {"workload": "llama3.2-1b_fp32_greedy_prompt512_gen256", "unit": "tok/s", "value": tok_s,
+            "ms": pre + dec, "ttft_ms": round(pre, 3), "decode_ms_per_token": round(dec / (new_tokens - 1), 4),
+            "kernel": "swiglu_gemv_kernel<8> (gate/up)",
+            "roofline": roofline(gu_gbs, HBM_PEAK_GBS, "GB/s", "hbm"),
+            "decode_step_roofline": roofline(step_gbs, HBM_PEAK_GBS, "GB/s", "hbm"),
+            "weight_bytes_per_token": weight_bytes, "kernels": breakdown,
+            "first_tokens": [int(t) for t in runs[-1][2][:8]]}
+
+
 WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "gemm": wl_gemm, "gemm_bf16": wl_gemm_bf16, "attention": wl_attention,
-             "attention_decode": wl_attention_decode}
-HEADLINE = "map"
+             "attention_decode": wl_attention_decode, "llama": wl_llama}
+HEADLINE = "llama"
 
 
 # --------------------------------------------------------------- CPU baseline

@@ -61,6 +61,14 @@ int opw_llama_debug_prefill(void *session, const int32_t *tokens, int n, float *
 int opw_llama_generate_greedy(void *session, const int32_t *prompt, int n, int max_new, int32_t *out_tokens,
                               double *prefill_ms, double *decode_ms, char *err, int err_len);
 
+/* One decode step (appends prev_token like opw_llama_decode_step) launched
+ * eagerly with a HIP event before every kernel on the session stream;
+ * kernel_ms receives each kernel's duration in launch order (per layer:
+ * qkv+rope, attention, o_proj, gate/up, down; then the LM head). Returns the
+ * number of kernels (5 * layers + 1), -1 on error. */
+int opw_llama_profile_decode_step(void *session, int32_t prev_token, float *kernel_ms, int capacity, char *err,
+                                  int err_len);
+
 #ifdef __cplusplus
 }
 #endif

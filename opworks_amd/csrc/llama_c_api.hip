@@ -210,4 +210,19 @@ int opw_llama_generate_greedy(void *session, const int32_t *prompt, int n, int m
         err, err_len);
 }
 
+int opw_llama_profile_decode_step(void *session, int32_t prev_token, float *kernel_ms, int capacity, char *err,
+                                  int err_len) {
+    return guard(
+        [&] {
+            auto *s = as_session(session);
+            int32_t next = -1;
+            std::vector<float> ms = s->owner->model->profile_decode_step(*s->session, prev_token, &next);
+            if (!kernel_ms || capacity < static_cast<int>(ms.size()))
+                throw std::invalid_argument("kernel_ms needs 5 * layers + 1 entries");
+            std::memcpy(kernel_ms, ms.data(), ms.size() * sizeof(float));
+            return static_cast<int>(ms.size());
+        },
+        err, err_len);
+}
+
 } // extern "C"

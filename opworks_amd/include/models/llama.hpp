@@ -22,6 +22,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <memory>
@@ -101,7 +102,7 @@ struct LlamaSession {
     TypedDeviceBuffer<float> kcache, vcache;
     // decode step
     TypedDeviceBuffer<float> d_hidden, d_q, d_attn, d_act, logits, attn_partial, lm_best_val;
-    TypedDeviceBuffer<int32_t> lm_best_idx, argmax_out, counters, state_buf, ids;
+    TypedDeviceBuffer<int32_t> lm_best_idx, argmax_out, state_buf, ids;
     // prefill
     TypedDeviceBuffer<float> hidden, normed, qkv, q_heads, attn_heads, attn, act;
     int attn_max_chunks = 0;
@@ -185,7 +186,6 @@ class LlamaModel {
         s->lm_best_val = TypedDeviceBuffer<float>(s->lm_grid);
         s->lm_best_idx = TypedDeviceBuffer<int32_t>(s->lm_grid);
         s->argmax_out = TypedDeviceBuffer<int32_t>(1);
-        s->counters = TypedDeviceBuffer<int32_t>(kvh + 1); // [kvh] attention merges, [kvh] LM head
         s->state_buf = TypedDeviceBuffer<int32_t>(4);
         s->ids = TypedDeviceBuffer<int32_t>(T);
         s->hidden = TypedDeviceBuffer<float>(T * H);
@@ -195,7 +195,6 @@ class LlamaModel {
         s->attn_heads = TypedDeviceBuffer<float>(T * qh * D);
         s->attn = TypedDeviceBuffer<float>(T * qh * D);
         s->act = TypedDeviceBuffer<float>(T * I);
-        OPWORKS_HIP_CHECK(hipMemsetAsync(s->counters.data(), 0, sizeof(int32_t) * (kvh + 1), s->stream));
         OPWORKS_HIP_CHECK(hipMemsetAsync(s->state_buf.data(), 0, sizeof(int32_t) * 4, s->stream));
         OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&s->h_state), sizeof(llama::StepState)));
         OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&s->h_token), sizeof(int32_t)));
@@ -221,15 +220,56 @@ class LlamaModel {
         s.h_state->next = -1;
         OPWORKS_HIP_CHECK(hipMemcpyAsync(s.state(), s.h_state, sizeof(llama::StepState), hipMemcpyHostToDevice,
                                          s.stream));
-        if (!s.graph_exec)
-            capture_decode_graph(s);
-        OPWORKS_HIP_CHECK(hipGraphLaunch(s.graph_exec, s.stream));
+        launch_decode(s);
         OPWORKS_HIP_CHECK(hipMemcpyAsync(s.h_state, s.state(), sizeof(llama::StepState), hipMemcpyDeviceToHost,
                                          s.stream));
         synchronize(s.stream);
         s.length += 1;
         s.last_prefill_rows = 0;
         return s.h_state->next;
+    }
+
+    // One decode step launched eagerly with an event before every kernel and
+    // one after the last, all on the session stream; returns the kernel
+    // durations in launch order (per layer: qkv_rope, attention, o_proj,
+    // gate_up, down; then lm_head) and the next token in *next.
+    std::vector<float> profile_decode_step(Session &s, int32_t token, int32_t *next) {
+        if (token < 0 || token >= cfg_.vocab_size)
+            throw std::invalid_argument("token id outside the vocabulary");
+        if (s.length >= s.max_seq_len)
+            throw std::invalid_argument("session capacity exhausted");
+        s.h_state->token = token;
+        s.h_state->pos = s.length;
+        OPWORKS_HIP_CHECK(hipMemcpyAsync(s.state(), s.h_state, sizeof(llama::StepState), hipMemcpyHostToDevice,
+                                         s.stream));
+        std::vector<hipEvent_t> ev;
+        const std::function<void()> rec = [&] {
+            hipEvent_t e;
+            OPWORKS_HIP_CHECK(hipEventCreate(&e));
+            OPWORKS_HIP_CHECK(hipEventRecord(e, s.stream));
+            ev.push_back(e);
+        };
+        tick_ = &rec;
+        try {
+            enqueue_decode(s);
+        } catch (...) {
+            tick_ = nullptr;
+            throw;
+        }
+        tick_ = nullptr;
+        rec();
+        OPWORKS_HIP_CHECK(hipMemcpyAsync(s.h_state, s.state(), sizeof(llama::StepState), hipMemcpyDeviceToHost,
+                                         s.stream));
+        synchronize(s.stream);
+        std::vector<float> ms(ev.size() - 1);
+        for (size_t i = 0; i + 1 < ev.size(); ++i)
+            OPWORKS_HIP_CHECK(hipEventElapsedTime(&ms[i], ev[i], ev[i + 1]));
+        for (hipEvent_t e : ev)
+            (void)hipEventDestroy(e);
+        s.length += 1;
+        if (next)
+            *next = s.h_state->next;
+        return ms;
     }
 
     bool is_eos(int32_t token) const {
@@ -282,6 +322,12 @@ class LlamaModel {
 
     ModelConfig cfg_;
     LlamaWeights w_;
+    // When set (profiling only), called before every kernel of the decode step.
+    const std::function<void()> *tick_ = nullptr;
+    void tick() const {
+        if (tick_)
+            (*tick_)();
+    }
 
     void check_supported() const {
         const int H = cfg_.hidden_size, I = cfg_.intermediate_size;
@@ -440,6 +486,7 @@ class LlamaModel {
         qa.kvh = kvh;
         qa.D = D;
         qa.cap = s.max_seq_len;
+        tick();
         launch_async(st, llama::qkv_rope_kernel<kV>, detail::blocks_for64(qkv_waves, llama::kWavesPerBlock),
                      llama::kBlock, qa);
         llama::DecodeAttnArgs aa{};
@@ -448,21 +495,36 @@ class LlamaModel {
         aa.vcache = layer_v(s, l);
         aa.out = s.d_attn.data();
         aa.partial = s.attn_partial.data();
-        aa.counters = reinterpret_cast<unsigned *>(s.counters.data());
         aa.state = s.state();
         aa.kv_rep = cfg_.kv_rep();
         aa.D = D;
         aa.cap = s.max_seq_len;
         aa.max_chunks = s.attn_max_chunks;
         aa.scale = 1.f / std::sqrt(static_cast<float>(D));
-        launch_async(st, llama::decode_attention_kernel, dim3(kvh, s.attn_max_chunks), cfg_.kv_rep() * kWaveSize, aa);
+        tick();
+        const int rep = cfg_.kv_rep();
+        const dim3 agrid(kvh, s.attn_max_chunks);
+        if (rep <= 1)
+            launch_async(st, llama::decode_attention_kernel<1>, agrid, kWaveSize, aa);
+        else if (rep <= 2)
+            launch_async(st, llama::decode_attention_kernel<2>, agrid, 2 * kWaveSize, aa);
+        else if (rep <= 4)
+            launch_async(st, llama::decode_attention_kernel<4>, agrid, 4 * kWaveSize, aa);
+        else if (rep <= 8)
+            launch_async(st, llama::decode_attention_kernel<8>, agrid, 8 * kWaveSize, aa);
+        else
+            launch_async(st, llama::decode_attention_kernel<16>, agrid, 16 * kWaveSize, aa);
+        launch_async(st, llama::decode_combine_kernel, kvh, rep * kWaveSize, aa);
+        tick();
         launch_async(st, llama::gemv_residual_kernel<kV>,
                      detail::blocks_for64(detail::blocks_for64(H, llama::kRows), llama::kWavesPerBlock), llama::kBlock,
                      lw.wo.data(), s.d_attn.data(), s.d_hidden.data(), H);
+        tick();
         launch_async(st, llama::swiglu_gemv_kernel<kV>,
                      detail::blocks_for64(detail::blocks_for64(I, llama::kRows / 2), llama::kWavesPerBlock),
                      llama::kBlock, s.d_hidden.data(), lw.post_norm.data(), cfg_.rms_norm_eps, lw.wgu.data(),
                      s.d_act.data(), I);
+        tick();
         launch_async(st, llama::down_residual_kernel<kV2>, detail::blocks_for64(H, llama::kRows), llama::kBlock,
                      lw.wdown.data(), s.d_act.data(), s.d_hidden.data(), H);
     }
@@ -488,12 +550,12 @@ class LlamaModel {
         la.logits = s.logits.data();
         la.best_val = s.lm_best_val.data();
         la.best_idx = s.lm_best_idx.data();
-        la.counter = reinterpret_cast<unsigned *>(s.counters.data() + cfg_.num_kv_heads);
-        la.state = s.state();
-        la.argmax_out = s.argmax_out.data();
         la.eps = cfg_.rms_norm_eps;
         la.vocab = cfg_.vocab_size;
-        launch_async(s.stream, llama::lm_head_argmax_kernel<kV>, s.lm_grid, llama::kBlock, la);
+        tick();
+        launch_async(s.stream, llama::lm_head_kernel<kV>, s.lm_grid, llama::kBlock, la);
+        launch_async(s.stream, llama::argmax_records_kernel, 1, 1024, s.lm_best_val.data(), s.lm_best_idx.data(),
+                     s.lm_grid, s.state(), s.argmax_out.data());
     }
 
     template <typename F> void dispatch_widths(F &&f) const {
@@ -516,6 +578,27 @@ class LlamaModel {
         case 16: with_v2(detail::IntTag<16>{}); break;
         default: throw std::runtime_error("unsupported hidden_size");
         }
+    }
+
+    // Replays the session's decode graph (captured on first use). With
+    // OPWORKS_DECODE_GRAPH=0 in the environment the same kernels are enqueued
+    // one by one instead, for tools that do not follow graph launches.
+    static bool use_graph() {
+        static const bool on = [] {
+            const char *v = std::getenv("OPWORKS_DECODE_GRAPH");
+            return !(v && v[0] == '0');
+        }();
+        return on;
+    }
+
+    void launch_decode(Session &s) const {
+        if (!use_graph()) {
+            enqueue_decode(s);
+            return;
+        }
+        if (!s.graph_exec)
+            capture_decode_graph(s);
+        OPWORKS_HIP_CHECK(hipGraphLaunch(s.graph_exec, s.stream));
     }
 
     void capture_decode_graph(Session &s) const {
@@ -542,13 +625,10 @@ class LlamaModel {
             s.h_state->next = -1;
             OPWORKS_HIP_CHECK(hipMemcpyAsync(s.state(), s.h_state, sizeof(llama::StepState),
                                              hipMemcpyHostToDevice, s.stream));
-            if (hook) {
+            if (hook)
                 run_decode_layers_with_hook(s, hook);
-            } else {
-                if (!s.graph_exec)
-                    capture_decode_graph(s);
-                OPWORKS_HIP_CHECK(hipGraphLaunch(s.graph_exec, s.stream));
-            }
+            else
+                launch_decode(s);
         } else {
             OPWORKS_HIP_CHECK(hipMemcpyAsync(s.ids.data(), ids.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice,
                                              s.stream));

@@ -43,54 +43,87 @@ constexpr int kRows = 4;       // GEMV rows per wave
 constexpr int kBlock = 256;    // threads per GEMV workgroup
 constexpr int kWavesPerBlock = kBlock / kWaveSize;
 
-// x (H = 256 * kV floats) -> registers, optionally RMS-normalised with gamma:
-// xn = x * rsqrtf(mean(x^2) + eps) * gamma, same expression order as ops::rms_norm.
+// GEMV of a 4-wave workgroup: each wave owns kRows rows of a [*, H] matrix,
+// H = 256 * kV. The input vector is staged once per workgroup: its loads are
+// issued first, then every weight pack of the wave, so with in-order vmcnt
+// accounting the RMS statistics are computed while the weights stream in.
+// The (optionally RMS-normalised) vector goes to LDS and each wave reads its
+// kV packs from there. Waves with active == false still take part in the
+// barriers. xn = x * rsqrtf(mean(x^2) + eps) * gamma, ops::rms_norm's order.
 template <int kV>
-__device__ __forceinline__ void load_vector(const float *__restrict__ x, const float *__restrict__ gamma, float eps,
-                                            int lane, f32x4 (&xn)[kV]) {
+__device__ __forceinline__ void block_gemv(const float *__restrict__ x, const float *__restrict__ gamma, float eps,
+                                           const float *__restrict__ W, const int (&row)[kRows], bool active,
+                                           float *__restrict__ copy_x_to, float (&y)[kRows]) {
+    constexpr int H = 256 * kV;
+    constexpr int kPacks = H / 4;
+    constexpr int kX = (kPacks + kBlock - 1) / kBlock; // input packs per thread
+    __shared__ __attribute__((aligned(16))) float xs[H];
+    __shared__ float red[kWavesPerBlock];
+    const int tid = threadIdx.x, lane = tid % kWaveSize, wave = tid / kWaveSize;
     const f32x4 *x4 = reinterpret_cast<const f32x4 *>(x);
+    const f32x4 *g4 = reinterpret_cast<const f32x4 *>(gamma);
+    f32x4 xv[kX], gv[kX];
 #pragma unroll
-    for (int u = 0; u < kV; ++u)
-        xn[u] = x4[lane + kWaveSize * u];
+    for (int i = 0; i < kX; ++i) {
+        const int c = tid + kBlock * i;
+        if (c < kPacks) {
+            xv[i] = x4[c];
+            if (gamma)
+                gv[i] = g4[c];
+        }
+    }
+    f32x4 w[kRows][kV];
+    if (active) {
+#pragma unroll
+        for (int r = 0; r < kRows; ++r)
+#pragma unroll
+            for (int u = 0; u < kV; ++u)
+                w[r][u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(W + int64_t(row[r]) * H) + lane +
+                                                     kWaveSize * u);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float inv = 1.f;
     if (gamma) {
         float ss = 0.f;
 #pragma unroll
-        for (int u = 0; u < kV; ++u)
+        for (int i = 0; i < kX; ++i)
+            if (tid + kBlock * i < kPacks)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                ss = fmaf(xn[u][j], xn[u][j], ss);
-        const float inv = rsqrtf(wave::sum(ss) / (256 * kV) + eps);
-        const f32x4 *g4 = reinterpret_cast<const f32x4 *>(gamma);
+                for (int j = 0; j < 4; ++j)
+                    ss = fmaf(xv[i][j], xv[i][j], ss);
+        ss = wave::sum(ss);
+        if (lane == 0)
+            red[wave] = ss;
+        __syncthreads();
+        inv = rsqrtf(((red[0] + red[1]) + (red[2] + red[3])) / H + eps);
+    }
 #pragma unroll
-        for (int u = 0; u < kV; ++u) {
-            const f32x4 g = g4[lane + kWaveSize * u];
+    for (int i = 0; i < kX; ++i) {
+        const int c = tid + kBlock * i;
+        if (c < kPacks) {
+            if (copy_x_to)
+                reinterpret_cast<f32x4 *>(copy_x_to)[c] = xv[i];
+            f32x4 v = xv[i];
+            if (gamma)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                xn[u][j] = xn[u][j] * inv * g[j];
+                for (int j = 0; j < 4; ++j)
+                    v[j] = v[j] * inv * gv[i][j];
+            *reinterpret_cast<f32x4 *>(&xs[4 * c]) = v;
         }
     }
-}
-
-// y[r] = dot(W[row_r, :], xn) for kRows rows, wave-uniform results.
-template <int kV>
-__device__ __forceinline__ void gemv_rows(const float *__restrict__ W, const int (&row)[kRows], const f32x4 (&xn)[kV],
-                                          int lane, float (&y)[kRows]) {
-    constexpr int H = 256 * kV;
-    f32x4 w[kRows][kV];
-#pragma unroll
-    for (int r = 0; r < kRows; ++r)
-#pragma unroll
-        for (int u = 0; u < kV; ++u)
-            w[r][u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(W + int64_t(row[r]) * H) + lane +
-                                                 kWaveSize * u);
+    __syncthreads();
+    if (!active)
+        return;
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
         float acc = 0.f;
 #pragma unroll
-        for (int u = 0; u < kV; ++u)
+        for (int u = 0; u < kV; ++u) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(&xs[4 * (lane + kWaveSize * u)]);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                acc = fmaf(w[r][u][j], xn[u][j], acc);
+                acc = fmaf(w[r][u][j], v[j], acc);
+        }
         y[r] = wave::sum(acc);
     }
 }
@@ -121,26 +154,18 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(QkvArgs a) {
     const int w = blockIdx.x * kWavesPerBlock + threadIdx.x / kWaveSize;
     const int waves_per_head = a.D / 4;
     const int slot = w / waves_per_head;
-    if (slot >= a.qh + 2 * a.kvh)
-        return;
+    const bool active = slot < a.qh + 2 * a.kvh;
     const int pos = a.state->pos;
     const float *src = a.hidden_in ? a.hidden_in : a.embed + int64_t(a.state->token) * H;
-    f32x4 xn[kV];
-    if (!a.hidden_in && w == 0) { // layer 0: residual stream = embedding row
-        const f32x4 *s4 = reinterpret_cast<const f32x4 *>(src);
-        f32x4 *h4 = reinterpret_cast<f32x4 *>(a.hidden_out);
-#pragma unroll
-        for (int u = 0; u < kV; ++u)
-            h4[lane + kWaveSize * u] = s4[lane + kWaveSize * u];
-    }
-    load_vector<kV>(src, a.gamma, a.eps, lane, xn);
     const int half = a.D / 2;
     const int j = 2 * (w % waves_per_head);
-    const int base = slot * a.D;
+    const int base = (active ? slot : 0) * a.D;
     const int row[kRows] = {base + j, base + j + 1, base + j + half, base + j + 1 + half};
     float y[kRows];
-    gemv_rows<kV>(a.wqkv, row, xn, lane, y);
-    if (lane != 0)
+    // layer 0: workgroup 0 also writes the embedding row into the residual stream
+    block_gemv<kV>(src, a.gamma, a.eps, a.wqkv, row, active,
+                   (!a.hidden_in && blockIdx.x == 0) ? a.hidden_out : nullptr, y);
+    if (!active || lane != 0)
         return;
     if (slot < a.qh + a.kvh) { // rotate q and k: (lo, hi) = (a c - b s, b c + a s)
 #pragma unroll
@@ -165,26 +190,31 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(QkvArgs a) {
     dst[j + 1 + half] = y[3];
 }
 
-// ---- 2. decode attention with an in-kernel merge -----------------------------
-// grid (kvh, max_chunks), block kv_rep waves. Partial records [qh][max_chunks][D + 2]
-// (max, sum, unnormalised output); counters[kvh] start at zero and are
-// returned to zero by the merging workgroup.
+// ---- 2. decode attention: split-KV partials + combine ---------------------
+// Partial kernel: grid (kvh, max_chunks), block kWaves waves (kWaves = kv_rep
+// rounded up to a power of two; extra waves only stage K/V). Records
+// [qh][max_chunks][D + 2] hold (max, sum, unnormalised output) per chunk.
+// Combine kernel: one workgroup per kv head, one wave per q head.
 struct DecodeAttnArgs {
     const float *q;                  // [qh][D]
     const float *kcache, *vcache;    // [kvh][cap][D]
     float *out;                      // [qh][D]
     float *partial;                  // [qh][max_chunks][D + 2]
-    unsigned *counters;              // [kvh]
     const StepState *state;          // len = pos + 1
     int kv_rep, D, cap, max_chunks;
     float scale;
 };
 
-__global__ __launch_bounds__(16 * kWaveSize) static void decode_attention_kernel(DecodeAttnArgs a) {
-    constexpr int C = detail::kAttnChunk;
+__device__ __forceinline__ int decode_len(const DecodeAttnArgs &a) {
     int len = a.state->pos + 1;
     len = len < a.cap ? len : a.cap;
-    len = len < a.max_chunks * C ? len : a.max_chunks * C;
+    return len < a.max_chunks * detail::kAttnChunk ? len : a.max_chunks * detail::kAttnChunk;
+}
+
+template <int kWaves>
+__global__ __launch_bounds__(kWaves *kWaveSize) void decode_attention_kernel(DecodeAttnArgs a) {
+    constexpr int C = detail::kAttnChunk;
+    const int len = decode_len(a);
     const int nchunks = (len + C - 1) / C;
     const int kvh = blockIdx.x, chunk = blockIdx.y;
     if (chunk >= nchunks)
@@ -194,85 +224,116 @@ __global__ __launch_bounds__(16 * kWaveSize) static void decode_attention_kernel
     const int D = a.D;
     __shared__ __attribute__((aligned(16))) float Ks[C][64 + 4];
     __shared__ __attribute__((aligned(16))) float Vs[C][64];
-    __shared__ __attribute__((aligned(16))) float Qs[16][64];
-    __shared__ float Ps[16][C];
-    __shared__ bool merge;
+    __shared__ __attribute__((aligned(16))) float Qs[kWaves][64];
+    __shared__ __attribute__((aligned(16))) float Ps[kWaves][C];
     const float *kh = a.kcache + (int64_t(kvh) * a.cap + k0) * D;
     const float *vh = a.vcache + (int64_t(kvh) * a.cap + k0) * D;
-    for (int i = threadIdx.x; i < C * D; i += blockDim.x) {
-        const int r = i / D, d = i % D;
-        Ks[r][d] = r < n ? kh[i] : 0.f;
-        Vs[r][d] = r < n ? vh[i] : 0.f;
-    }
     const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
-    const int h = kvh * a.kv_rep + wave;
+    const bool head_ok = wave < a.kv_rep;
+    const int h = kvh * a.kv_rep + (head_ok ? wave : 0);
+    {
+        // 16-byte chunks of the K/V rows; every load of the thread is issued before the LDS stores
+        constexpr int kMaxPer = C * 64 / 4 / (kWaves * kWaveSize);
+        constexpr int nthreads = kWaves * kWaveSize;
+        const int chunks = C * D / 4;
+        f32x4 kv[kMaxPer], vv[kMaxPer];
+#pragma unroll
+        for (int i = 0; i < kMaxPer; ++i) {
+            const int c = threadIdx.x + i * nthreads;
+            const int r = (4 * c) / D;
+            kv[i] = vv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (c < chunks && r < n) {
+                kv[i] = reinterpret_cast<const f32x4 *>(kh)[c];
+                vv[i] = reinterpret_cast<const f32x4 *>(vh)[c];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kMaxPer; ++i) {
+            const int c = threadIdx.x + i * nthreads;
+            if (c < chunks) {
+                const int r = (4 * c) / D, d = (4 * c) % D;
+                *reinterpret_cast<f32x4 *>(&Ks[r][d]) = kv[i];
+                *reinterpret_cast<f32x4 *>(&Vs[r][d]) = vv[i];
+            }
+        }
+    }
     if (lane < D)
         Qs[wave][lane] = a.q[int64_t(h) * D + lane];
     __syncthreads();
-    // lane = key
-    float s = 0.f;
+    // lane = key; four partial dot products break the FMA chain
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
     for (int d = 0; d < D; d += 4) {
         const f32x4 kv = *reinterpret_cast<const f32x4 *>(&Ks[lane][d]);
         const f32x4 qv = *reinterpret_cast<const f32x4 *>(&Qs[wave][d]);
-        s = fmaf(qv[0], kv[0], s);
-        s = fmaf(qv[1], kv[1], s);
-        s = fmaf(qv[2], kv[2], s);
-        s = fmaf(qv[3], kv[3], s);
+        s0 = fmaf(qv[0], kv[0], s0);
+        s1 = fmaf(qv[1], kv[1], s1);
+        s2 = fmaf(qv[2], kv[2], s2);
+        s3 = fmaf(qv[3], kv[3], s3);
     }
-    s = lane < n ? s * a.scale : kNegInf;
+    const float s = lane < n ? ((s0 + s1) + (s2 + s3)) * a.scale : kNegInf;
     const float m = wave::max(s);
     const float p = lane < n ? expf(s - m) : 0.f;
     const float l = wave::sum(p);
     Ps[wave][lane] = p;
     __builtin_amdgcn_wave_barrier();
-    // lane = head-dim element
-    float o = 0.f;
+    // lane = head-dim element; keys past n have p = 0 and zero V rows
     if (lane < D) {
-        for (int key = 0; key < n; ++key)
-            o = fmaf(Ps[wave][key], Vs[key][lane], o);
-    }
-    float *rec = a.partial + (int64_t(h) * a.max_chunks + chunk) * (D + 2);
-    if (lane == 0) {
-        rec[0] = m;
-        rec[1] = l;
-    }
-    if (lane < D)
-        rec[2 + lane] = o;
-    // last workgroup of this kv head merges the chunks
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0)
-        merge = atomicAdd(&a.counters[kvh], 1u) == static_cast<unsigned>(nchunks - 1);
-    __syncthreads();
-    if (!merge)
-        return;
-    __threadfence();
-    const float *base = a.partial + int64_t(h) * a.max_chunks * (D + 2);
-    float M = kNegInf;
-    for (int c = lane; c < nchunks; c += kWaveSize)
-        M = fmaxf(M, __hip_atomic_load(base + int64_t(c) * (D + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    M = wave::max(M);
-    float L = 0.f;
-    for (int c = lane; c < nchunks; c += kWaveSize) {
-        const float mc = __hip_atomic_load(base + int64_t(c) * (D + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const float lc = __hip_atomic_load(base + int64_t(c) * (D + 2) + 1, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-        L = fmaf(lc, expf(mc - M), L);
-    }
-    L = wave::sum(L);
-    float acc = 0.f;
-    if (lane < D) {
-        for (int c = 0; c < nchunks; ++c) {
-            const float mc = __hip_atomic_load(base + int64_t(c) * (D + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const float oc = __hip_atomic_load(base + int64_t(c) * (D + 2) + 2 + lane, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-            acc = fmaf(oc, expf(mc - M), acc);
+        float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+#pragma unroll 4
+        for (int key = 0; key < C; key += 4) {
+            const f32x4 pv = *reinterpret_cast<const f32x4 *>(&Ps[wave][key]);
+            o0 = fmaf(pv[0], Vs[key][lane], o0);
+            o1 = fmaf(pv[1], Vs[key + 1][lane], o1);
+            o2 = fmaf(pv[2], Vs[key + 2][lane], o2);
+            o3 = fmaf(pv[3], Vs[key + 3][lane], o3);
         }
-        a.out[int64_t(h) * D + lane] = L > 0.f ? acc / L : 0.f;
+        if (head_ok) {
+            float *rec = a.partial + (int64_t(h) * a.max_chunks + chunk) * (D + 2);
+            if (lane == 0) {
+                rec[0] = m;
+                rec[1] = l;
+            }
+            rec[2 + lane] = (o0 + o1) + (o2 + o3);
+        }
     }
-    __syncthreads();
-    if (threadIdx.x == 0)
-        a.counters[kvh] = 0u;
+}
+
+// grid kvh, block kv_rep waves; wave w merges q head kvh * kv_rep + w.
+__global__ __launch_bounds__(16 * kWaveSize) static void decode_combine_kernel(DecodeAttnArgs a) {
+    constexpr int C = detail::kAttnChunk;
+    const int len = decode_len(a);
+    const int nchunks = (len + C - 1) / C; // <= max_chunks <= 128
+    const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
+    const int h = blockIdx.x * a.kv_rep + wave;
+    const int D = a.D;
+    const float *base = a.partial + int64_t(h) * a.max_chunks * (D + 2);
+    float m0 = kNegInf, l0 = 0.f, m1 = kNegInf, l1 = 0.f;
+    if (lane < nchunks) {
+        m0 = base[int64_t(lane) * (D + 2)];
+        l0 = base[int64_t(lane) * (D + 2) + 1];
+    }
+    if (lane + kWaveSize < nchunks) {
+        m1 = base[int64_t(lane + kWaveSize) * (D + 2)];
+        l1 = base[int64_t(lane + kWaveSize) * (D + 2) + 1];
+    }
+    const float M = wave::max(fmaxf(m0, m1));
+    const float w0 = lane < nchunks ? expf(m0 - M) : 0.f;
+    const float w1 = lane + kWaveSize < nchunks ? expf(m1 - M) : 0.f;
+    const float L = wave::sum(l0 * w0 + l1 * w1);
+    if (lane >= D)
+        return;
+    float acc0 = 0.f, acc1 = 0.f;
+    int c = 0;
+    for (; c + 1 < nchunks; c += 2) {
+        const float wa = wave::readlane(c < kWaveSize ? w0 : w1, c % kWaveSize);
+        const float wb = wave::readlane(c + 1 < kWaveSize ? w0 : w1, (c + 1) % kWaveSize);
+        acc0 = fmaf(base[int64_t(c) * (D + 2) + 2 + lane], wa, acc0);
+        acc1 = fmaf(base[int64_t(c + 1) * (D + 2) + 2 + lane], wb, acc1);
+    }
+    if (c < nchunks)
+        acc0 = fmaf(base[int64_t(c) * (D + 2) + 2 + lane], wave::readlane(c < kWaveSize ? w0 : w1, c % kWaveSize),
+                    acc0);
+    a.out[int64_t(h) * D + lane] = L > 0.f ? (acc0 + acc1) / L : 0.f;
 }
 
 // ---- 3. hidden += W x (in = H) -----------------------------------------------
@@ -283,17 +344,13 @@ __global__ __launch_bounds__(kBlock) void gemv_residual_kernel(const float *__re
     const int lane = threadIdx.x % kWaveSize;
     const int w = blockIdx.x * kWavesPerBlock + threadIdx.x / kWaveSize;
     const int r0 = w * kRows;
-    if (r0 >= out)
-        return;
-    f32x4 xv[kV];
-    load_vector<kV>(x, nullptr, 0.f, lane, xv);
     int row[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; ++r)
-        row[r] = r0 + r < out ? r0 + r : r0;
+        row[r] = r0 + r < out ? r0 + r : 0;
     float y[kRows];
-    gemv_rows<kV>(W, row, xv, lane, y);
-    if (lane == 0) {
+    block_gemv<kV>(x, nullptr, 0.f, W, row, r0 < out, nullptr, y);
+    if (r0 < out && lane == 0) {
 #pragma unroll
         for (int r = 0; r < kRows; ++r)
             if (r0 + r < out)
@@ -310,14 +367,12 @@ __global__ __launch_bounds__(kBlock) void swiglu_gemv_kernel(const float *__rest
     const int lane = threadIdx.x % kWaveSize;
     const int w = blockIdx.x * kWavesPerBlock + threadIdx.x / kWaveSize;
     const int i0 = w * (kRows / 2); // two (gate, up) pairs per wave
-    if (i0 >= inter)
-        return;
-    f32x4 xn[kV];
-    load_vector<kV>(hidden, gamma, eps, lane, xn);
-    const int row[kRows] = {2 * i0, 2 * i0 + 1, 2 * i0 + 2, 2 * i0 + 3};
+    const bool active = i0 < inter;
+    const int b = active ? i0 : 0;
+    const int row[kRows] = {2 * b, 2 * b + 1, 2 * b + 2, 2 * b + 3};
     float y[kRows];
-    gemv_rows<kV>(wgu, row, xn, lane, y);
-    if (lane == 0) {
+    block_gemv<kV>(hidden, gamma, eps, wgu, row, active, nullptr, y);
+    if (active && lane == 0) {
         act[i0] = y[0] / (1.f + expf(-y[0])) * y[1];
         act[i0 + 1] = y[2] / (1.f + expf(-y[2])) * y[3];
     }
@@ -348,6 +403,7 @@ __global__ __launch_bounds__(kBlock) void down_residual_kernel(const float *__re
         for (int u = 0; u < kV2; ++u)
             wv[r][u] = __builtin_nontemporal_load(w4 + lane + kWaveSize * u);
     }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
         float acc = 0.f;
@@ -398,31 +454,25 @@ struct LmHeadArgs {
     float *logits;           // [V]
     float *best_val;         // [grid]
     int *best_idx;           // [grid]
-    unsigned *counter;       // zero-initialised, reset by the last workgroup
-    StepState *state;        // next <- argmax
-    int *argmax_out;         // [1]
     float eps;
     int vocab;
 };
 
 template <int kV>
-__global__ __launch_bounds__(kBlock) void lm_head_argmax_kernel(LmHeadArgs a) {
+__global__ __launch_bounds__(kBlock) void lm_head_kernel(LmHeadArgs a) {
     __shared__ float sv[kWavesPerBlock];
     __shared__ int si[kWavesPerBlock];
-    __shared__ bool last;
     const int lane = threadIdx.x % kWaveSize, wave = threadIdx.x / kWaveSize;
     const int r0 = (blockIdx.x * kWavesPerBlock + wave) * kRows;
+    int row[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r)
+        row[r] = r0 + r < a.vocab ? r0 + r : 0;
+    float y[kRows];
+    block_gemv<kV>(a.hidden_row, a.gamma, a.eps, a.embed, row, r0 < a.vocab, nullptr, y);
     float bv = kNegInf;
     int bi = 0x7fffffff;
     if (r0 < a.vocab) {
-        f32x4 xn[kV];
-        load_vector<kV>(a.hidden_row, a.gamma, a.eps, lane, xn);
-        int row[kRows];
-#pragma unroll
-        for (int r = 0; r < kRows; ++r)
-            row[r] = r0 + r < a.vocab ? r0 + r : r0;
-        float y[kRows];
-        gemv_rows<kV>(a.embed, row, xn, lane, y);
 #pragma unroll
         for (int r = 0; r < kRows; ++r) {
             if (r0 + r < a.vocab) {
@@ -442,18 +492,32 @@ __global__ __launch_bounds__(kBlock) void lm_head_argmax_kernel(LmHeadArgs a) {
             argmax_merge(bv, bi, sv[k], si[k]);
         a.best_val[blockIdx.x] = bv;
         a.best_idx[blockIdx.x] = bi;
-        __threadfence();
-        last = atomicAdd(a.counter, 1u) == gridDim.x - 1;
     }
-    __syncthreads();
-    if (!last)
-        return;
-    __threadfence();
-    bv = kNegInf;
-    bi = 0x7fffffff;
-    for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += blockDim.x)
-        argmax_merge(bv, bi, __hip_atomic_load(a.best_val + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                     __hip_atomic_load(a.best_idx + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// One workgroup of 1024 threads reduces the per-workgroup records.
+__global__ __launch_bounds__(1024) static void argmax_records_kernel(const float *__restrict__ best_val,
+                                                                     const int *__restrict__ best_idx, int count,
+                                                                     StepState *state, int *argmax_out) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int lane = threadIdx.x % kWaveSize, wave = threadIdx.x / kWaveSize;
+    float bv = kNegInf;
+    int bi = 0x7fffffff;
+    constexpr int kBatch = 8;
+    for (int base = threadIdx.x; base < count; base += kBatch * 1024) {
+        float v[kBatch];
+        int ix[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int b = base + u * 1024;
+            v[u] = b < count ? best_val[b] : kNegInf;
+            ix[u] = b < count ? best_idx[b] : 0x7fffffff;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+            argmax_merge(bv, bi, v[u], ix[u]);
+    }
     wave_argmax(bv, bi);
     if (lane == 0) {
         sv[wave] = bv;
@@ -461,11 +525,10 @@ __global__ __launch_bounds__(kBlock) void lm_head_argmax_kernel(LmHeadArgs a) {
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int k = 0; k < kWavesPerBlock; ++k)
+        for (int k = 0; k < static_cast<int>(blockDim.x) / kWaveSize; ++k)
             argmax_merge(bv, bi, sv[k], si[k]);
-        a.argmax_out[0] = bi;
-        a.state->next = bi;
-        *a.counter = 0u;
+        argmax_out[0] = bi;
+        state->next = bi;
     }
 }
 

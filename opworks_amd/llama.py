@@ -32,6 +32,7 @@ for _name, _res, _args in [
     ("opw_llama_model_config", c_int, [c_void_p, POINTER(c_int), c_char_p, c_int]),
     ("opw_llama_debug_prefill", c_int, [c_void_p, POINTER(c_int32), c_int, POINTER(c_float), c_int64, c_char_p,
                                         c_int]),
+    ("opw_llama_profile_decode_step", c_int, [c_void_p, c_int32, POINTER(c_float), c_int, c_char_p, c_int]),
     ("opw_llama_generate_greedy", c_int, [c_void_p, POINTER(c_int32), c_int, c_int, POINTER(c_int32),
                                           POINTER(c_double), POINTER(c_double), c_char_p, c_int]),
 ]:
@@ -145,6 +146,19 @@ class LlamaSession:
                                                     out.ctypes.data_as(POINTER(c_int32)), ctypes.byref(pre),
                                                     ctypes.byref(dec), self._err, _ERR_LEN))
         return out, pre.value, dec.value
+
+    KERNELS_PER_LAYER = ("qkv_rope", "attention", "o_proj", "gate_up", "down")
+
+    def profile_decode_step(self, prev_token: int):
+        """Returns ({kernel name: [ms per layer]} + {"lm_head": [ms]}) for one eager decode step."""
+        m = self.model
+        n = 5 * m.num_layers + 1
+        ms = np.empty(n, np.float32)
+        self._check(lib().opw_llama_profile_decode_step(self.handle, prev_token, ms.ctypes.data_as(POINTER(c_float)),
+                                                        n, self._err, _ERR_LEN))
+        out = {k: [float(ms[5 * l + i]) for l in range(m.num_layers)] for i, k in enumerate(self.KERNELS_PER_LAYER)}
+        out["lm_head"] = [float(ms[-1])]
+        return out
 
     def close(self) -> None:
         if self.handle:
