@@ -43,7 +43,10 @@ HIP_FLAGS = [
 
 LIB_SOURCES = sorted(CSRC.glob("*.hip"))
 ADAPTER_SOURCES = sorted((CSRC / "adapters").glob("*.hip"))
-TEST_SOURCES = sorted((CSRC / "tests").glob("*.hip"))
+# One executable per top-level .hip file or per subdirectory (all its .hip files).
+TEST_SOURCES = sorted((CSRC / "tests").glob("*.hip")) + sorted(
+    d for d in (CSRC / "tests").glob("*") if d.is_dir() and any(d.glob("*.hip"))
+)
 
 
 def _run(cmd: list[str], cwd: Path | None = None) -> None:
@@ -92,7 +95,8 @@ def build_tests(jobs: int) -> list[Path]:
 
     def one(src: Path) -> Path:
         exe = out_dir / src.stem
-        _run([HIPCC, *HIP_FLAGS, "-o", str(exe), str(src)])
+        files = sorted(src.glob("*.hip")) if src.is_dir() else [src]
+        _run([HIPCC, *HIP_FLAGS, "-o", str(exe), *map(str, files)])
         return exe
 
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:

@@ -1,12 +1,14 @@
 #pragma once
 
-// MatmulBuilder — validated GEMM configuration (reference:
-// include/builders/matmul.cuh:7-57). Same fluent surface: transpose_a/b,
-// bias, activation and the apply(fn) callback. In addition run(stream)
-// launches the fused MFMA kernel: C = act(A @ op(B) + bias), with the bias and
-// activation applied in the kernel's epilogue (the reference has no kernel
-// behind this builder). Shapes use the reference's names: A is m x n, B is
-// n x k (k x n when transposed), output m x k.
+// MatmulBuilder — a checked GEMM description with the reference's fluent
+// surface (interface: include/builders/matmul.cuh:7-57: transpose_a/b, bias,
+// activation, accessors, apply(fn)). run() is an addition: it launches the
+// fused MFMA kernel, output = act(a @ op(b) + bias), with bias and activation
+// applied in the kernel's epilogue. Shapes keep the reference's names: a is
+// m x n, b is n x k (k x n when transposed), the output m x k.
+
+#include <initializer_list>
+#include <utility>
 
 #include "../ops/matmul.hpp"
 #include "builder_common.hpp"
@@ -15,62 +17,55 @@ namespace opworks {
 
 enum class MatmulActivation { none, relu, gelu };
 
-class MatmulBuilder {
+class MatmulBuilder : public detail::CallbackBuilder<MatmulBuilder> {
   public:
     MatmulBuilder(DeviceSpan<const float> a, DeviceSpan<const float> b, DeviceSpan<float> output, int m, int n, int k,
                   hipStream_t stream = nullptr)
-        : a_(a), b_(b), output_(output), m_(m), n_(n), k_(k), stream_(stream) {
-        detail::validate_matrix(m, n);
-        detail::validate_matrix(n, k);
-        detail::validate_matrix(m, k);
-        detail::require(a.size() >= m * n && b.size() >= n * k && output.size() >= m * k,
-                        "matmul buffer is too small");
+        : lhs_(a), rhs_(b), out_(output), dims_{m, n, k}, stream_(stream) {
+        for (auto [r, c] : {std::pair{m, n}, std::pair{n, k}, std::pair{m, k}})
+            detail::validate_matrix(r, c);
+        const bool fits = lhs_.size() >= int64_t(m) * n && rhs_.size() >= int64_t(n) * k &&
+                          out_.size() >= int64_t(m) * k;
+        detail::require(fits, "matmul buffer is too small");
     }
-    MatmulBuilder &transpose_a(bool value = true) {
-        transpose_a_ = value;
-        return *this;
-    }
-    MatmulBuilder &transpose_b(bool value = true) {
-        transpose_b_ = value;
-        return *this;
-    }
-    MatmulBuilder &bias(DeviceSpan<const float> value) {
-        bias_ = value;
-        return *this;
-    }
-    MatmulBuilder &activation(MatmulActivation value) {
-        activation_ = value;
-        return *this;
-    }
-    bool transposed_a() const { return transpose_a_; }
-    bool transposed_b() const { return transpose_b_; }
-    DeviceSpan<const float> a() const { return a_; }
-    DeviceSpan<const float> b() const { return b_; }
-    DeviceSpan<float> output() const { return output_; }
+
+    MatmulBuilder &transpose_a(bool value = true) { return flags_.ta = value, *this; }
+    MatmulBuilder &transpose_b(bool value = true) { return flags_.tb = value, *this; }
+    MatmulBuilder &bias(DeviceSpan<const float> value) { return bias_ = value, *this; }
+    MatmulBuilder &activation(MatmulActivation value) { return flags_.act = value, *this; }
+
+    bool transposed_a() const { return flags_.ta; }
+    bool transposed_b() const { return flags_.tb; }
+    DeviceSpan<const float> a() const { return lhs_; }
+    DeviceSpan<const float> b() const { return rhs_; }
+    DeviceSpan<float> output() const { return out_; }
     DeviceSpan<const float> bias() const { return bias_; }
-    MatmulActivation activation() const { return activation_; }
-    int m() const { return m_; }
-    int n() const { return n_; }
-    int k() const { return k_; }
+    MatmulActivation activation() const { return flags_.act; }
+    int m() const { return dims_[0]; }
+    int n() const { return dims_[1]; }
+    int k() const { return dims_[2]; }
     hipStream_t stream() const { return stream_; }
 
-    template <typename Fn> decltype(auto) apply(Fn &&fn) const { return apply_builder(*this, static_cast<Fn &&>(fn)); }
-
-    // Launches output = act(a @ op(b) + bias) on the builder's stream.
     void run() const {
-        detail::require(!transpose_a_, "MatmulBuilder::run: transpose_a is not supported by the fused kernel");
-        detail::require(bias_.size() == 0 || bias_.size() >= k_, "matmul bias is shorter than the output width");
-        ops::mat_mul_fused(a_.data(), b_.data(), bias_.size() ? bias_.data() : nullptr, output_.data(), m_, n_, k_,
-                           transpose_b_, static_cast<ops::Activation>(static_cast<int>(activation_)), stream_);
+        detail::require(!flags_.ta, "MatmulBuilder::run: transpose_a is not supported by the fused kernel");
+        detail::require(bias_.size() == 0 || bias_.size() >= k(), "matmul bias is shorter than the output width");
+        const auto act = flags_.act == MatmulActivation::relu   ? ops::Activation::relu
+                         : flags_.act == MatmulActivation::gelu ? ops::Activation::gelu
+                                                                : ops::Activation::none;
+        ops::mat_mul_fused(lhs_.data(), rhs_.data(), bias_.size() ? bias_.data() : nullptr, out_.data(), m(), n(),
+                           k(), flags_.tb, act, stream_);
     }
 
   private:
-    DeviceSpan<const float> a_, b_;
-    DeviceSpan<float> output_;
+    struct Flags {
+        bool ta = false, tb = false;
+        MatmulActivation act = MatmulActivation::none;
+    };
+    DeviceSpan<const float> lhs_, rhs_;
+    DeviceSpan<float> out_;
     DeviceSpan<const float> bias_;
-    int m_, n_, k_;
-    bool transpose_a_ = false, transpose_b_ = false;
-    MatmulActivation activation_ = MatmulActivation::none;
+    int dims_[3];
+    Flags flags_;
     hipStream_t stream_;
 };
 

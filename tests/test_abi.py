@@ -44,7 +44,9 @@ def test_adapters_export_solve():
     built = {p.name for p in adapters}
     for n in names:
         assert f"libopw_solve_{n}.so" in built, n
-        assert hasattr(ctypes.CDLL(str(ROOT / "opworks_amd" / "lib" / "adapters" / f"libopw_solve_{n}.so")), "solve")
+        lib = ctypes.CDLL(str(ROOT / "opworks_amd" / "lib" / "adapters" / f"libopw_solve_{n}.so"))
+        for sym in declared(hdr) + ["solve"]:
+            assert hasattr(lib, sym), (n, sym)
 
 
 # Contract checks mirror tests/unit/framework.cu:91-106; none reaches the device.
