@@ -122,6 +122,25 @@ int opw_attention_decode_ws_f32(const float *q, const float *kcache, const float
                                 int num_q_heads, int kv_rep, int head_dim, int len, int max_seq, float *workspace,
                                 int workspace_size, void *stream);
 
+/* ---- decoder-block steps (reference: include/ops/add.cuh:18-25, swiglu.cuh:19-26,
+ *      causal_scale.cuh:24-33, embedding.cuh:24-34, split_heads.cuh:39-66, rope.cuh:34-46,
+ *      argmax.cuh:59-63) ---- */
+int opw_add_f32(const float *a, const float *b, float *out, long long n, void *stream);
+int opw_swiglu_f32(const float *gate, const float *up, float *out, long long n, void *stream);
+int opw_causal_scale_f32(float *scores, int rows, int cols, float scale, void *stream);
+/* table [vocab][hidden]; an id outside [0, vocab) yields a NaN row (no out-of-table read). */
+int opw_embedding_f32(const float *table, long long vocab, const int *ids, float *out, int n, int hidden,
+                      void *stream);
+int opw_embedding_bf16(const uint16_t *table, long long vocab, const int *ids, float *out, int n, int hidden,
+                       void *stream);
+int opw_split_heads_f32(const float *in, float *out, int rows, int heads, int head_dim, int out_row_stride,
+                        int out_row_offset, void *stream);
+int opw_merge_heads_f32(const float *in, float *out, int rows, int heads, int head_dim, int in_row_stride,
+                        int in_row_offset, void *stream);
+int opw_rope_f32(float *x, const float *inv_freq, int rows, int heads, int head_dim, int pos_start, void *stream);
+/* out[0] (device int) = index of the maximum; ties -> lowest index, NaN never wins, all-NaN -> 0x7fffffff. */
+int opw_argmax_f32(const float *x, int n, int *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

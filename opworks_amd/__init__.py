@@ -80,6 +80,15 @@ _SIGNATURES = {
     "opw_attention_decode_workspace_size": (c_int, [c_int, c_int, c_int]),
     "opw_attention_decode_ws_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                             c_void_p, c_int, c_void_p]),
+    "opw_add_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "opw_swiglu_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "opw_causal_scale_f32": (c_int, [c_void_p, c_int, c_int, c_float, c_void_p]),
+    "opw_embedding_f32": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "opw_embedding_bf16": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "opw_split_heads_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
+    "opw_merge_heads_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
+    "opw_rope_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
+    "opw_argmax_f32": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
 }
 
 
@@ -366,6 +375,37 @@ class _Ops:
 
     def convert_f32_to_bf16(self, src: Ptr, dst: Ptr, n: int, stream=None) -> None:
         check(lib().opw_convert_f32_to_bf16(_p(src), _p(dst), n, _stream(stream)))
+
+    # ---- decoder-block steps
+    def add(self, a: Ptr, b: Ptr, out: Ptr, n: int, stream=None) -> None:
+        check(lib().opw_add_f32(_p(a), _p(b), _p(out), n, _stream(stream)))
+
+    def swiglu(self, gate: Ptr, up: Ptr, out: Ptr, n: int, stream=None) -> None:
+        check(lib().opw_swiglu_f32(_p(gate), _p(up), _p(out), n, _stream(stream)))
+
+    def causal_scale(self, scores: Ptr, rows: int, cols: int, scale: float, stream=None) -> None:
+        check(lib().opw_causal_scale_f32(_p(scores), rows, cols, scale, _stream(stream)))
+
+    def embedding(self, table: Ptr, vocab: int, ids: Ptr, out: Ptr, n: int, hidden: int, bf16: bool = False,
+                  stream=None) -> None:
+        fn = lib().opw_embedding_bf16 if bf16 else lib().opw_embedding_f32
+        check(fn(_p(table), vocab, _p(ids), _p(out), n, hidden, _stream(stream)))
+
+    def split_heads(self, x: Ptr, out: Ptr, rows: int, heads: int, head_dim: int, out_row_stride: int,
+                    out_row_offset: int = 0, stream=None) -> None:
+        check(lib().opw_split_heads_f32(_p(x), _p(out), rows, heads, head_dim, out_row_stride, out_row_offset,
+                                        _stream(stream)))
+
+    def merge_heads(self, x: Ptr, out: Ptr, rows: int, heads: int, head_dim: int, in_row_stride: int,
+                    in_row_offset: int = 0, stream=None) -> None:
+        check(lib().opw_merge_heads_f32(_p(x), _p(out), rows, heads, head_dim, in_row_stride, in_row_offset,
+                                        _stream(stream)))
+
+    def rope(self, x: Ptr, inv_freq: Ptr, rows: int, heads: int, head_dim: int, pos_start: int, stream=None) -> None:
+        check(lib().opw_rope_f32(_p(x), _p(inv_freq), rows, heads, head_dim, pos_start, _stream(stream)))
+
+    def argmax(self, x: Ptr, n: int, out: Ptr, stream=None) -> None:
+        check(lib().opw_argmax_f32(_p(x), n, _p(out), _stream(stream)))
 
 
 ops = _Ops()

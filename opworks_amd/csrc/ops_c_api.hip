@@ -5,10 +5,14 @@
 #include <hip/hip_runtime.h>
 
 #include "../include/core/random.hpp"
+#include "../include/ops/argmax.hpp"
 #include "../include/ops/elementwise.hpp"
+#include "../include/ops/heads.hpp"
 #include "../include/ops/layer_norm.hpp"
+#include "../include/ops/model_pointwise.hpp"
 #include "../include/ops/reduction.hpp"
 #include "../include/ops/rms_norm.hpp"
+#include "../include/ops/rope.hpp"
 #include "../include/ops/softmax.hpp"
 #include "c_api_common.hpp"
 
@@ -325,6 +329,76 @@ int opw_layer_norm_f32(const float *in, float *out, const float *gamma, const fl
 int opw_rms_norm_f32(const float *x, const float *weight, float *out, int rows, int cols, float eps, void *stream) {
     return guard([&] {
         opworks::ops::rms_norm(x, weight, out, rows, cols, eps, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_add_f32(const float *a, const float *b, float *out, long long n, void *stream) {
+    return guard([&] {
+        opworks::ops::add(a, b, out, n, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_swiglu_f32(const float *gate, const float *up, float *out, long long n, void *stream) {
+    return guard([&] {
+        opworks::ops::swiglu(gate, up, out, n, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_causal_scale_f32(float *scores, int rows, int cols, float scale, void *stream) {
+    return guard([&] {
+        opworks::ops::causal_scale(scores, rows, cols, scale, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_embedding_f32(const float *table, long long vocab, const int *ids, float *out, int n, int hidden,
+                      void *stream) {
+    return guard([&] {
+        opworks::detail::require(vocab > 0, "embedding vocab must be positive");
+        opworks::ops::embedding(table, ids, out, n, hidden, as_stream(stream), vocab);
+        return 0;
+    });
+}
+
+int opw_embedding_bf16(const uint16_t *table, long long vocab, const int *ids, float *out, int n, int hidden,
+                       void *stream) {
+    return guard([&] {
+        opworks::detail::require(vocab > 0, "embedding vocab must be positive");
+        opworks::ops::embedding(reinterpret_cast<const opworks::bf16 *>(table), ids, out, n, hidden,
+                                as_stream(stream), vocab);
+        return 0;
+    });
+}
+
+int opw_split_heads_f32(const float *in, float *out, int rows, int heads, int head_dim, int out_row_stride,
+                        int out_row_offset, void *stream) {
+    return guard([&] {
+        opworks::ops::split_heads(in, out, rows, heads, head_dim, out_row_stride, out_row_offset, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_merge_heads_f32(const float *in, float *out, int rows, int heads, int head_dim, int in_row_stride,
+                        int in_row_offset, void *stream) {
+    return guard([&] {
+        opworks::ops::merge_heads(in, out, rows, heads, head_dim, in_row_stride, in_row_offset, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_rope_f32(float *x, const float *inv_freq, int rows, int heads, int head_dim, int pos_start, void *stream) {
+    return guard([&] {
+        opworks::ops::rope(x, inv_freq, rows, heads, head_dim, pos_start, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_argmax_f32(const float *x, int n, int *out, void *stream) {
+    return guard([&] {
+        opworks::ops::argmax(x, n, out, as_stream(stream));
         return 0;
     });
 }

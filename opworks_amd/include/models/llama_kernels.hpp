@@ -24,6 +24,7 @@
 
 #include "../core/hip_utils.hpp"
 #include "../core/wave.hpp"
+#include "../ops/argmax.hpp"
 #include "../ops/attention.hpp"
 #include "../ops/elementwise.hpp"
 
@@ -431,21 +432,8 @@ __global__ __launch_bounds__(kBlock) void down_residual_kernel(const float *__re
 // (value, index); the last workgroup reduces the records. Ties go to the lowest
 // index and NaN never wins (reference: include/ops/argmax.cuh:8-14); an all-NaN
 // input yields 0x7fffffff.
-__device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i)) {
-        v = v2;
-        i = i2;
-    }
-}
-
-__device__ __forceinline__ void wave_argmax(float &v, int &i) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const float v2 = __shfl_xor(v, off);
-        const int i2 = __shfl_xor(i, off);
-        argmax_merge(v, i, v2, i2);
-    }
-}
+using detail::argmax_merge;
+using detail::wave_argmax;
 
 struct LmHeadArgs {
     const float *hidden_row; // [H]

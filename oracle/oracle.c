@@ -657,6 +657,25 @@ void orc_rope(float *x, const float *inv_freq, int rows, int heads, int head_dim
             }
 }
 
+/* swiglu_kernel (include/ops/swiglu.cuh:7-12): out = g / (1 + expf(-g)) * u,
+ * evaluated left to right in float. */
+void orc_swiglu(const float *gate, const float *up, float *out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float g = gate[i];
+        out[i] = g / (1.f + expf(-g)) * up[i];
+    }
+}
+
+/* causal_scale_kernel (include/ops/causal_scale.cuh:9-16): query row r sits at
+ * position cols - rows + r; keys up to it are scaled, later ones become -inf. */
+void orc_causal_scale(float *scores, int rows, int cols, float scale) {
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) {
+            float *p = scores + (int64_t)r * cols + c;
+            *p = c <= cols - rows + r ? *p * scale : -INFINITY;
+        }
+}
+
 typedef struct {
     int L, H, I, qh, kvh, D, V;
     float eps;

@@ -35,6 +35,11 @@
  *                        the reference's own model_config.cuh via oracle/_ref
  *  orc_rope              position 0 is the identity; pair norms preserved
  *  orc_argmax            brute force incl. ties, -inf and NaN
+ *  orc_swiglu            zeros at g = 0 and u = 0; silu(g) - silu(-g) = g;
+ *                        silu(g) -> g for large g and -> 0 for very negative g;
+ *                        float64 formula within 4 ulp
+ *  orc_causal_scale      visible count of row r is cols - rows + r + 1; each
+ *                        visible value equals the fp32 product x * scale
  *  orc_llama_*           float64 numpy forward of a tiny model; KV-cache
  *                        decode equals full recompute
  */
@@ -97,6 +102,8 @@ void orc_rope_inv_freq(int head_dim, float theta, int llama3, float factor, floa
                        float *out);
 void orc_rope(float *x, const float *inv_freq, int rows, int heads, int head_dim, int pos_start);
 int orc_argmax(const float *x, int n);
+void orc_swiglu(const float *gate, const float *up, float *out, int64_t n);
+void orc_causal_scale(float *scores, int rows, int cols, float scale);
 void *orc_llama_create(int L, int H, int I, int qh, int kvh, int D, int V, float eps, float theta, int llama3,
                        float factor, float low, float high, int orig, uint64_t seed, float sd, int norm_uniform);
 void orc_llama_destroy(void *m);

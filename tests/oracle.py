@@ -45,6 +45,8 @@ _SIGS = {
     "orc_rope_inv_freq": (None, [c_int, c_float, c_int, c_float, c_float, c_float, c_int, _F]),
     "orc_rope": (None, [_F, _F, c_int, c_int, c_int, c_int]),
     "orc_argmax": (c_int, [_F, c_int]),
+    "orc_swiglu": (None, [_F, _F, _F, ctypes.c_int64]),
+    "orc_causal_scale": (None, [_F, c_int, c_int, ctypes.c_float]),
     "orc_llama_create": (c_void_p, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_float, c_int,
                                     c_float, c_float, c_float, c_int, c_uint64, c_float, c_int]),
     "orc_llama_destroy": (None, [c_void_p]),
@@ -277,3 +279,16 @@ class Llama:
         if getattr(self, "h", None) and _lib is not None:
             _lib.orc_llama_destroy(self.h)
             self.h = None
+
+
+def swiglu(gate, up) -> np.ndarray:
+    g, u = f32(gate), f32(up)
+    out = np.empty_like(g)
+    lib().orc_swiglu(fp(g), fp(u), fp(out), g.size)
+    return out
+
+
+def causal_scale(scores, rows: int, cols: int, scale: float) -> np.ndarray:
+    s = f32(scores).copy()
+    lib().orc_causal_scale(fp(s), rows, cols, scale)
+    return s

@@ -150,3 +150,37 @@ def test_tiny_model_vs_float64(orc):
     tok2, logits2 = m.decode(tok)
     ref2 = _np_forward(m, TINY, ids + [tok])
     assert np.sqrt(np.mean((logits2 - ref2) ** 2)) / np.sqrt(np.mean(ref2 ** 2)) < 1e-5
+
+
+# ---- swiglu / causal_scale restatements (include/ops/swiglu.cuh:7-12,
+#      include/ops/causal_scale.cuh:9-16), pinned by closed forms
+def test_oracle_swiglu_closed_forms(orc):
+    g = np.array([0.0, 0.0, 30.0, -100.0, 1.5, -1.5, 4.0, -4.0], np.float32)
+    u = np.array([3.0, 0.0, 2.0, 5.0, 1.0, 1.0, 1.0, 1.0], np.float32)
+    out = orc.swiglu(g, u)
+    assert out[0] == 0.0 and out[1] == 0.0          # silu(0) = 0
+    assert out[2] == np.float32(60.0)               # sigmoid(30) rounds to 1 in fp32
+    assert out[3] == 0.0                            # exp(100) overflows: g / inf = -0
+    # silu(g) - silu(-g) = g
+    assert abs(float(out[4]) - float(out[5]) - 1.5) <= 4e-7 * 1.5
+    assert abs(float(out[6]) - float(out[7]) - 4.0) <= 4e-7 * 4.0
+    rng = np.random.default_rng(3)
+    gg = rng.normal(0, 4, 4096).astype(np.float32)
+    uu = rng.normal(0, 1, 4096).astype(np.float32)
+    want = gg.astype(np.float64) / (1 + np.exp(-gg.astype(np.float64))) * uu
+    got = orc.swiglu(gg, uu).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 4 * np.finfo(np.float32).eps * np.abs(want) + 1e-37)
+
+
+def test_oracle_causal_scale_mask_shape(orc):
+    rows, cols, scale = 5, 9, 0.125
+    x = np.random.default_rng(4).normal(size=rows * cols).astype(np.float32)
+    out = orc.causal_scale(x, rows, cols, scale).reshape(rows, cols)
+    for r in range(rows):
+        visible = np.isfinite(out[r])
+        assert visible.sum() == cols - rows + r + 1
+        assert np.all(visible[: cols - rows + r + 1])  # a prefix of the keys
+        assert np.array_equal(out[r][visible], (x.reshape(rows, cols)[r][visible] * np.float32(scale)))
+        assert np.all(out[r][~visible] == -np.inf)
+    sq = orc.causal_scale(np.ones(16, np.float32), 4, 4, 1.0).reshape(4, 4)
+    assert np.array_equal(np.isfinite(sq), np.tril(np.ones((4, 4), bool)))
