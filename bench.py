@@ -66,6 +66,20 @@ def roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) 
             "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "llama_decode_traffic.md"
+
+
+def profiled_traffic(stage: str):
+    """HBM bytes per launch of a decode stage's kernel, as measured by the committed rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE passes (scaled by the copy-kernel calibration in that file), or None."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith(f"traffic_bytes_per_launch {stage}:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
 # ------------------------------------------------------------------ workloads
 def wl_map(stream, steps, warmup):
     """Config 2a: ScaleAdd(alpha=2.5) over n = 2^28 fp32; 12 B/element."""
@@ -211,7 +225,7 @@ def wl_llama(stream, steps, warmup):
     """Config 5: Llama-3.2-1B architecture, fp32 weights N(0, 0.02) (seeded), RMSNorm gamma = 1, 512
     uniform-random prompt ids, greedy 256 tokens with the KV cache, no EOS stop. A step is one full
     generation through the C ABI's greedy loop; value = 255 decode steps / decode wall time (median over
-    steps, after warmup). The roofline is the gate/up GEMV (the largest decode kernel, 134,225,920 B per
+    steps, after warmup). The roofline is the gate/up GEMV (the largest decode kernel, 134,266,880 B per
     launch) timed with HIP events on the session stream."""
     from opworks_amd.llama import LLAMA_3_2_1B, LlamaModel
     cfg = dict(LLAMA_3_2_1B)
@@ -229,29 +243,28 @@ def wl_llama(stream, steps, warmup):
     dec = sorted(r[1] for r in runs)[len(runs) // 2]
     pre = sorted(r[0] for r in runs)[len(runs) // 2]
     tok_s = (new_tokens - 1) / (dec / 1e3)
-    # per-kernel profile of one more decode step at the end of the sequence
-    prof = sess.profile_decode_step(int(runs[-1][2][-1]))
+    # Each decode stage launched back to back over the 16 layers (HIP events on the session stream):
+    # kernel time without launch gaps, comparable with rocprofv3's per-kernel average.
     H, I, V, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"], cfg["num_hidden_layers"]
     qkv_w = (cfg["num_attention_heads"] + 2 * cfg["num_key_value_heads"]) * cfg["head_dim"]
     kernel_bytes = {"qkv_rope": 4 * (qkv_w * H + 2 * H), "o_proj": 4 * (H * H + 3 * H),
                     "gate_up": 4 * (2 * I * H + 2 * H + I), "down": 4 * (H * I + I + 2 * H),
                     "lm_head": 4 * (V * H + 2 * H + V)}
     breakdown = {}
-    for k, ms_list in prof.items():
-        avg = sum(ms_list) / len(ms_list)
-        entry = {"avg_us": round(avg * 1e3, 2), "total_us_per_token": round(sum(ms_list) * 1e3, 1)}
+    for k in sess.STAGES:
+        us = sess.time_decode_stage(k, reps=10)
+        entry = {"avg_us": round(us, 2)}
         if k in kernel_bytes:
-            entry["gbs"] = round(kernel_bytes[k] / (avg * 1e-3) / 1e9, 1)
+            entry["gbs"] = round(kernel_bytes[k] / (us * 1e-6) / 1e9, 1)
         breakdown[k] = entry
-    gu_ms = sum(prof["gate_up"]) / L
-    gu_gbs = kernel_bytes["gate_up"] / (gu_ms * 1e-3) / 1e9
+    gu_gbs = kernel_bytes["gate_up"] / (breakdown["gate_up"]["avg_us"] * 1e-6) / 1e9
     weight_bytes = 4 * (V * H + L * (qkv_w * H + H * H + 2 * I * H + H * I) + (2 * L + 1) * H)
     kv_bytes_avg = 2 * L * cfg["num_key_value_heads"] * cfg["head_dim"] * 4 * (512 + new_tokens / 2)
     step_gbs = (weight_bytes + kv_bytes_avg) / (dec / (new_tokens - 1) * 1e-3) / 1e9
     return {"workload": "llama3.2-1b_fp32_greedy_prompt512_gen256", "unit": "tok/s", "value": tok_s,
             "ms": pre + dec, "ttft_ms": round(pre, 3), "decode_ms_per_token": round(dec / (new_tokens - 1), 4),
             "kernel": "swiglu_gemv_kernel<8> (gate/up)",
-            "roofline": roofline(gu_gbs, HBM_PEAK_GBS, "GB/s", "hbm"),
+            "roofline": roofline(gu_gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("gate_up")),
             "decode_step_roofline": roofline(step_gbs, HBM_PEAK_GBS, "GB/s", "hbm"),
             "weight_bytes_per_token": weight_bytes, "kernels": breakdown,
             "first_tokens": [int(t) for t in runs[-1][2][:8]]}
@@ -313,6 +326,28 @@ def cpu_baseline(name: str) -> dict:
         dt = (time.perf_counter() - t0) / reps
         return {"value": round(8 * rows * cols / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
                 "sample": f"oracle orc_rms_norm_rows, 2048 of the 8192 rows, {reps} reps"}
+    if name == "llama":
+        from opworks_amd.llama import LLAMA_3_2_1B
+        cfg = dict(LLAMA_3_2_1B)
+        t_build = time.perf_counter()
+        model = orc.Llama(cfg, SEED, 0.02, "ones")  # the same seeded weights as the GPU model
+        build_s = time.perf_counter() - t_build
+        rng = np.random.default_rng(SEED)
+        prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], 512)][:16]
+        model.reset(1024)
+        tok, _ = model.prefill(prompt)
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            tok, _ = model.decode(tok)
+            steps += 1
+            if time.perf_counter() - t0 > 15.0 or steps >= 64:
+                break
+        dt = (time.perf_counter() - t0) / steps
+        del model
+        return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+                "sample": f"oracle fp32 Llama forward (orc_llama_*), same seeded weights: 16-token prompt "
+                          f"(first 16 of the 512 ids), then {steps} greedy decode steps timed "
+                          f"(~15 s; weight generation {build_s:.1f} s untimed)"}
     return {}
 
 

@@ -68,6 +68,12 @@ int opw_llama_generate_greedy(void *session, const int32_t *prompt, int n, int m
  * number of kernels (5 * layers + 1), -1 on error. */
 int opw_llama_profile_decode_step(void *session, int32_t prev_token, float *kernel_ms, int capacity, char *err,
                                   int err_len);
+/* Average duration (microseconds) of one launch of a decode stage: 0 qkv_rope, 1 attention (partial +
+ * combine), 2 o_proj, 3 gate_up, 4 down, 5 lm_head + argmax. The stage alone runs for every layer in
+ * order, `reps` times, between two events on the session stream (consecutive launches stream different
+ * layers' weights). Needs a prefilled session with free capacity; -1 on error. Timing aid, no
+ * counterpart in the reference. */
+float opw_llama_time_decode_stage(void *session, int stage, int reps, char *err, int err_len);
 
 #ifdef __cplusplus
 }

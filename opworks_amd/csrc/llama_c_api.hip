@@ -225,4 +225,16 @@ int opw_llama_profile_decode_step(void *session, int32_t prev_token, float *kern
         err, err_len);
 }
 
+float opw_llama_time_decode_stage(void *session, int stage, int reps, char *err, int err_len) {
+    float us = -1.f;
+    const int rc = guard(
+        [&] {
+            auto *s = as_session(session);
+            us = s->owner->model->time_decode_stage(*s->session, stage, reps);
+            return 0;
+        },
+        err, err_len);
+    return rc < 0 ? -1.f : us;
+}
+
 } // extern "C"

@@ -272,6 +272,48 @@ class LlamaModel {
         return ms;
     }
 
+    // Average duration in microseconds of one launch of a decode stage
+    // (0 qkv_rope, 1 attention partial + combine, 2 o_proj, 3 gate_up,
+    // 4 down, 5 lm_head + argmax): the stage alone is enqueued for every layer
+    // in order, `reps` times, between two events on the session stream, so
+    // consecutive launches stream different layers' weights. Uses the state
+    // of the last decode step; the KV entry it writes lies past the session's
+    // length and is overwritten by the next real step. Requires a prefill.
+    float time_decode_stage(Session &s, int stage, int reps) {
+        if (stage < 0 || stage > 5)
+            throw std::invalid_argument("decode stage must be in [0, 5]");
+        if (reps <= 0)
+            throw std::invalid_argument("reps must be positive");
+        if (s.length == 0 || s.length >= s.max_seq_len)
+            throw std::invalid_argument("time_decode_stage needs a prefilled session with free capacity");
+        s.h_state->token = 0;
+        s.h_state->pos = s.length;
+        OPWORKS_HIP_CHECK(hipMemcpyAsync(s.state(), s.h_state, sizeof(llama::StepState), hipMemcpyHostToDevice,
+                                         s.stream));
+        hipEvent_t e0, e1;
+        OPWORKS_HIP_CHECK(hipEventCreate(&e0));
+        OPWORKS_HIP_CHECK(hipEventCreate(&e1));
+        stage_mask_ = 1u << stage;
+        try {
+            enqueue_decode(s); // warm-up pass
+            OPWORKS_HIP_CHECK(hipEventRecord(e0, s.stream));
+            for (int r = 0; r < reps; ++r)
+                enqueue_decode(s);
+            OPWORKS_HIP_CHECK(hipEventRecord(e1, s.stream));
+        } catch (...) {
+            stage_mask_ = kAllStages;
+            throw;
+        }
+        stage_mask_ = kAllStages;
+        synchronize(s.stream);
+        float ms = 0.f;
+        OPWORKS_HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        const int per_pass = stage == 5 ? 1 : cfg_.num_layers;
+        return 1e3f * ms / float(reps * per_pass);
+    }
+
     bool is_eos(int32_t token) const {
         return std::find(cfg_.eos_token_ids.begin(), cfg_.eos_token_ids.end(), token) != cfg_.eos_token_ids.end();
     }
@@ -324,6 +366,11 @@ class LlamaModel {
     LlamaWeights w_;
     // When set (profiling only), called before every kernel of the decode step.
     const std::function<void()> *tick_ = nullptr;
+    // Stages enqueued by the decode step (timing only narrows it): bit 0
+    // qkv_rope, 1 attention, 2 o_proj, 3 gate_up, 4 down, 5 lm_head + argmax.
+    unsigned stage_mask_ = kAllStages;
+    static constexpr unsigned kAllStages = 0x3f;
+    bool stage_on(int stage) const { return (stage_mask_ >> stage) & 1u; }
     void tick() const {
         if (tick_)
             (*tick_)();
@@ -486,9 +533,11 @@ class LlamaModel {
         qa.kvh = kvh;
         qa.D = D;
         qa.cap = s.max_seq_len;
-        tick();
-        launch_async(st, llama::qkv_rope_kernel<kV>, detail::blocks_for64(qkv_waves, llama::kWavesPerBlock),
-                     llama::kBlock, qa);
+        if (stage_on(0)) {
+            tick();
+            launch_async(st, llama::qkv_rope_kernel<kV>, detail::blocks_for64(qkv_waves, llama::kWavesPerBlock),
+                         llama::kBlock, qa);
+        }
         llama::DecodeAttnArgs aa{};
         aa.q = s.d_q.data();
         aa.kcache = layer_k(s, l);
@@ -501,32 +550,40 @@ class LlamaModel {
         aa.cap = s.max_seq_len;
         aa.max_chunks = s.attn_max_chunks;
         aa.scale = 1.f / std::sqrt(static_cast<float>(D));
-        tick();
         const int rep = cfg_.kv_rep();
         const dim3 agrid(kvh, s.attn_max_chunks);
-        if (rep <= 1)
-            launch_async(st, llama::decode_attention_kernel<1>, agrid, kWaveSize, aa);
-        else if (rep <= 2)
-            launch_async(st, llama::decode_attention_kernel<2>, agrid, 2 * kWaveSize, aa);
-        else if (rep <= 4)
-            launch_async(st, llama::decode_attention_kernel<4>, agrid, 4 * kWaveSize, aa);
-        else if (rep <= 8)
-            launch_async(st, llama::decode_attention_kernel<8>, agrid, 8 * kWaveSize, aa);
-        else
-            launch_async(st, llama::decode_attention_kernel<16>, agrid, 16 * kWaveSize, aa);
-        launch_async(st, llama::decode_combine_kernel, kvh, rep * kWaveSize, aa);
-        tick();
-        launch_async(st, llama::gemv_residual_kernel<kV>,
-                     detail::blocks_for64(detail::blocks_for64(H, llama::kRows), llama::kWavesPerBlock), llama::kBlock,
-                     lw.wo.data(), s.d_attn.data(), s.d_hidden.data(), H);
-        tick();
-        launch_async(st, llama::swiglu_gemv_kernel<kV>,
-                     detail::blocks_for64(detail::blocks_for64(I, llama::kRows / 2), llama::kWavesPerBlock),
-                     llama::kBlock, s.d_hidden.data(), lw.post_norm.data(), cfg_.rms_norm_eps, lw.wgu.data(),
-                     s.d_act.data(), I);
-        tick();
-        launch_async(st, llama::down_residual_kernel<kV2>, detail::blocks_for64(H, llama::kRows), llama::kBlock,
-                     lw.wdown.data(), s.d_act.data(), s.d_hidden.data(), H);
+        if (stage_on(1)) {
+            tick();
+            if (rep <= 1)
+                launch_async(st, llama::decode_attention_kernel<1>, agrid, kWaveSize, aa);
+            else if (rep <= 2)
+                launch_async(st, llama::decode_attention_kernel<2>, agrid, 2 * kWaveSize, aa);
+            else if (rep <= 4)
+                launch_async(st, llama::decode_attention_kernel<4>, agrid, 4 * kWaveSize, aa);
+            else if (rep <= 8)
+                launch_async(st, llama::decode_attention_kernel<8>, agrid, 8 * kWaveSize, aa);
+            else
+                launch_async(st, llama::decode_attention_kernel<16>, agrid, 16 * kWaveSize, aa);
+            launch_async(st, llama::decode_combine_kernel, kvh, rep * kWaveSize, aa);
+        }
+        if (stage_on(2)) {
+            tick();
+            launch_async(st, llama::gemv_residual_kernel<kV>,
+                         detail::blocks_for64(detail::blocks_for64(H, llama::kRows), llama::kWavesPerBlock),
+                         llama::kBlock, lw.wo.data(), s.d_attn.data(), s.d_hidden.data(), H);
+        }
+        if (stage_on(3)) {
+            tick();
+            launch_async(st, llama::swiglu_gemv_kernel<kV>,
+                         detail::blocks_for64(detail::blocks_for64(I, llama::kRows / 2), llama::kWavesPerBlock),
+                         llama::kBlock, s.d_hidden.data(), lw.post_norm.data(), cfg_.rms_norm_eps, lw.wgu.data(),
+                         s.d_act.data(), I);
+        }
+        if (stage_on(4)) {
+            tick();
+            launch_async(st, llama::down_residual_kernel<kV2>, detail::blocks_for64(H, llama::kRows), llama::kBlock,
+                         lw.wdown.data(), s.d_act.data(), s.d_hidden.data(), H);
+        }
     }
 
     // All layers then the LM head; `hook(l)` (debug only) runs after layer l.
@@ -538,7 +595,8 @@ class LlamaModel {
                 if (hook)
                     hook(l);
             }
-            enqueue_lm_head<kV>(s, s.d_hidden.data());
+            if (stage_on(5))
+                enqueue_lm_head<kV>(s, s.d_hidden.data());
         });
     }
 

@@ -33,6 +33,7 @@ for _name, _res, _args in [
     ("opw_llama_debug_prefill", c_int, [c_void_p, POINTER(c_int32), c_int, POINTER(c_float), c_int64, c_char_p,
                                         c_int]),
     ("opw_llama_profile_decode_step", c_int, [c_void_p, c_int32, POINTER(c_float), c_int, c_char_p, c_int]),
+    ("opw_llama_time_decode_stage", c_float, [c_void_p, c_int, c_int, c_char_p, c_int]),
     ("opw_llama_generate_greedy", c_int, [c_void_p, POINTER(c_int32), c_int, c_int, POINTER(c_int32),
                                           POINTER(c_double), POINTER(c_double), c_char_p, c_int]),
 ]:
@@ -159,6 +160,15 @@ class LlamaSession:
         out = {k: [float(ms[5 * l + i]) for l in range(m.num_layers)] for i, k in enumerate(self.KERNELS_PER_LAYER)}
         out["lm_head"] = [float(ms[-1])]
         return out
+
+    STAGES = ("qkv_rope", "attention", "o_proj", "gate_up", "down", "lm_head")
+
+    def time_decode_stage(self, stage: str, reps: int = 10) -> float:
+        """Average microseconds per launch of one decode stage, launched back to back over all layers."""
+        us = lib().opw_llama_time_decode_stage(self.handle, self.STAGES.index(stage), reps, self._err, _ERR_LEN)
+        if us < 0:
+            raise OpworksError(self._err.value.decode(errors="replace"))
+        return float(us)
 
     def close(self) -> None:
         if self.handle:

@@ -127,6 +127,29 @@ def test_reset_repeat_is_deterministic(tiny):
     assert outs[0][0] == outs[1][0] and np.array_equal(outs[0][1], outs[1][1])
 
 
+def test_stage_timing_leaves_the_sequence_unchanged(tiny, ow):
+    """time_decode_stage runs stages out of order against the live session; the
+    tokens and logits that follow must equal an untimed run's."""
+    gpu, _ = tiny
+    ids = prompt(6, TINY["vocab_size"], 4)
+    runs = []
+    for timed in (False, True):
+        s = gpu.session(64)
+        tok = s.prefill(ids)
+        seq = [tok]
+        for i in range(10):
+            if timed and i == 3:
+                for stage in s.STAGES:
+                    assert s.time_decode_stage(stage, reps=2) > 0
+            tok = s.decode_step(tok)
+            seq.append(tok)
+        runs.append((seq, s.last_logits()))
+    assert runs[0][0] == runs[1][0] and np.array_equal(runs[0][1], runs[1][1])
+    fresh = gpu.session(8)
+    with pytest.raises(ow.OpworksError, match="prefilled"):
+        fresh.time_decode_stage("gate_up")
+
+
 def test_interleaved_sessions(tiny):
     gpu, _ = tiny
     ids_a, ids_b = prompt(6, TINY["vocab_size"], 4), prompt(11, TINY["vocab_size"], 5)
