@@ -47,6 +47,10 @@ const char *opw_llama_last_error(void);
  * (norm_init 1). Replaces writing a multi-GB synthetic pack. NULL on error. */
 void *opw_llama_load_random(const char *config_json, uint64_t seed, float init_std, int norm_init, char *err,
                             int err_len);
+/* RoPE inverse frequencies (head_dim / 2 floats) the runtime derives from an
+ * HF-style config JSON object, llama3 scaling included (ModelConfig::rope_inv_freq,
+ * include/runtime/model_config.cuh:68-89). Host only, no device work. 0 / -1. */
+int opw_llama_config_inv_freq(const char *config_json, float *out, int n, char *err, int err_len);
 /* Model shape: out[0..6] = layers, hidden, intermediate, q heads, kv heads, head_dim, vocab. 0 / -1. */
 int opw_llama_model_config(void *model, int *out7, char *err, int err_len);
 /* Prefill that also returns the residual stream after the embedding and after

@@ -143,6 +143,22 @@ void *opw_llama_load_random(const char *config_json, uint64_t seed, float init_s
         err, err_len);
 }
 
+int opw_llama_config_inv_freq(const char *config_json, float *out, int n, char *err, int err_len) {
+    return guard(
+        [&] {
+            if (!config_json || !out)
+                throw std::invalid_argument("null config or output");
+            const opworks::json::Value cfg = opworks::json::parse(config_json);
+            const std::vector<float> f =
+                opworks::ModelConfig::from_json(cfg, cfg.find("eos_token_id")).rope_inv_freq();
+            if (n != static_cast<int>(f.size()))
+                throw std::invalid_argument("output must hold head_dim / 2 floats");
+            std::memcpy(out, f.data(), f.size() * sizeof(float));
+            return 0;
+        },
+        err, err_len);
+}
+
 int opw_llama_model_config(void *model, int *out7, char *err, int err_len) {
     return guard(
         [&] {

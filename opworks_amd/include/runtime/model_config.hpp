@@ -78,10 +78,8 @@ struct ModelConfig {
             throw std::runtime_error("invalid model config");
         if (num_q_heads * head_dim != hidden_size)
             throw std::runtime_error("num_attention_heads * head_dim != hidden_size");
-        if (head_dim % 2 != 0 || head_dim > 64 || head_dim % 16 != 0)
-            throw std::runtime_error("head_dim must be 16, 32, 48 or 64");
-        if (hidden_size % 64 != 0 || intermediate_size % 64 != 0)
-            throw std::runtime_error("hidden and intermediate sizes must be multiples of 64");
+        if (head_dim % 2 != 0)
+            throw std::runtime_error("head_dim must be even");
         if (!(rms_norm_eps > 0.f) || !(rope_theta > 0.f))
             throw std::runtime_error("rms_norm_eps and rope_theta must be positive");
     }
