@@ -514,7 +514,7 @@ class LlamaModel {
     template <int kV, int kV2> void enqueue_decode_layer(Session &s, int l) const {
         const int H = cfg_.hidden_size, I = cfg_.intermediate_size, D = cfg_.head_dim;
         const int qh = cfg_.num_q_heads, kvh = cfg_.num_kv_heads;
-        const int qkv_waves = (qh + 2 * kvh) * (D / 4);
+        const int qkv_groups = (qh + 2 * kvh) * (D / 4); // 4 rows each
         hipStream_t st = s.stream;
         const LlamaLayerWeights &lw = w_.layers[static_cast<size_t>(l)];
         llama::QkvArgs qa{};
@@ -535,8 +535,7 @@ class LlamaModel {
         qa.cap = s.max_seq_len;
         if (stage_on(0)) {
             tick();
-            launch_async(st, llama::qkv_rope_kernel<kV>, detail::blocks_for64(qkv_waves, llama::kWavesPerBlock),
-                         llama::kBlock, qa);
+            launch_async(st, llama::qkv_rope_kernel<kV>, qkv_groups, llama::kBlock, qa);
         }
         llama::DecodeAttnArgs aa{};
         aa.q = s.d_q.data();
@@ -568,14 +567,12 @@ class LlamaModel {
         }
         if (stage_on(2)) {
             tick();
-            launch_async(st, llama::gemv_residual_kernel<kV>,
-                         detail::blocks_for64(detail::blocks_for64(H, llama::kRows), llama::kWavesPerBlock),
+            launch_async(st, llama::gemv_residual_kernel<kV>, detail::blocks_for64(H, llama::kRows),
                          llama::kBlock, lw.wo.data(), s.d_attn.data(), s.d_hidden.data(), H);
         }
         if (stage_on(3)) {
             tick();
-            launch_async(st, llama::swiglu_gemv_kernel<kV>,
-                         detail::blocks_for64(detail::blocks_for64(I, llama::kRows / 2), llama::kWavesPerBlock),
+            launch_async(st, llama::swiglu_gemv_kernel<kV>, detail::blocks_for64(2 * I, llama::kWavesPerBlock),
                          llama::kBlock, s.d_hidden.data(), lw.post_norm.data(), cfg_.rms_norm_eps, lw.wgu.data(),
                          s.d_act.data(), I);
         }

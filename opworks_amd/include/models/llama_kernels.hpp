@@ -2,22 +2,23 @@
 
 // Kernels of the Llama decode step and prefill glue (fp32 weights).
 //
-// Decode step per layer (5 launches; every kernel reads the step position from
-// device memory, so one captured HIP graph replays every token):
+// Decode step per layer (every kernel reads the step position from device
+// memory, so one captured HIP graph replays every token):
 //   1. qkv_rope_kernel   RMSNorm(hidden) -> fused [q;k;v] GEMV -> RoPE on q, k ->
 //                        q to the workspace, k and v appended to the KV cache
-//   2. decode_attention_kernel  split-KV partials; the last workgroup of each
-//                        kv head merges the chunks (no second launch)
+//   2. decode_attention_kernel + decode_combine_kernel  split-KV partial
+//                        records per 64-key chunk, merged in fixed order
 //   3. gemv_residual_kernel   hidden += W_o attn
-//   4. norm_gemv_kernel<SwiGLU>  RMSNorm(hidden) -> interleaved [gate;up] GEMV ->
+//   4. swiglu_gemv_kernel     RMSNorm(hidden) -> interleaved [gate;up] GEMV ->
 //                        act = silu(gate) * up
 //   5. down_residual_kernel   hidden += W_down act (K split over 4 waves)
-// then final RMSNorm + LM-head GEMV with a fused argmax (last-workgroup reduce).
+// then lm_head_kernel (final RMSNorm + tied-embedding GEMV + per-workgroup
+// argmax records) and argmax_records_kernel.
 //
-// GEMV shape: a wave owns kRows output rows; each lane streams 16-byte packs
-// of those rows at columns 4*(lane + 64*u) with all loads issued before the
-// FMAs; the normalised input vector lives in registers (kV packs per lane);
-// one DPP reduction per row. Weight bytes are read once per token.
+// GEMV shape: a wave owns one output row (LM head: four; o_proj: a quarter of
+// the columns of four rows); each lane streams 16-byte packs of its rows with
+// every load issued before the FMAs, and the (normalised) input vector is
+// staged once per workgroup in LDS. Weight bytes are read once per token.
 
 #include <cmath>
 #include <cstdint>
@@ -40,21 +41,21 @@ struct StepState {
     int32_t pad;
 };
 
-constexpr int kRows = 4;       // GEMV rows per wave
+constexpr int kRows = 4;       // rows per LM-head wave; rows per workgroup of the other GEMVs
 constexpr int kBlock = 256;    // threads per GEMV workgroup
 constexpr int kWavesPerBlock = kBlock / kWaveSize;
 
-// GEMV of a 4-wave workgroup: each wave owns kRows rows of a [*, H] matrix,
+// GEMV of a 4-wave workgroup: each wave owns kR rows of a [*, H] matrix,
 // H = 256 * kV. The input vector is staged once per workgroup: its loads are
 // issued first, then every weight pack of the wave, so with in-order vmcnt
 // accounting the RMS statistics are computed while the weights stream in.
 // The (optionally RMS-normalised) vector goes to LDS and each wave reads its
 // kV packs from there. Waves with active == false still take part in the
 // barriers. xn = x * rsqrtf(mean(x^2) + eps) * gamma, ops::rms_norm's order.
-template <int kV>
+template <int kV, int kR = kRows>
 __device__ __forceinline__ void block_gemv(const float *__restrict__ x, const float *__restrict__ gamma, float eps,
-                                           const float *__restrict__ W, const int (&row)[kRows], bool active,
-                                           float *__restrict__ copy_x_to, float (&y)[kRows]) {
+                                           const float *__restrict__ W, const int (&row)[kR], bool active,
+                                           float *__restrict__ copy_x_to, float (&y)[kR]) {
     constexpr int H = 256 * kV;
     constexpr int kPacks = H / 4;
     constexpr int kX = (kPacks + kBlock - 1) / kBlock; // input packs per thread
@@ -73,10 +74,10 @@ __device__ __forceinline__ void block_gemv(const float *__restrict__ x, const fl
                 gv[i] = g4[c];
         }
     }
-    f32x4 w[kRows][kV];
+    f32x4 w[kR][kV];
     if (active) {
 #pragma unroll
-        for (int r = 0; r < kRows; ++r)
+        for (int r = 0; r < kR; ++r)
 #pragma unroll
             for (int u = 0; u < kV; ++u)
                 w[r][u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(W + int64_t(row[r]) * H) + lane +
@@ -116,7 +117,7 @@ __device__ __forceinline__ void block_gemv(const float *__restrict__ x, const fl
     if (!active)
         return;
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
+    for (int r = 0; r < kR; ++r) {
         float acc = 0.f;
 #pragma unroll
         for (int u = 0; u < kV; ++u) {
@@ -129,11 +130,57 @@ __device__ __forceinline__ void block_gemv(const float *__restrict__ x, const fl
     }
 }
 
+// GEMV of kRows rows by a whole workgroup, the columns split across its four
+// waves: thread t owns input packs t + kBlock * i (i < kV / 4), so wave w
+// covers packs w * 64 + lane + 256 * i of every row. The thread's input packs
+// are exactly the ones its dot products need, so only the per-wave partial
+// sums go through LDS, combined in the fixed order (w0 + w1) + (w2 + w3).
+// Serves short matrices (o_proj), where it measured faster than one row per
+// wave.
+template <int kV>
+__device__ __forceinline__ void block_gemv_split(const float *__restrict__ x, const float *__restrict__ W,
+                                                 const int (&row)[kRows], float (&y)[kRows]) {
+    static_assert(kV % 4 == 0, "the split GEMV needs H to be a multiple of 1024");
+    constexpr int H = 256 * kV;
+    constexpr int kX = kV / 4; // packs per thread
+    __shared__ float part[kWavesPerBlock][kRows];
+    const int tid = threadIdx.x, lane = tid % kWaveSize, wave = tid / kWaveSize;
+    const f32x4 *x4 = reinterpret_cast<const f32x4 *>(x);
+    f32x4 xv[kX];
+#pragma unroll
+    for (int i = 0; i < kX; ++i)
+        xv[i] = x4[tid + kBlock * i];
+    f32x4 w[kRows][kX];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r)
+#pragma unroll
+        for (int i = 0; i < kX; ++i)
+            w[r][i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(W + int64_t(row[r]) * H) + tid +
+                                                 kBlock * i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < kX; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc = fmaf(w[r][i][j], xv[i][j], acc);
+        acc = wave::sum(acc);
+        if (lane == 0)
+            part[wave][r] = acc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kRows; ++r)
+        y[r] = (part[0][r] + part[1][r]) + (part[2][r] + part[3][r]);
+}
+
 // ---- 1. QKV + RoPE + cache append ------------------------------------------
-// Fused weight rows: [q heads | k heads | v heads], each head D rows. Wave w
-// owns rotary pairs (j, j + D/2) and (j+1, j+1 + D/2) of head slot w / (D/4),
-// j = 2 * (w % (D/4)). Layer 0 reads its input from the embedding row of the
-// step token and also writes it to the residual stream.
+// Fused weight rows: [q heads | k heads | v heads], each head D rows.
+// Workgroup g owns rotary pairs (j, j + D/2) and (j+1, j+1 + D/2) of head
+// slot g / (D/4), j = 2 * (g % (D/4)). Layer 0 reads its input from the
+// embedding row of the step token and also writes it to the residual stream.
 struct QkvArgs {
     const float *hidden_in; // residual stream (or nullptr: use embed[token])
     const float *embed;     // [V][H]
@@ -148,26 +195,9 @@ struct QkvArgs {
     int qh, kvh, D, cap;
 };
 
-template <int kV>
-__global__ __launch_bounds__(kBlock) void qkv_rope_kernel(QkvArgs a) {
-    constexpr int H = 256 * kV;
-    const int lane = threadIdx.x % kWaveSize;
-    const int w = blockIdx.x * kWavesPerBlock + threadIdx.x / kWaveSize;
-    const int waves_per_head = a.D / 4;
-    const int slot = w / waves_per_head;
-    const bool active = slot < a.qh + 2 * a.kvh;
-    const int pos = a.state->pos;
-    const float *src = a.hidden_in ? a.hidden_in : a.embed + int64_t(a.state->token) * H;
+__device__ __forceinline__ void qkv_store(const QkvArgs &a, int slot, int j, int pos, const float (&y_in)[4]) {
     const int half = a.D / 2;
-    const int j = 2 * (w % waves_per_head);
-    const int base = (active ? slot : 0) * a.D;
-    const int row[kRows] = {base + j, base + j + 1, base + j + half, base + j + 1 + half};
-    float y[kRows];
-    // layer 0: workgroup 0 also writes the embedding row into the residual stream
-    block_gemv<kV>(src, a.gamma, a.eps, a.wqkv, row, active,
-                   (!a.hidden_in && blockIdx.x == 0) ? a.hidden_out : nullptr, y);
-    if (!active || lane != 0)
-        return;
+    float y[4] = {y_in[0], y_in[1], y_in[2], y_in[3]};
     if (slot < a.qh + a.kvh) { // rotate q and k: (lo, hi) = (a c - b s, b c + a s)
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
@@ -189,6 +219,29 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(QkvArgs a) {
     dst[j + 1] = y[1];
     dst[j + half] = y[2];
     dst[j + 1 + half] = y[3];
+}
+
+// One workgroup per 4-row group (grid = (qh + 2 kvh) * D / 4), one row per
+// wave: wave w computes row j + (w & 1) + (w >> 1) * D/2 of the head slot.
+template <int kV>
+__global__ __launch_bounds__(kBlock) void qkv_rope_kernel(QkvArgs a) {
+    constexpr int H = 256 * kV;
+    __shared__ float res[kWavesPerBlock];
+    const int g = blockIdx.x, wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
+    const int groups_per_head = a.D / 4;
+    const int slot = g / groups_per_head;
+    const int j = 2 * (g % groups_per_head);
+    const int pos = a.state->pos;
+    const float *src = a.hidden_in ? a.hidden_in : a.embed + int64_t(a.state->token) * H;
+    const int row[1] = {slot * a.D + j + (wave & 1) + (wave >> 1) * (a.D / 2)};
+    float y[1];
+    // layer 0: workgroup 0 also writes the embedding row into the residual stream
+    block_gemv<kV, 1>(src, a.gamma, a.eps, a.wqkv, row, true, (!a.hidden_in && g == 0) ? a.hidden_out : nullptr, y);
+    if (lane == 0)
+        res[wave] = y[0];
+    __syncthreads();
+    if (threadIdx.x == 0)
+        qkv_store(a, slot, j, pos, {res[0], res[1], res[2], res[3]});
 }
 
 // ---- 2. decode attention: split-KV partials + combine ---------------------
@@ -342,40 +395,53 @@ template <int kV>
 __global__ __launch_bounds__(kBlock) void gemv_residual_kernel(const float *__restrict__ W,
                                                                const float *__restrict__ x, float *__restrict__ hidden,
                                                                int out) {
-    const int lane = threadIdx.x % kWaveSize;
-    const int w = blockIdx.x * kWavesPerBlock + threadIdx.x / kWaveSize;
-    const int r0 = w * kRows;
-    int row[kRows];
-#pragma unroll
-    for (int r = 0; r < kRows; ++r)
-        row[r] = r0 + r < out ? r0 + r : 0;
-    float y[kRows];
-    block_gemv<kV>(x, nullptr, 0.f, W, row, r0 < out, nullptr, y);
-    if (r0 < out && lane == 0) {
+    if constexpr (kV % 4 == 0) { // in >= 1024: 4 rows per workgroup, columns split across the waves
+        const int r0 = blockIdx.x * kRows;
+        int row[kRows];
 #pragma unroll
         for (int r = 0; r < kRows; ++r)
-            if (r0 + r < out)
-                hidden[r0 + r] += y[r];
+            row[r] = r0 + r < out ? r0 + r : r0;
+        float y[kRows];
+        block_gemv_split<kV>(x, W, row, y);
+        if (threadIdx.x < kRows && r0 + threadIdx.x < out) {
+            float v = y[0];
+#pragma unroll
+            for (int r = 1; r < kRows; ++r)
+                v = threadIdx.x == r ? y[r] : v;
+            hidden[r0 + threadIdx.x] += v;
+        }
+    } else { // one row per wave
+        const int r = blockIdx.x * kWavesPerBlock + threadIdx.x / kWaveSize;
+        const bool active = r < out;
+        const int row[1] = {active ? r : 0};
+        float y[1];
+        block_gemv<kV, 1>(x, nullptr, 0.f, W, row, active, nullptr, y);
+        if (active && threadIdx.x % kWaveSize == 0)
+            hidden[r] += y[0];
     }
 }
 
 // ---- 4. act = silu(gate) * up, interleaved [gate_i; up_i] rows ----------------
+// Workgroup b computes pairs 2b and 2b + 1, one row per wave (rows 4b .. 4b+3).
 template <int kV>
 __global__ __launch_bounds__(kBlock) void swiglu_gemv_kernel(const float *__restrict__ hidden,
                                                              const float *__restrict__ gamma, float eps,
                                                              const float *__restrict__ wgu, float *__restrict__ act,
                                                              int inter) {
-    const int lane = threadIdx.x % kWaveSize;
-    const int w = blockIdx.x * kWavesPerBlock + threadIdx.x / kWaveSize;
-    const int i0 = w * (kRows / 2); // two (gate, up) pairs per wave
-    const bool active = i0 < inter;
-    const int b = active ? i0 : 0;
-    const int row[kRows] = {2 * b, 2 * b + 1, 2 * b + 2, 2 * b + 3};
-    float y[kRows];
-    block_gemv<kV>(hidden, gamma, eps, wgu, row, active, nullptr, y);
-    if (active && lane == 0) {
-        act[i0] = y[0] / (1.f + expf(-y[0])) * y[1];
-        act[i0 + 1] = y[2] / (1.f + expf(-y[2])) * y[3];
+    __shared__ float res[kWavesPerBlock];
+    const int wave = threadIdx.x / kWaveSize;
+    const int r = blockIdx.x * kWavesPerBlock + wave;
+    const bool active = r < 2 * inter;
+    const int row[1] = {active ? r : 0};
+    float y[1];
+    block_gemv<kV, 1>(hidden, gamma, eps, wgu, row, active, nullptr, y);
+    if (threadIdx.x % kWaveSize == 0)
+        res[wave] = y[0];
+    __syncthreads();
+    const int i = 2 * blockIdx.x + threadIdx.x;
+    if (threadIdx.x < 2 && i < inter) {
+        const float g = res[2 * threadIdx.x], u = res[2 * threadIdx.x + 1];
+        act[i] = g / (1.f + expf(-g)) * u;
     }
 }
 

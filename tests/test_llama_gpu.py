@@ -22,6 +22,11 @@ SMALL = dict(num_hidden_layers=4, hidden_size=512, intermediate_size=2048, num_a
              num_key_value_heads=2, head_dim=64, vocab_size=1000, rms_norm_eps=1e-5, rope_theta=500000.0,
              rope_scaling={"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
                            "original_max_position_embeddings": 8192}, eos_token_id=[1])
+# hidden >= 1024 selects the column-split qkv / o_proj GEMV kernels
+MID = dict(num_hidden_layers=3, hidden_size=1024, intermediate_size=2048, num_attention_heads=16,
+           num_key_value_heads=4, head_dim=64, vocab_size=3000, rms_norm_eps=1e-5, rope_theta=500000.0,
+           rope_scaling={"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                         "original_max_position_embeddings": 8192}, eos_token_id=[1])
 SEED = 2024
 
 
@@ -48,6 +53,13 @@ def small(ow):
     from opworks_amd.llama import LlamaModel
     from tests import oracle as orc
     return LlamaModel.load_random(SMALL, SEED + 1, 0.02, "uniform"), orc.Llama(SMALL, SEED + 1, 0.02, "uniform")
+
+
+@pytest.fixture(scope="module")
+def mid(ow):
+    from opworks_amd.llama import LlamaModel
+    from tests import oracle as orc
+    return LlamaModel.load_random(MID, SEED + 2, 0.02, "uniform"), orc.Llama(MID, SEED + 2, 0.02, "uniform")
 
 
 def prompt(n, vocab, seed):
@@ -89,12 +101,15 @@ def greedy_compare(gpu, cpu, ids, steps, cap):
     return got, want, worst
 
 
-@pytest.mark.parametrize("fixture,n,steps", [("tiny", 5, 40), ("tiny", 1, 20), ("small", 64, 48)])
+@pytest.mark.parametrize("fixture,n,steps", [("tiny", 5, 40), ("tiny", 1, 20), ("small", 64, 48), ("mid", 1, 24),
+                                             ("mid", 37, 40)])
 def test_greedy_matches_oracle(request, fixture, n, steps):
     gpu, cpu = request.getfixturevalue(fixture)
-    cfg = TINY if fixture == "tiny" else SMALL
+    cfg = {"tiny": TINY, "small": SMALL, "mid": MID}[fixture]
     got, want, _ = greedy_compare(gpu, cpu, prompt(n, cfg["vocab_size"], 99 + n), steps, 256)
-    assert got == want
+    # identical ids; a divergence is accepted only at a near tie (< 1e-3, asserted
+    # inside greedy_compare), after which the sequences are not compared further
+    assert got[:-1] == want[:-1] and (got[-1] == want[-1] or len(got) < steps)
 
 
 @pytest.mark.parametrize("L", [1, 2, 31, 32, 33, 64, 65, 127, 128, 129])
