@@ -374,20 +374,24 @@ __global__ __launch_bounds__(16 * kWaveSize) static void decode_combine_kernel(D
     const float w0 = lane < nchunks ? expf(m0 - M) : 0.f;
     const float w1 = lane + kWaveSize < nchunks ? expf(m1 - M) : 0.f;
     const float L = wave::sum(l0 * w0 + l1 * w1);
-    if (lane >= D)
-        return;
-    float acc0 = 0.f, acc1 = 0.f;
-    int c = 0;
-    for (; c + 1 < nchunks; c += 2) {
-        const float wa = wave::readlane(c < kWaveSize ? w0 : w1, c % kWaveSize);
-        const float wb = wave::readlane(c + 1 < kWaveSize ? w0 : w1, (c + 1) % kWaveSize);
-        acc0 = fmaf(base[int64_t(c) * (D + 2) + 2 + lane], wa, acc0);
-        acc1 = fmaf(base[int64_t(c + 1) * (D + 2) + 2 + lane], wb, acc1);
+    // lane = head-dim element; the chunk rows are fetched 16 at a time, every
+    // load of a batch issued before its FMAs (one L2 round trip per batch)
+    constexpr int kBatch = 16;
+    float acc = 0.f;
+    for (int c0 = 0; c0 < nchunks; c0 += kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+            v[j] = c0 + j < nchunks && lane < D ? base[int64_t(c0 + j) * (D + 2) + 2 + lane] : 0.f;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int c = c0 + j;
+            const float wc = wave::readlane(c < kWaveSize ? w0 : w1, c % kWaveSize);
+            acc = c < nchunks ? fmaf(v[j], wc, acc) : acc;
+        }
     }
-    if (c < nchunks)
-        acc0 = fmaf(base[int64_t(c) * (D + 2) + 2 + lane], wave::readlane(c < kWaveSize ? w0 : w1, c % kWaveSize),
-                    acc0);
-    a.out[int64_t(h) * D + lane] = L > 0.f ? (acc0 + acc1) / L : 0.f;
+    if (lane < D)
+        a.out[int64_t(h) * D + lane] = L > 0.f ? acc / L : 0.f;
 }
 
 // ---- 3. hidden += W x (in = H) -----------------------------------------------
