@@ -21,6 +21,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstddef>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -543,27 +544,16 @@ class LlamaModel {
         aa.vcache = layer_v(s, l);
         aa.out = s.d_attn.data();
         aa.partial = s.attn_partial.data();
-        aa.state = s.state();
+        aa.len_ptr = s.state_buf.data() + offsetof(llama::StepState, pos) / sizeof(int32_t); // length pos + 1
+        aa.len_bias = 1;
         aa.kv_rep = cfg_.kv_rep();
         aa.D = D;
         aa.cap = s.max_seq_len;
         aa.max_chunks = s.attn_max_chunks;
         aa.scale = 1.f / std::sqrt(static_cast<float>(D));
-        const int rep = cfg_.kv_rep();
-        const dim3 agrid(kvh, s.attn_max_chunks);
         if (stage_on(1)) {
             tick();
-            if (rep <= 1)
-                launch_async(st, llama::decode_attention_kernel<1>, agrid, kWaveSize, aa);
-            else if (rep <= 2)
-                launch_async(st, llama::decode_attention_kernel<2>, agrid, 2 * kWaveSize, aa);
-            else if (rep <= 4)
-                launch_async(st, llama::decode_attention_kernel<4>, agrid, 4 * kWaveSize, aa);
-            else if (rep <= 8)
-                launch_async(st, llama::decode_attention_kernel<8>, agrid, 8 * kWaveSize, aa);
-            else
-                launch_async(st, llama::decode_attention_kernel<16>, agrid, 16 * kWaveSize, aa);
-            launch_async(st, llama::decode_combine_kernel, kvh, rep * kWaveSize, aa);
+            detail::attention_decode_launch(aa, kvh, st);
         }
         if (stage_on(2)) {
             tick();

@@ -245,154 +245,9 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(QkvArgs a) {
 }
 
 // ---- 2. decode attention: split-KV partials + combine ---------------------
-// Partial kernel: grid (kvh, max_chunks), block kWaves waves (kWaves = kv_rep
-// rounded up to a power of two; extra waves only stage K/V). Records
-// [qh][max_chunks][D + 2] hold (max, sum, unnormalised output) per chunk.
-// Combine kernel: one workgroup per kv head, one wave per q head.
-struct DecodeAttnArgs {
-    const float *q;                  // [qh][D]
-    const float *kcache, *vcache;    // [kvh][cap][D]
-    float *out;                      // [qh][D]
-    float *partial;                  // [qh][max_chunks][D + 2]
-    const StepState *state;          // len = pos + 1
-    int kv_rep, D, cap, max_chunks;
-    float scale;
-};
-
-__device__ __forceinline__ int decode_len(const DecodeAttnArgs &a) {
-    int len = a.state->pos + 1;
-    len = len < a.cap ? len : a.cap;
-    return len < a.max_chunks * detail::kAttnChunk ? len : a.max_chunks * detail::kAttnChunk;
-}
-
-template <int kWaves>
-__global__ __launch_bounds__(kWaves *kWaveSize) void decode_attention_kernel(DecodeAttnArgs a) {
-    constexpr int C = detail::kAttnChunk;
-    const int len = decode_len(a);
-    const int nchunks = (len + C - 1) / C;
-    const int kvh = blockIdx.x, chunk = blockIdx.y;
-    if (chunk >= nchunks)
-        return;
-    const int k0 = chunk * C;
-    const int n = len - k0 < C ? len - k0 : C;
-    const int D = a.D;
-    __shared__ __attribute__((aligned(16))) float Ks[C][64 + 4];
-    __shared__ __attribute__((aligned(16))) float Vs[C][64];
-    __shared__ __attribute__((aligned(16))) float Qs[kWaves][64];
-    __shared__ __attribute__((aligned(16))) float Ps[kWaves][C];
-    const float *kh = a.kcache + (int64_t(kvh) * a.cap + k0) * D;
-    const float *vh = a.vcache + (int64_t(kvh) * a.cap + k0) * D;
-    const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
-    const bool head_ok = wave < a.kv_rep;
-    const int h = kvh * a.kv_rep + (head_ok ? wave : 0);
-    {
-        // 16-byte chunks of the K/V rows; every load of the thread is issued before the LDS stores
-        constexpr int kMaxPer = C * 64 / 4 / (kWaves * kWaveSize);
-        constexpr int nthreads = kWaves * kWaveSize;
-        const int chunks = C * D / 4;
-        f32x4 kv[kMaxPer], vv[kMaxPer];
-#pragma unroll
-        for (int i = 0; i < kMaxPer; ++i) {
-            const int c = threadIdx.x + i * nthreads;
-            const int r = (4 * c) / D;
-            kv[i] = vv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (c < chunks && r < n) {
-                kv[i] = reinterpret_cast<const f32x4 *>(kh)[c];
-                vv[i] = reinterpret_cast<const f32x4 *>(vh)[c];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < kMaxPer; ++i) {
-            const int c = threadIdx.x + i * nthreads;
-            if (c < chunks) {
-                const int r = (4 * c) / D, d = (4 * c) % D;
-                *reinterpret_cast<f32x4 *>(&Ks[r][d]) = kv[i];
-                *reinterpret_cast<f32x4 *>(&Vs[r][d]) = vv[i];
-            }
-        }
-    }
-    if (lane < D)
-        Qs[wave][lane] = a.q[int64_t(h) * D + lane];
-    __syncthreads();
-    // lane = key; four partial dot products break the FMA chain
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-    for (int d = 0; d < D; d += 4) {
-        const f32x4 kv = *reinterpret_cast<const f32x4 *>(&Ks[lane][d]);
-        const f32x4 qv = *reinterpret_cast<const f32x4 *>(&Qs[wave][d]);
-        s0 = fmaf(qv[0], kv[0], s0);
-        s1 = fmaf(qv[1], kv[1], s1);
-        s2 = fmaf(qv[2], kv[2], s2);
-        s3 = fmaf(qv[3], kv[3], s3);
-    }
-    const float s = lane < n ? ((s0 + s1) + (s2 + s3)) * a.scale : kNegInf;
-    const float m = wave::max(s);
-    const float p = lane < n ? expf(s - m) : 0.f;
-    const float l = wave::sum(p);
-    Ps[wave][lane] = p;
-    __builtin_amdgcn_wave_barrier();
-    // lane = head-dim element; keys past n have p = 0 and zero V rows
-    if (lane < D) {
-        float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
-#pragma unroll 4
-        for (int key = 0; key < C; key += 4) {
-            const f32x4 pv = *reinterpret_cast<const f32x4 *>(&Ps[wave][key]);
-            o0 = fmaf(pv[0], Vs[key][lane], o0);
-            o1 = fmaf(pv[1], Vs[key + 1][lane], o1);
-            o2 = fmaf(pv[2], Vs[key + 2][lane], o2);
-            o3 = fmaf(pv[3], Vs[key + 3][lane], o3);
-        }
-        if (head_ok) {
-            float *rec = a.partial + (int64_t(h) * a.max_chunks + chunk) * (D + 2);
-            if (lane == 0) {
-                rec[0] = m;
-                rec[1] = l;
-            }
-            rec[2 + lane] = (o0 + o1) + (o2 + o3);
-        }
-    }
-}
-
-// grid kvh, block kv_rep waves; wave w merges q head kvh * kv_rep + w.
-__global__ __launch_bounds__(16 * kWaveSize) static void decode_combine_kernel(DecodeAttnArgs a) {
-    constexpr int C = detail::kAttnChunk;
-    const int len = decode_len(a);
-    const int nchunks = (len + C - 1) / C; // <= max_chunks <= 128
-    const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
-    const int h = blockIdx.x * a.kv_rep + wave;
-    const int D = a.D;
-    const float *base = a.partial + int64_t(h) * a.max_chunks * (D + 2);
-    float m0 = kNegInf, l0 = 0.f, m1 = kNegInf, l1 = 0.f;
-    if (lane < nchunks) {
-        m0 = base[int64_t(lane) * (D + 2)];
-        l0 = base[int64_t(lane) * (D + 2) + 1];
-    }
-    if (lane + kWaveSize < nchunks) {
-        m1 = base[int64_t(lane + kWaveSize) * (D + 2)];
-        l1 = base[int64_t(lane + kWaveSize) * (D + 2) + 1];
-    }
-    const float M = wave::max(fmaxf(m0, m1));
-    const float w0 = lane < nchunks ? expf(m0 - M) : 0.f;
-    const float w1 = lane + kWaveSize < nchunks ? expf(m1 - M) : 0.f;
-    const float L = wave::sum(l0 * w0 + l1 * w1);
-    // lane = head-dim element; the chunk rows are fetched 16 at a time, every
-    // load of a batch issued before its FMAs (one L2 round trip per batch)
-    constexpr int kBatch = 16;
-    float acc = 0.f;
-    for (int c0 = 0; c0 < nchunks; c0 += kBatch) {
-        float v[kBatch];
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j)
-            v[j] = c0 + j < nchunks && lane < D ? base[int64_t(c0 + j) * (D + 2) + 2 + lane] : 0.f;
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            const int c = c0 + j;
-            const float wc = wave::readlane(c < kWaveSize ? w0 : w1, c % kWaveSize);
-            acc = c < nchunks ? fmaf(v[j], wc, acc) : acc;
-        }
-    }
-    if (lane < D)
-        a.out[int64_t(h) * D + lane] = L > 0.f ? acc / L : 0.f;
-}
+// ops/attention.hpp's decode kernels with the length read from the step
+// state on the device (len = pos + 1), so the captured graph replays it.
+using detail::DecodeAttnArgs;
 
 // ---- 3. hidden += W x (in = H) -----------------------------------------------
 template <int kV>

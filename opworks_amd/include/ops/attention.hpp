@@ -275,77 +275,173 @@ inline int attention_decode_workspace_floats(int num_q_heads, int max_len, int h
     return num_q_heads * chunks * (head_dim + 2);
 }
 
-// grid = num_kv_heads x max_chunks; block = kv_rep waves.
-__global__ __launch_bounds__(kAttnMaxRep *kWaveSize) static void attention_decode_partial_kernel(
-    const float *__restrict__ q, const float *__restrict__ kcache, const float *__restrict__ vcache,
-    float *__restrict__ partial, int len_value, const int *__restrict__ len_ptr, int len_bias, int head_dim,
-    int kv_rep, int cap, int max_chunks, float scale) {
-    int len = len_ptr ? *len_ptr + len_bias : len_value;
-    len = len < max_chunks * kAttnChunk ? len : max_chunks * kAttnChunk; // never past the grid / workspace
-    len = len < cap ? len : cap;
+// Split-KV decode ("flash-decoding"): one workgroup per (kv head, chunk of
+// kAttnChunk keys) stages the chunk's K/V rows in LDS with 16-byte loads
+// (all issued before the LDS stores); wave w handles q head kvh * kv_rep + w:
+// lane = key for the scores (four partial dot products), then lane = head-dim
+// element for P V. Each chunk leaves a record (max, sum, unnormalised
+// output[D]); the combine kernel (one wave per q head) merges a head's
+// records in chunk order: M = max m_c, L = sum l_c e^(m_c - M),
+// out = sum acc_c e^(m_c - M) / L, loading 16 chunk rows per round trip.
+// The length is a host value or, for graph replay, read on the device.
+struct DecodeAttnArgs {
+    const float *q;               // [qh][D]
+    const float *kcache, *vcache; // [kvh][cap][D]
+    float *out;                   // [qh][D]
+    float *partial;               // [qh][max_chunks][D + 2]
+    const int *len_ptr;           // if set, length = *len_ptr + len_bias
+    int len, len_bias;
+    int kv_rep, D, cap, max_chunks;
+    float scale;
+};
+
+__device__ __forceinline__ int decode_len(const DecodeAttnArgs &a) {
+    int len = a.len_ptr ? *a.len_ptr + a.len_bias : a.len;
+    len = len < a.cap ? len : a.cap;
+    return len < a.max_chunks * kAttnChunk ? len : a.max_chunks * kAttnChunk;
+}
+
+template <int kWaves>
+__global__ __launch_bounds__(kWaves *kWaveSize) void attention_decode_partial_kernel(DecodeAttnArgs a) {
+    constexpr int C = kAttnChunk;
+    const int len = decode_len(a);
+    const int nchunks = (len + C - 1) / C;
     const int kvh = blockIdx.x, chunk = blockIdx.y;
-    const int k0 = chunk * kAttnChunk;
-    if (k0 >= len)
+    if (chunk >= nchunks)
         return;
-    const int n = len - k0 < kAttnChunk ? len - k0 : kAttnChunk;
-    __shared__ float Ks[kAttnChunk][kAttnMaxD + 1];
-    __shared__ __attribute__((aligned(16))) float Vs[kAttnChunk][kAttnMaxD];
-    const float *kh = kcache + (int64_t(kvh) * cap + k0) * head_dim;
-    const float *vh = vcache + (int64_t(kvh) * cap + k0) * head_dim;
-    for (int i = threadIdx.x; i < n * head_dim; i += blockDim.x) {
-        const int r = i / head_dim, d = i % head_dim;
-        Ks[r][d] = kh[i];
-        Vs[r][d] = vh[i];
-    }
+    const int k0 = chunk * C;
+    const int n = len - k0 < C ? len - k0 : C;
+    const int D = a.D;
+    __shared__ __attribute__((aligned(16))) float Ks[C][kAttnMaxD + 4];
+    __shared__ __attribute__((aligned(16))) float Vs[C][kAttnMaxD];
+    __shared__ __attribute__((aligned(16))) float Qs[kWaves][kAttnMaxD];
+    __shared__ __attribute__((aligned(16))) float Ps[kWaves][C];
+    const float *kh = a.kcache + (int64_t(kvh) * a.cap + k0) * D;
+    const float *vh = a.vcache + (int64_t(kvh) * a.cap + k0) * D;
     const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
-    const int h = kvh * kv_rep + wave;
-    // lane d keeps q[h][d]; dot products broadcast q[d] with readlane
-    const float qd = lane < head_dim ? q[int64_t(h) * head_dim + lane] : 0.f;
+    const bool head_ok = wave < a.kv_rep;
+    const int h = kvh * a.kv_rep + (head_ok ? wave : 0);
+    {
+        constexpr int kMaxPer = C * kAttnMaxD / 4 / (kWaves * kWaveSize);
+        constexpr int nthreads = kWaves * kWaveSize;
+        const int packs = C * D / 4;
+        f32x4 kv[kMaxPer], vv[kMaxPer];
+#pragma unroll
+        for (int i = 0; i < kMaxPer; ++i) {
+            const int c = threadIdx.x + i * nthreads;
+            const int r = (4 * c) / D;
+            kv[i] = vv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (c < packs && r < n) {
+                kv[i] = reinterpret_cast<const f32x4 *>(kh)[c];
+                vv[i] = reinterpret_cast<const f32x4 *>(vh)[c];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kMaxPer; ++i) {
+            const int c = threadIdx.x + i * nthreads;
+            if (c < packs) {
+                const int r = (4 * c) / D, d = (4 * c) % D;
+                *reinterpret_cast<f32x4 *>(&Ks[r][d]) = kv[i];
+                *reinterpret_cast<f32x4 *>(&Vs[r][d]) = vv[i];
+            }
+        }
+    }
+    if (lane < D)
+        Qs[wave][lane] = a.q[int64_t(h) * D + lane];
     __syncthreads();
-    // lane = key within the chunk
-    float s = 0.f;
-    for (int d = 0; d < head_dim; ++d)
-        s = fmaf(wave::readlane(qd, d), Ks[lane < n ? lane : 0][d], s);
-    s = lane < n ? s * scale : kNegInf;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    for (int d = 0; d < D; d += 4) {
+        const f32x4 kq = *reinterpret_cast<const f32x4 *>(&Ks[lane][d]);
+        const f32x4 qv = *reinterpret_cast<const f32x4 *>(&Qs[wave][d]);
+        s0 = fmaf(qv[0], kq[0], s0);
+        s1 = fmaf(qv[1], kq[1], s1);
+        s2 = fmaf(qv[2], kq[2], s2);
+        s3 = fmaf(qv[3], kq[3], s3);
+    }
+    const float s = lane < n ? ((s0 + s1) + (s2 + s3)) * a.scale : kNegInf;
     const float m = wave::max(s);
     const float p = lane < n ? expf(s - m) : 0.f;
     const float l = wave::sum(p);
-    // lane = head-dim element: o[d] = sum_key p[key] V[key][d]
-    float o = 0.f;
-    for (int key = 0; key < n; ++key)
-        o = fmaf(wave::readlane(p, key), Vs[key][lane < head_dim ? lane : 0], o);
-    float *rec = partial + (int64_t(h) * max_chunks + chunk) * (head_dim + 2);
-    if (lane == 0) {
-        rec[0] = m;
-        rec[1] = l;
+    Ps[wave][lane] = p;
+    __builtin_amdgcn_wave_barrier();
+    // lane = head-dim element; keys past n have p = 0 and zero V rows
+    if (lane < D) {
+        float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+#pragma unroll 4
+        for (int key = 0; key < C; key += 4) {
+            const f32x4 pv = *reinterpret_cast<const f32x4 *>(&Ps[wave][key]);
+            o0 = fmaf(pv[0], Vs[key][lane], o0);
+            o1 = fmaf(pv[1], Vs[key + 1][lane], o1);
+            o2 = fmaf(pv[2], Vs[key + 2][lane], o2);
+            o3 = fmaf(pv[3], Vs[key + 3][lane], o3);
+        }
+        if (head_ok) {
+            float *rec = a.partial + (int64_t(h) * a.max_chunks + chunk) * (D + 2);
+            if (lane == 0) {
+                rec[0] = m;
+                rec[1] = l;
+            }
+            rec[2 + lane] = (o0 + o1) + (o2 + o3);
+        }
     }
-    if (lane < head_dim)
-        rec[2 + lane] = o;
 }
 
-// grid = num_q_heads; block = 64 (lane = head-dim element).
-__global__ __launch_bounds__(kWaveSize) static void attention_decode_combine_kernel(
-    const float *__restrict__ partial, float *__restrict__ out, int len_value, const int *__restrict__ len_ptr,
-    int len_bias, int head_dim, int max_chunks) {
-    // (the partial kernel clamps len to the cache capacity the same way before writing records)
-    int len = len_ptr ? *len_ptr + len_bias : len_value;
-    len = len < max_chunks * kAttnChunk ? len : max_chunks * kAttnChunk;
-    const int h = blockIdx.x, lane = threadIdx.x;
-    const int chunks = (len + kAttnChunk - 1) / kAttnChunk;
-    const float *base = partial + int64_t(h) * max_chunks * (head_dim + 2);
-    float M = kNegInf;
-    for (int c = 0; c < chunks; ++c)
-        M = fmaxf(M, base[c * (head_dim + 2)]);
-    float L = 0.f, o = 0.f;
-    for (int c = 0; c < chunks; ++c) {
-        const float *rec = base + c * (head_dim + 2);
-        const float w = expf(rec[0] - M);
-        L = fmaf(rec[1], w, L);
-        if (lane < head_dim)
-            o = fmaf(rec[2 + lane], w, o);
+// grid kvh, block kv_rep waves; wave w merges q head kvh * kv_rep + w.
+__global__ __launch_bounds__(kAttnMaxRep *kWaveSize) static void attention_decode_combine_kernel(DecodeAttnArgs a) {
+    constexpr int C = kAttnChunk;
+    const int len = decode_len(a);
+    const int nchunks = (len + C - 1) / C; // <= max_chunks <= 2 * kWaveSize
+    const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
+    const int h = blockIdx.x * a.kv_rep + wave;
+    const int D = a.D;
+    const float *base = a.partial + int64_t(h) * a.max_chunks * (D + 2);
+    float m0 = kNegInf, l0 = 0.f, m1 = kNegInf, l1 = 0.f;
+    if (lane < nchunks) {
+        m0 = base[int64_t(lane) * (D + 2)];
+        l0 = base[int64_t(lane) * (D + 2) + 1];
     }
-    if (lane < head_dim)
-        out[int64_t(h) * head_dim + lane] = L > 0.f ? o / L : 0.f;
+    if (lane + kWaveSize < nchunks) {
+        m1 = base[int64_t(lane + kWaveSize) * (D + 2)];
+        l1 = base[int64_t(lane + kWaveSize) * (D + 2) + 1];
+    }
+    const float M = wave::max(fmaxf(m0, m1));
+    const float w0 = lane < nchunks ? expf(m0 - M) : 0.f;
+    const float w1 = lane + kWaveSize < nchunks ? expf(m1 - M) : 0.f;
+    const float L = wave::sum(l0 * w0 + l1 * w1);
+    constexpr int kBatch = 16;
+    float acc = 0.f;
+    for (int c0 = 0; c0 < nchunks; c0 += kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+            v[j] = c0 + j < nchunks && lane < D ? base[int64_t(c0 + j) * (D + 2) + 2 + lane] : 0.f;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int c = c0 + j;
+            const float wc = wave::readlane(c < kWaveSize ? w0 : w1, c % kWaveSize);
+            acc = c < nchunks ? fmaf(v[j], wc, acc) : acc;
+        }
+    }
+    if (lane < D)
+        a.out[int64_t(h) * D + lane] = L > 0.f ? acc / L : 0.f;
+}
+
+// Enqueues the partial and combine kernels: grid (kvh, max_chunks) with
+// kv_rep rounded up to a power of two waves per workgroup.
+inline void attention_decode_launch(const DecodeAttnArgs &a, int kvh, hipStream_t stream) {
+    const dim3 grid(kvh, a.max_chunks);
+    const int rep = a.kv_rep;
+    if (rep <= 1)
+        launch_async(stream, attention_decode_partial_kernel<1>, grid, kWaveSize, a);
+    else if (rep <= 2)
+        launch_async(stream, attention_decode_partial_kernel<2>, grid, 2 * kWaveSize, a);
+    else if (rep <= 4)
+        launch_async(stream, attention_decode_partial_kernel<4>, grid, 4 * kWaveSize, a);
+    else if (rep <= 8)
+        launch_async(stream, attention_decode_partial_kernel<8>, grid, 8 * kWaveSize, a);
+    else
+        launch_async(stream, attention_decode_partial_kernel<16>, grid, 16 * kWaveSize, a);
+    launch_async(stream, attention_decode_combine_kernel, kvh, rep * kWaveSize, a);
 }
 
 } // namespace opworks::detail
@@ -401,12 +497,24 @@ inline void attention_decode_ws(const float *q, const float *kcache, const float
     detail::require(q && kcache && vcache && out && workspace, "attention_decode requires non-null pointers");
     const int max_chunks = (bound + detail::kAttnChunk - 1) / detail::kAttnChunk;
     detail::require(workspace_size >= num_q_heads * max_chunks * (head_dim + 2), "attention_decode workspace is too small");
-    const float scale = 1.f / std::sqrt(static_cast<float>(head_dim));
-    launch_async(stream, detail::attention_decode_partial_kernel, dim3(num_q_heads / kv_rep, max_chunks),
-                 kv_rep * kWaveSize, q, kcache, vcache, workspace, len, len_ptr, len_bias, head_dim, kv_rep, max_seq,
-                 max_chunks, scale);
-    launch_async(stream, detail::attention_decode_combine_kernel, num_q_heads, kWaveSize, workspace, out, len,
-                 len_ptr, len_bias, head_dim, max_chunks);
+    detail::require(head_dim % 4 == 0, "attention_decode needs head_dim to be a multiple of 4");
+    detail::require(detail::aligned16(q) && detail::aligned16(kcache) && detail::aligned16(vcache),
+                    "attention_decode needs 16-byte aligned q and caches");
+    detail::DecodeAttnArgs a{};
+    a.q = q;
+    a.kcache = kcache;
+    a.vcache = vcache;
+    a.out = out;
+    a.partial = workspace;
+    a.len_ptr = len_ptr;
+    a.len = len;
+    a.len_bias = len_bias;
+    a.kv_rep = kv_rep;
+    a.D = head_dim;
+    a.cap = max_seq;
+    a.max_chunks = max_chunks;
+    a.scale = 1.f / std::sqrt(static_cast<float>(head_dim));
+    detail::attention_decode_launch(a, num_q_heads / kv_rep, stream);
 }
 
 // Reference signature (include/ops/attention_decode.cuh:99-109): scratch comes

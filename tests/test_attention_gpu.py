@@ -81,6 +81,24 @@ def test_config4_prefill_full_size_sampled(ow, orc):
     run_prefill(ow, orc, T, T, qh, qh // kvh, D, T, rows=rows, data=(q, k, v))
 
 
+@pytest.mark.parametrize("qh,kv_rep,D", [(8, 1, 32), (16, 16, 64), (6, 3, 48), (8, 8, 16), (12, 2, 64)])
+@pytest.mark.parametrize("length", [1, 100, 1000])
+def test_decode_head_shapes(ow, orc, qh, kv_rep, D, length):
+    """Other GQA ratios (kv_rep 3 rounds up to 4 waves) and head sizes."""
+    cap = 1024
+    kvh = qh // kv_rep
+    q = orc.fill_normal(qh * D, SEED, 20, 0.0, 1.0)
+    k = orc.fill_normal(kvh * cap * D, SEED, 21, 0.0, 1.0)
+    v = orc.fill_normal(kvh * cap * D, SEED, 22, 0.0, 1.0)
+    dq, dk, dv = upload(ow, q), upload(ow, k), upload(ow, v)
+    out = ow.DeviceBuffer.empty(qh * D)
+    ow.ops.attention_decode(dq, dk, dv, out, qh, kv_rep, D, length, cap)
+    got = out.to_host().reshape(qh, D)
+    ref = orc.attention_decode(q, k, v, qh, kv_rep, D, length, cap)
+    _, bound = orc.attention_explicit(q, k, v, 1, length, qh, kv_rep, D, cap)
+    check(got, ref, bound[:, 0])
+
+
 @pytest.mark.parametrize("length,cap", [(1, 1), (2, 8), (63, 64), (64, 64), (65, 128), (767, 1024), (2048, 2048),
                                         (8192, 8192)])
 @pytest.mark.parametrize("use_ws", [False, True])
