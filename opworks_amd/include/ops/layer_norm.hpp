@@ -9,7 +9,7 @@
 
 namespace opworks::detail {
 
-template <int kW, int kV>
+template <int kW, int kV, bool kExact>
 __global__ __launch_bounds__(RowShape<kW>::kBlock) void layer_norm_reg_kernel(
     const float *__restrict__ in, float *__restrict__ out, const float *__restrict__ gamma,
     const float *__restrict__ beta, int rows, int cols, float eps) {
@@ -21,7 +21,7 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void layer_norm_reg_kernel(
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
         const int q = pack_index<kW>(p, k);
-        if (p.active && q < n4) {
+        if (p.active && (kExact || q < n4)) {
             x[k] = __builtin_nontemporal_load(src + q);
             local += (x[k][0] + x[k][1]) + (x[k][2] + x[k][3]);
         }
@@ -31,7 +31,7 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void layer_norm_reg_kernel(
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
         const int q = pack_index<kW>(p, k);
-        if (p.active && q < n4) {
+        if (p.active && (kExact || q < n4)) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float d = x[k][j] - mean;
@@ -46,7 +46,7 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void layer_norm_reg_kernel(
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
         const int q = pack_index<kW>(p, k);
-        if (p.active && q < n4) {
+        if (p.active && (kExact || q < n4)) {
             const f32x4 g = g4[q], b = b4[q];
             f32x4 r;
 #pragma unroll
@@ -95,7 +95,9 @@ inline void layer_norm(const float *in, float *out, const float *gamma, const fl
     }
     detail::dispatch_row_plan(plan, [&](auto w, auto v) {
         constexpr int kW = decltype(w)::value, kV = decltype(v)::value;
-        launch_async(stream, detail::layer_norm_reg_kernel<kW, kV>, detail::row_grid<kW>(rows),
+        auto *kernel = detail::row_plan_exact<kW, kV>(cols) ? detail::layer_norm_reg_kernel<kW, kV, true>
+                                                              : detail::layer_norm_reg_kernel<kW, kV, false>;
+        launch_async(stream, kernel, detail::row_grid<kW>(rows),
                      detail::RowShape<kW>::kBlock, in, out, gamma, beta, rows, cols, eps);
     });
 }

@@ -7,7 +7,7 @@
 
 namespace opworks::detail {
 
-template <int kW, int kV>
+template <int kW, int kV, bool kExact>
 __global__ __launch_bounds__(RowShape<kW>::kBlock) void rms_norm_reg_kernel(const float *__restrict__ x,
                                                                              const float *__restrict__ weight,
                                                                              float *__restrict__ out, int rows,
@@ -20,7 +20,7 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void rms_norm_reg_kernel(cons
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
         const int q = pack_index<kW>(p, k);
-        if (p.active && q < n4) {
+        if (p.active && (kExact || q < n4)) {
             v[k] = __builtin_nontemporal_load(src + q);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -33,7 +33,7 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void rms_norm_reg_kernel(cons
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
         const int q = pack_index<kW>(p, k);
-        if (p.active && q < n4) {
+        if (p.active && (kExact || q < n4)) {
             const f32x4 w = w4[q];
             f32x4 r;
 #pragma unroll
@@ -79,7 +79,9 @@ inline void rms_norm(const float *x, const float *weight, float *out, int rows, 
     }
     detail::dispatch_row_plan(plan, [&](auto w, auto v) {
         constexpr int kW = decltype(w)::value, kV = decltype(v)::value;
-        launch_async(stream, detail::rms_norm_reg_kernel<kW, kV>, detail::row_grid<kW>(rows),
+        auto *kernel = detail::row_plan_exact<kW, kV>(cols) ? detail::rms_norm_reg_kernel<kW, kV, true>
+                                                              : detail::rms_norm_reg_kernel<kW, kV, false>;
+        launch_async(stream, kernel, detail::row_grid<kW>(rows),
                      detail::RowShape<kW>::kBlock, x, weight, out, rows, cols, eps);
     });
 }

@@ -117,6 +117,11 @@ template <typename Fn> inline void dispatch_row_plan(const RowPlan &plan, Fn &&f
     }
 }
 
+// True when the plan's kW * kV * 64 packs cover the row exactly: the kernels
+// then drop the per-lane bounds test, which keeps every load of a lane in one
+// unpredicated batch.
+template <int kW, int kV> inline bool row_plan_exact(int cols) { return cols / 4 == kW * kV * kWaveSize; }
+
 template <int kW> inline int row_grid(int rows) {
     return static_cast<int>(blocks_for64(rows, RowShape<kW>::kRowsPerBlock));
 }

@@ -2,14 +2,15 @@
 
 // ops::softmax — row-wise softmax over the last dimension of a rows x cols
 // fp32 matrix (reference: include/ops/softmax.cuh:10-43). Per row:
-// m = max_j x_j, s = sum_j expf(x_j - m), out_j = expf(x_j - m) / s.
+// m = max_j x_j, s = sum_j expf(x_j - m), out_j = expf(x_j - m) / s (the
+// register-resident kernel multiplies by 1/s: within 1.5 ulp of the divide).
 // Register-resident rows compute each expf once and read the row once.
 
 #include "rowwise_kernels.hpp"
 
 namespace opworks::detail {
 
-template <int kW, int kV>
+template <int kW, int kV, bool kExact>
 __global__ __launch_bounds__(RowShape<kW>::kBlock) void softmax_rows_reg_kernel(const float *__restrict__ in,
                                                                                  float *__restrict__ out, int rows,
                                                                                  int cols) {
@@ -21,7 +22,7 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void softmax_rows_reg_kernel(
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
         const int q = pack_index<kW>(p, k);
-        if (p.active && q < n4) {
+        if (p.active && (kExact || q < n4)) {
             x[k] = __builtin_nontemporal_load(src + q);
             local_max = fmaxf(local_max, fmaxf(fmaxf(x[k][0], x[k][1]), fmaxf(x[k][2], x[k][3])));
         }
@@ -31,7 +32,7 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void softmax_rows_reg_kernel(
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
         const int q = pack_index<kW>(p, k);
-        if (p.active && q < n4) {
+        if (p.active && (kExact || q < n4)) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 x[k][j] = expf(x[k][j] - m);
@@ -40,15 +41,16 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void softmax_rows_reg_kernel(
         }
     }
     const float s = row_combine<kW>(wave::sum(local_sum), p, wave::Add{});
+    const float inv_s = 1.f / s; // one divide per row; each output is e * (1/s)
     f32x4 *dst = reinterpret_cast<f32x4 *>(out + p.row * cols);
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
         const int q = pack_index<kW>(p, k);
-        if (p.active && q < n4) {
+        if (p.active && (kExact || q < n4)) {
             f32x4 r;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                r[j] = x[k][j] / s;
+                r[j] = x[k][j] * inv_s;
             __builtin_nontemporal_store(r, dst + q);
         }
     }
@@ -86,7 +88,9 @@ inline void softmax(const float *in, float *out, int rows, int cols, hipStream_t
     }
     detail::dispatch_row_plan(plan, [&](auto w, auto v) {
         constexpr int kW = decltype(w)::value, kV = decltype(v)::value;
-        launch_async(stream, detail::softmax_rows_reg_kernel<kW, kV>, detail::row_grid<kW>(rows),
+        auto *kernel = detail::row_plan_exact<kW, kV>(cols) ? detail::softmax_rows_reg_kernel<kW, kV, true>
+                                                              : detail::softmax_rows_reg_kernel<kW, kV, false>;
+        launch_async(stream, kernel, detail::row_grid<kW>(rows),
                      detail::RowShape<kW>::kBlock, in, out, rows, cols);
     });
 }
