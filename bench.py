@@ -221,14 +221,15 @@ def wl_attention_decode(stream, steps, warmup):
             "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
 
 
-def wl_llama(stream, steps, warmup):
+def wl_llama(stream, steps, warmup, bf16=False):
     """Config 5: Llama-3.2-1B architecture, fp32 weights N(0, 0.02) (seeded), RMSNorm gamma = 1, 512
     uniform-random prompt ids, greedy 256 tokens with the KV cache, no EOS stop. A step is one full
     generation through the C ABI's greedy loop; value = 255 decode steps / decode wall time (median over
     steps, after warmup). The roofline is the gate/up GEMV (the largest decode kernel, 134,266,880 B per
     launch) timed with HIP events on the session stream."""
     from opworks_amd.llama import LLAMA_3_2_1B, LlamaModel
-    cfg = dict(LLAMA_3_2_1B)
+    cfg = dict(LLAMA_3_2_1B, torch_dtype="bfloat16") if bf16 else dict(LLAMA_3_2_1B)
+    wb = 2 if bf16 else 4  # bytes per weight
     model = LlamaModel.load_random(cfg, SEED, 0.02, "ones")
     sess = model.session(1024)
     rng = np.random.default_rng(SEED)
@@ -247,9 +248,9 @@ def wl_llama(stream, steps, warmup):
     # kernel time without launch gaps, comparable with rocprofv3's per-kernel average.
     H, I, V, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"], cfg["num_hidden_layers"]
     qkv_w = (cfg["num_attention_heads"] + 2 * cfg["num_key_value_heads"]) * cfg["head_dim"]
-    kernel_bytes = {"qkv_rope": 4 * (qkv_w * H + 2 * H), "o_proj": 4 * (H * H + 3 * H),
-                    "gate_up": 4 * (2 * I * H + 2 * H + I), "down": 4 * (H * I + I + 2 * H),
-                    "lm_head": 4 * (V * H + 2 * H + V)}
+    kernel_bytes = {"qkv_rope": wb * qkv_w * H + 4 * 2 * H, "o_proj": wb * H * H + 4 * 3 * H,
+                    "gate_up": wb * 2 * I * H + 4 * (2 * H + I), "down": wb * H * I + 4 * (I + 2 * H),
+                    "lm_head": wb * V * H + 4 * (2 * H + V)}
     breakdown = {}
     for k in sess.STAGES:
         us = sess.time_decode_stage(k, reps=10)
@@ -258,20 +259,23 @@ def wl_llama(stream, steps, warmup):
             entry["gbs"] = round(kernel_bytes[k] / (us * 1e-6) / 1e9, 1)
         breakdown[k] = entry
     gu_gbs = kernel_bytes["gate_up"] / (breakdown["gate_up"]["avg_us"] * 1e-6) / 1e9
-    weight_bytes = 4 * (V * H + L * (qkv_w * H + H * H + 2 * I * H + H * I) + (2 * L + 1) * H)
+    weight_bytes = wb * (V * H + L * (qkv_w * H + H * H + 2 * I * H + H * I)) + 4 * (2 * L + 1) * H
     kv_bytes_avg = 2 * L * cfg["num_key_value_heads"] * cfg["head_dim"] * 4 * (512 + new_tokens / 2)
     step_gbs = (weight_bytes + kv_bytes_avg) / (dec / (new_tokens - 1) * 1e-3) / 1e9
-    return {"workload": "llama3.2-1b_fp32_greedy_prompt512_gen256", "unit": "tok/s", "value": tok_s,
+    return {"workload": f"llama3.2-1b_{'bf16' if bf16 else 'fp32'}_greedy_prompt512_gen256", "unit": "tok/s",
+            "value": tok_s,
             "ms": pre + dec, "ttft_ms": round(pre, 3), "decode_ms_per_token": round(dec / (new_tokens - 1), 4),
-            "kernel": "swiglu_gemv_kernel<8> (gate/up)",
-            "roofline": roofline(gu_gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("gate_up")),
+            "kernel": f"swiglu_gemv_kernel<8{', bf16' if bf16 else ''}> (gate/up)",
+            "roofline": roofline(gu_gbs, HBM_PEAK_GBS, "GB/s", "hbm",
+                                 traffic=None if bf16 else profiled_traffic("gate_up")),
             "decode_step_roofline": roofline(step_gbs, HBM_PEAK_GBS, "GB/s", "hbm"),
             "weight_bytes_per_token": weight_bytes, "kernels": breakdown,
             "first_tokens": [int(t) for t in runs[-1][2][:8]]}
 
 
 WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "gemm": wl_gemm, "gemm_bf16": wl_gemm_bf16, "attention": wl_attention,
-             "attention_decode": wl_attention_decode, "llama": wl_llama}
+             "attention_decode": wl_attention_decode, "llama": wl_llama,
+             "llama_bf16": lambda st, k, w: wl_llama(st, k, w, bf16=True)}
 HEADLINE = "llama"
 
 

@@ -8,7 +8,9 @@
  * opw_llama_last_error(). A session refers to its model: destroy sessions
  * before freeing the model. One host thread per session at a time.
  *
- * This build runs float32 packs; a bfloat16 pack is rejected at load time.
+ * Packs of dtype float32 load the fp32 model, bfloat16 packs the bf16-weight
+ * model (projections and embedding bf16, norms and activations fp32), as the
+ * reference's loader dispatches (src/llama_c_api.cu:56-73).
  */
 #ifndef OPWORKS_LLAMA_H
 #define OPWORKS_LLAMA_H
@@ -44,7 +46,9 @@ const char *opw_llama_last_error(void);
  * weights: every projection and the (tied) embedding ~ N(0, init_std) from the
  * counter-based generator of include/opworks_ops.h (per-tensor streams fixed
  * by the runtime), RMSNorm weights = 1 (norm_init 0) or U[0.5, 1.5]
- * (norm_init 1). Replaces writing a multi-GB synthetic pack. NULL on error. */
+ * (norm_init 1). "torch_dtype": "bfloat16" in the config selects bf16 weights
+ * (each value rounded to nearest-even, norms included, as a bf16 pack stores
+ * them). Replaces writing a multi-GB synthetic pack. NULL on error. */
 void *opw_llama_load_random(const char *config_json, uint64_t seed, float init_std, int norm_init, char *err,
                             int err_len);
 /* RoPE inverse frequencies (head_dim / 2 floats) the runtime derives from an

@@ -16,7 +16,7 @@ using opworks::capi::guard;
 namespace {
 
 struct ModelHolder {
-    std::unique_ptr<opworks::LlamaModel> model;
+    std::unique_ptr<opworks::LlamaRuntime> model;
 };
 struct SessionHolder {
     ModelHolder *owner;
@@ -49,7 +49,7 @@ void *opw_llama_load(const char *pack_path, char *err, int err_len) {
         [&]() -> void * {
             if (!pack_path)
                 throw std::invalid_argument("null pack path");
-            return new ModelHolder{opworks::LlamaModel::load(pack_path)};
+            return new ModelHolder{opworks::load_llama(pack_path)};
         },
         err, err_len);
 }
@@ -137,8 +137,16 @@ void *opw_llama_load_random(const char *config_json, uint64_t seed, float init_s
                 throw std::invalid_argument("norm_init must be 0 (ones) or 1 (uniform)");
             const opworks::json::Value cfg = opworks::json::parse(config_json);
             const opworks::ModelConfig mc = opworks::ModelConfig::from_json(cfg, cfg.find("eos_token_id"));
-            return new ModelHolder{opworks::LlamaModel::load_random(mc, seed, init_std,
-                                                                    static_cast<opworks::NormInit>(norm_init))};
+            // HF configs name the checkpoint dtype in "torch_dtype"; bfloat16 selects bf16 weights
+            const opworks::json::Value *dt = cfg.find("torch_dtype");
+            if (!dt)
+                dt = cfg.find("dtype");
+            const std::string dtype = dt ? dt->as_string() : "float32";
+            if (dtype != "float32" && dtype != "bfloat16")
+                throw std::invalid_argument("torch_dtype must be float32 or bfloat16");
+            return new ModelHolder{opworks::load_llama_random(mc, seed, init_std,
+                                                              static_cast<opworks::NormInit>(norm_init),
+                                                              dtype == "bfloat16")};
         },
         err, err_len);
 }
@@ -205,7 +213,7 @@ int opw_llama_generate_greedy(void *session, const int32_t *prompt, int n, int m
             auto *s = as_session(session);
             if (!prompt || n <= 0 || max_new <= 0 || !out_tokens)
                 throw std::invalid_argument("generate needs a prompt, max_new > 0 and an output buffer");
-            opworks::LlamaModel &m = *s->owner->model;
+            opworks::LlamaRuntime &m = *s->owner->model;
             std::vector<int32_t> ids(prompt, prompt + n);
             using clock = std::chrono::steady_clock;
             const auto t0 = clock::now();

@@ -37,6 +37,7 @@
 #include "../ops/attention.hpp"
 #include "../ops/gemm_f32.hpp"
 #include "../ops/rms_norm.hpp"
+#include "../ops/gemm_bf16.hpp"
 #include "../runtime/model_config.hpp"
 #include "../runtime/pack_reader.hpp"
 #include "llama_kernels.hpp"
@@ -53,18 +54,31 @@ constexpr uint64_t kStreamFinalNorm = 2;
 inline uint64_t layer_stream(int layer, int which) { return 64 + 16 * static_cast<uint64_t>(layer) + which; }
 enum LayerTensor { kQ = 0, kK = 1, kV = 2, kO = 3, kGate = 4, kUp = 5, kDown = 6, kInNorm = 7, kPostNorm = 8 };
 
+template <typename T> __device__ __forceinline__ T store_as(float v) {
+    if constexpr (std::is_same_v<T, bf16>)
+        return bf16{float_to_bf16_rne(v)};
+    else
+        return v;
+}
+
 // dst[(r * row_stride + row_offset) * cols + c] = N(mean, sd) draw r * cols + c
-__global__ __launch_bounds__(256) static void fill_rows_normal_kernel(float *dst, int64_t rows, int cols,
-                                                                      int row_stride, int row_offset, uint64_t key,
-                                                                      float mean, float sd) {
+// (rounded to nearest-even for a bf16 destination)
+template <typename T>
+__global__ __launch_bounds__(256) static void fill_rows_normal_kernel(T *dst, int64_t rows, int cols, int row_stride,
+                                                                      int row_offset, uint64_t key, float mean,
+                                                                      float sd) {
     OPWORKS_GRID_LOOP(i, rows * cols) {
         const int64_t r = i / cols, c = i % cols;
-        dst[(r * row_stride + row_offset) * cols + c] = rng::normal(key, static_cast<uint64_t>(i), mean, sd);
+        dst[(r * row_stride + row_offset) * cols + c] = store_as<T>(rng::normal(key, static_cast<uint64_t>(i), mean, sd));
     }
 }
+// round_bf16: the values a bf16 pack would hold, kept in fp32
 __global__ __launch_bounds__(256) static void fill_uniform_kernel(float *dst, int64_t n, uint64_t key, float lo,
-                                                                  float hi) {
-    OPWORKS_GRID_LOOP(i, n) { dst[i] = rng::uniform(key, static_cast<uint64_t>(i), lo, hi); }
+                                                                  float hi, bool round_bf16) {
+    OPWORKS_GRID_LOOP(i, n) {
+        const float v = rng::uniform(key, static_cast<uint64_t>(i), lo, hi);
+        dst[i] = round_bf16 ? bf16_to_float(float_to_bf16_rne(v)) : v;
+    }
 }
 __global__ __launch_bounds__(256) static void fill_const_kernel(float *dst, int64_t n, float v) {
     OPWORKS_GRID_LOOP(i, n) { dst[i] = v; }
@@ -80,19 +94,21 @@ inline int fill_grid(int64_t n) {
 // Norm weights of the seeded init: ones (HF init) or U[0.5, 1.5] (exercises gamma in tests).
 enum class NormInit { ones = 0, uniform = 1 };
 
-struct LlamaLayerWeights {
+// WT: storage of the projections and the embedding (float or bf16); norm
+// weights and every activation stay fp32 (reference: runtime/weights.cuh:16-27).
+template <typename WT> struct LlamaLayerWeights {
     TypedDeviceBuffer<float> input_norm, post_norm; // [H]
-    TypedDeviceBuffer<float> wqkv;                  // [(qh + 2 kvh) D][H]
-    TypedDeviceBuffer<float> wo;                    // [H][qh D]
-    TypedDeviceBuffer<float> wgu;                   // [2 I][H], rows gate_0, up_0, gate_1, ...
-    TypedDeviceBuffer<float> wdown;                 // [H][I]
+    TypedDeviceBuffer<WT> wqkv;                     // [(qh + 2 kvh) D][H]
+    TypedDeviceBuffer<WT> wo;                       // [H][qh D]
+    TypedDeviceBuffer<WT> wgu;                      // [2 I][H], rows gate_0, up_0, gate_1, ...
+    TypedDeviceBuffer<WT> wdown;                    // [H][I]
 };
 
-struct LlamaWeights {
-    TypedDeviceBuffer<float> embed;      // [V][H], also the LM head
+template <typename WT> struct LlamaWeights {
+    TypedDeviceBuffer<WT> embed;         // [V][H], also the LM head
     TypedDeviceBuffer<float> final_norm; // [H]
     TypedDeviceBuffer<float> inv_freq;   // [D/2]
-    std::vector<LlamaLayerWeights> layers;
+    std::vector<LlamaLayerWeights<WT>> layers;
 };
 
 struct LlamaSession {
@@ -136,37 +152,63 @@ struct LlamaSession {
     llama::StepState *state() { return reinterpret_cast<llama::StepState *>(state_buf.data()); }
 };
 
-class LlamaModel {
+// What the C ABI drives; implemented by LlamaModelT<float> and LlamaModelT<bf16>.
+class LlamaRuntime {
+  public:
+    using Session = LlamaSession;
+    virtual ~LlamaRuntime() = default;
+    virtual const ModelConfig &config() const = 0;
+    virtual const char *weight_dtype() const = 0; // "float32" | "bfloat16"
+    virtual std::unique_ptr<Session> create_session(int max_seq_len) const = 0;
+    virtual int32_t prefill(Session &s, const std::vector<int32_t> &ids) = 0;
+    virtual int32_t decode_step(Session &s, int32_t token) = 0;
+    virtual std::vector<float> profile_decode_step(Session &s, int32_t token, int32_t *next) = 0;
+    virtual float time_decode_stage(Session &s, int stage, int reps) = 0;
+    virtual bool is_eos(int32_t token) const = 0;
+    virtual std::vector<float> last_logits(Session &s) const = 0;
+    virtual void copy_last_logits(Session &s, float *out, int n) const = 0;
+    virtual std::vector<float> hidden_state(Session &s, int rows) const = 0;
+    virtual std::vector<std::vector<float>> debug_prefill(Session &s, const std::vector<int32_t> &ids) = 0;
+};
+
+// The Llama runtime over WT-typed weights (reference: LlamaModelT<WT>,
+// include/models/llama.cuh:78-291; LlamaModel = fp32, LlamaModelBF16 = bf16).
+template <typename WT> class LlamaModelT final : public LlamaRuntime {
+    static constexpr bool kBf16 = std::is_same_v<WT, bf16>;
+
   public:
     using Session = LlamaSession;
     static constexpr int kMaxSeqLen = detail::kAttnDecodeMaxLen; // 8192
 
-    // Loads an OPWPACK1 float32 pack (scripts/llama/pack_format.py layout).
-    static std::unique_ptr<LlamaModel> load(const std::string &pack_path) {
-        PackReader pack(pack_path);
-        if (pack.dtype() != "float32")
-            throw std::runtime_error("this build runs float32 packs only (got " + pack.dtype() + ")");
-        auto m = std::unique_ptr<LlamaModel>(new LlamaModel(ModelConfig::from_manifest(pack.manifest())));
+    // Loads an OPWPACK1 pack of this model's dtype (scripts/llama/pack_format.py layout).
+    static std::unique_ptr<LlamaModelT> load(const PackReader &pack) {
+        if (pack.dtype() != (kBf16 ? "bfloat16" : "float32"))
+            throw std::runtime_error(std::string(kBf16 ? "bf16" : "fp32") + " model requires a " +
+                                     (kBf16 ? "bfloat16" : "float32") + " pack (got " + pack.dtype() + ")");
+        auto m = std::unique_ptr<LlamaModelT>(new LlamaModelT(ModelConfig::from_manifest(pack.manifest())));
         m->check_supported();
         m->allocate();
         m->upload_pack(pack);
         return m;
     }
+    static std::unique_ptr<LlamaModelT> load(const std::string &pack_path) { return load(PackReader(pack_path)); }
 
-    // Seeded random weights: projections and embedding ~ N(0, std), norms per NormInit.
-    static std::unique_ptr<LlamaModel> load_random(const ModelConfig &cfg, uint64_t seed, float std,
-                                                   NormInit norms) {
-        auto m = std::unique_ptr<LlamaModel>(new LlamaModel(cfg));
+    // Seeded random weights: projections and embedding ~ N(0, std) (bf16:
+    // rounded to nearest-even), norms per NormInit (bf16: rounded values).
+    static std::unique_ptr<LlamaModelT> load_random(const ModelConfig &cfg, uint64_t seed, float std,
+                                                    NormInit norms) {
+        auto m = std::unique_ptr<LlamaModelT>(new LlamaModelT(cfg));
         m->check_supported();
         m->allocate();
         m->init_random(seed, std, norms);
         return m;
     }
 
-    const ModelConfig &config() const { return cfg_; }
-    const LlamaWeights &weights() const { return w_; }
+    const ModelConfig &config() const override { return cfg_; }
+    const char *weight_dtype() const override { return kBf16 ? "bfloat16" : "float32"; }
+    const LlamaWeights<WT> &weights() const { return w_; }
 
-    std::unique_ptr<Session> create_session(int max_seq_len) const {
+    std::unique_ptr<Session> create_session(int max_seq_len) const override {
         if (max_seq_len <= 0 || max_seq_len > kMaxSeqLen)
             throw std::invalid_argument("max_seq_len must be in (0, 8192]");
         auto s = std::make_unique<Session>();
@@ -204,14 +246,14 @@ class LlamaModel {
     }
 
     // Runs the prompt, fills the cache, returns the first generated token.
-    int32_t prefill(Session &s, const std::vector<int32_t> &ids) {
+    int32_t prefill(Session &s, const std::vector<int32_t> &ids) override {
         check_prefill(s, ids);
         run_prefill(s, ids, nullptr);
         return s.h_state->next;
     }
 
     // Appends `token` at position length and returns the argmax of the next token.
-    int32_t decode_step(Session &s, int32_t token) {
+    int32_t decode_step(Session &s, int32_t token) override {
         if (token < 0 || token >= cfg_.vocab_size)
             throw std::invalid_argument("token id outside the vocabulary");
         if (s.length >= s.max_seq_len)
@@ -234,7 +276,7 @@ class LlamaModel {
     // one after the last, all on the session stream; returns the kernel
     // durations in launch order (per layer: qkv_rope, attention, o_proj,
     // gate_up, down; then lm_head) and the next token in *next.
-    std::vector<float> profile_decode_step(Session &s, int32_t token, int32_t *next) {
+    std::vector<float> profile_decode_step(Session &s, int32_t token, int32_t *next) override {
         if (token < 0 || token >= cfg_.vocab_size)
             throw std::invalid_argument("token id outside the vocabulary");
         if (s.length >= s.max_seq_len)
@@ -280,7 +322,7 @@ class LlamaModel {
     // consecutive launches stream different layers' weights. Uses the state
     // of the last decode step; the KV entry it writes lies past the session's
     // length and is overwritten by the next real step. Requires a prefill.
-    float time_decode_stage(Session &s, int stage, int reps) {
+    float time_decode_stage(Session &s, int stage, int reps) override {
         if (stage < 0 || stage > 5)
             throw std::invalid_argument("decode stage must be in [0, 5]");
         if (reps <= 0)
@@ -315,17 +357,17 @@ class LlamaModel {
         return 1e3f * ms / float(reps * per_pass);
     }
 
-    bool is_eos(int32_t token) const {
+    bool is_eos(int32_t token) const override {
         return std::find(cfg_.eos_token_ids.begin(), cfg_.eos_token_ids.end(), token) != cfg_.eos_token_ids.end();
     }
 
-    std::vector<float> last_logits(Session &s) const {
+    std::vector<float> last_logits(Session &s) const override {
         std::vector<float> out(static_cast<size_t>(cfg_.vocab_size));
         copy_last_logits(s, out.data(), cfg_.vocab_size);
         return out;
     }
 
-    void copy_last_logits(Session &s, float *out, int n) const {
+    void copy_last_logits(Session &s, float *out, int n) const override {
         if (n != cfg_.vocab_size)
             throw std::invalid_argument("logits buffer must hold vocab_size floats");
         OPWORKS_HIP_CHECK(hipMemcpyAsync(out, s.logits.data(), sizeof(float) * static_cast<size_t>(n),
@@ -334,7 +376,7 @@ class LlamaModel {
     }
 
     // Residual stream of the last prefill: rows x H.
-    std::vector<float> hidden_state(Session &s, int rows) const {
+    std::vector<float> hidden_state(Session &s, int rows) const override {
         if (rows <= 0 || rows > s.max_seq_len)
             throw std::invalid_argument("rows outside the session capacity");
         std::vector<float> out(static_cast<size_t>(rows) * cfg_.hidden_size);
@@ -345,7 +387,7 @@ class LlamaModel {
     }
 
     // Like prefill, also returning the residual stream after the embedding and after each layer.
-    std::vector<std::vector<float>> debug_prefill(Session &s, const std::vector<int32_t> &ids) {
+    std::vector<std::vector<float>> debug_prefill(Session &s, const std::vector<int32_t> &ids) override {
         check_prefill(s, ids);
         std::vector<std::vector<float>> captures;
         const int n = static_cast<int>(ids.size());
@@ -361,10 +403,10 @@ class LlamaModel {
     }
 
   private:
-    explicit LlamaModel(const ModelConfig &cfg) : cfg_(cfg) {}
+    explicit LlamaModelT(const ModelConfig &cfg) : cfg_(cfg) {}
 
     ModelConfig cfg_;
-    LlamaWeights w_;
+    LlamaWeights<WT> w_;
     // When set (profiling only), called before every kernel of the decode step.
     const std::function<void()> *tick_ = nullptr;
     // Stages enqueued by the decode step (timing only narrows it): bit 0
@@ -387,6 +429,8 @@ class LlamaModel {
             throw std::runtime_error("head_dim must be 32 or 64");
         if (cfg_.kv_rep() > 16)
             throw std::runtime_error("at most 16 query heads per kv head");
+        if (kBf16 && (H % 512 != 0 || I % 2048 != 0))
+            throw std::runtime_error("bf16 weights need hidden_size % 512 == 0 and intermediate_size % 2048 == 0");
     }
 
     void check_prefill(Session &s, const std::vector<int32_t> &ids) const {
@@ -403,17 +447,17 @@ class LlamaModel {
 
     void allocate() {
         const int64_t H = cfg_.hidden_size, I = cfg_.intermediate_size, V = cfg_.vocab_size;
-        w_.embed = TypedDeviceBuffer<float>(V * H);
+        w_.embed = TypedDeviceBuffer<WT>(V * H);
         w_.final_norm = TypedDeviceBuffer<float>(H);
         w_.inv_freq = TypedDeviceBuffer<float>::from_host(cfg_.rope_inv_freq());
         w_.layers.resize(static_cast<size_t>(cfg_.num_layers));
         for (auto &l : w_.layers) {
             l.input_norm = TypedDeviceBuffer<float>(H);
             l.post_norm = TypedDeviceBuffer<float>(H);
-            l.wqkv = TypedDeviceBuffer<float>(int64_t(cfg_.qkv_width()) * H);
-            l.wo = TypedDeviceBuffer<float>(H * cfg_.q_width());
-            l.wgu = TypedDeviceBuffer<float>(2 * I * H);
-            l.wdown = TypedDeviceBuffer<float>(H * I);
+            l.wqkv = TypedDeviceBuffer<WT>(int64_t(cfg_.qkv_width()) * H);
+            l.wo = TypedDeviceBuffer<WT>(H * cfg_.q_width());
+            l.wgu = TypedDeviceBuffer<WT>(2 * I * H);
+            l.wdown = TypedDeviceBuffer<WT>(H * I);
         }
     }
 
@@ -421,8 +465,8 @@ class LlamaModel {
         using namespace llama_detail;
         const int64_t H = cfg_.hidden_size, I = cfg_.intermediate_size, V = cfg_.vocab_size;
         const int64_t qw = cfg_.q_width(), kw = cfg_.kv_width();
-        auto rows_fill = [&](float *dst, int64_t rows, int64_t cols, int stride, int offset, uint64_t stream) {
-            launch_async(nullptr, fill_rows_normal_kernel, fill_grid(rows * cols), 256, dst, rows,
+        auto rows_fill = [&](WT *dst, int64_t rows, int64_t cols, int stride, int offset, uint64_t stream) {
+            launch_async(nullptr, fill_rows_normal_kernel<WT>, fill_grid(rows * cols), 256, dst, rows,
                          static_cast<int>(cols), stride, offset, rng::stream_key(seed, stream), 0.f, sd);
         };
         auto norm_fill = [&](float *dst, uint64_t stream) {
@@ -430,12 +474,12 @@ class LlamaModel {
                 launch_async(nullptr, fill_const_kernel, fill_grid(H), 256, dst, H, 1.f);
             else
                 launch_async(nullptr, fill_uniform_kernel, fill_grid(H), 256, dst, H, rng::stream_key(seed, stream),
-                             0.5f, 1.5f);
+                             0.5f, 1.5f, kBf16);
         };
         rows_fill(w_.embed.data(), V, H, 1, 0, kStreamEmbed);
         norm_fill(w_.final_norm.data(), kStreamFinalNorm);
         for (int l = 0; l < cfg_.num_layers; ++l) {
-            LlamaLayerWeights &lw = w_.layers[static_cast<size_t>(l)];
+            LlamaLayerWeights<WT> &lw = w_.layers[static_cast<size_t>(l)];
             rows_fill(lw.wqkv.data(), qw, H, 1, 0, layer_stream(l, kQ));
             rows_fill(lw.wqkv.data() + qw * H, kw, H, 1, 0, layer_stream(l, kK));
             rows_fill(lw.wqkv.data() + (qw + kw) * H, kw, H, 1, 0, layer_stream(l, kV));
@@ -452,35 +496,46 @@ class LlamaModel {
     void upload_pack(const PackReader &pack) {
         const int64_t H = cfg_.hidden_size, I = cfg_.intermediate_size, V = cfg_.vocab_size;
         const int64_t qw = cfg_.q_width(), kw = cfg_.kv_width();
-        // one pinned staging buffer, sized for the largest tensor
-        int64_t largest = std::max<int64_t>(V * H, I * H);
-        float *stage = nullptr;
-        OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&stage), sizeof(float) * largest));
+        // one pinned staging buffer of WT elements, sized for the largest tensor
+        const int64_t largest = std::max<int64_t>(V * H, I * H);
+        WT *stage = nullptr;
+        OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&stage), sizeof(WT) * largest));
         struct Free {
-            float *p;
+            void *p;
             ~Free() { (void)hipHostFree(p); }
         } guard{stage};
         auto read = [&](const std::string &name, int64_t numel) {
             if (pack.meta(name).numel != numel)
                 throw std::runtime_error(name + ": element count mismatch");
-            pack.read_into(name, stage, sizeof(float) * static_cast<size_t>(numel));
+            pack.read_into(name, stage, sizeof(WT) * static_cast<size_t>(numel));
         };
-        auto put = [&](float *dst, int64_t numel) {
-            OPWORKS_HIP_CHECK(hipMemcpy(dst, stage, sizeof(float) * numel, hipMemcpyHostToDevice));
+        auto put = [&](WT *dst, int64_t numel) {
+            OPWORKS_HIP_CHECK(hipMemcpy(dst, stage, sizeof(WT) * numel, hipMemcpyHostToDevice));
         };
-        auto put_rows_strided = [&](float *dst, int64_t rows, int64_t cols, int offset) {
-            OPWORKS_HIP_CHECK(hipMemcpy2D(dst + offset * cols, sizeof(float) * 2 * cols, stage, sizeof(float) * cols,
-                                          sizeof(float) * cols, rows, hipMemcpyHostToDevice));
+        auto put_rows_strided = [&](WT *dst, int64_t rows, int64_t cols, int offset) {
+            OPWORKS_HIP_CHECK(hipMemcpy2D(dst + offset * cols, sizeof(WT) * 2 * cols, stage, sizeof(WT) * cols,
+                                          sizeof(WT) * cols, rows, hipMemcpyHostToDevice));
+        };
+        // norm weights are fp32 on the device; a bf16 pack stores them as bf16
+        // (reference: runtime/weights.cuh:57-66, read_bf16_as_float)
+        auto put_norm = [&](const std::string &name, float *dst) {
+            read(name, H);
+            std::vector<float> f(static_cast<size_t>(H));
+            for (int64_t i = 0; i < H; ++i) {
+                if constexpr (kBf16)
+                    f[static_cast<size_t>(i)] = bf16_to_float(stage[i].bits);
+                else
+                    f[static_cast<size_t>(i)] = stage[i];
+            }
+            OPWORKS_HIP_CHECK(hipMemcpy(dst, f.data(), sizeof(float) * H, hipMemcpyHostToDevice));
         };
         read("model.embed_tokens.weight", V * H);
         put(w_.embed.data(), V * H);
-        read("model.norm.weight", H);
-        put(w_.final_norm.data(), H);
+        put_norm("model.norm.weight", w_.final_norm.data());
         for (int l = 0; l < cfg_.num_layers; ++l) {
             const std::string p = "model.layers." + std::to_string(l) + ".";
-            LlamaLayerWeights &lw = w_.layers[static_cast<size_t>(l)];
-            read(p + "input_layernorm.weight", H);
-            put(lw.input_norm.data(), H);
+            LlamaLayerWeights<WT> &lw = w_.layers[static_cast<size_t>(l)];
+            put_norm(p + "input_layernorm.weight", lw.input_norm.data());
             read(p + "self_attn.q_proj.weight", qw * H);
             put(lw.wqkv.data(), qw * H);
             read(p + "self_attn.k_proj.weight", kw * H);
@@ -489,8 +544,7 @@ class LlamaModel {
             put(lw.wqkv.data() + (qw + kw) * H, kw * H);
             read(p + "self_attn.o_proj.weight", H * qw);
             put(lw.wo.data(), H * qw);
-            read(p + "post_attention_layernorm.weight", H);
-            put(lw.post_norm.data(), H);
+            put_norm(p + "post_attention_layernorm.weight", lw.post_norm.data());
             read(p + "mlp.gate_proj.weight", I * H);
             put_rows_strided(lw.wgu.data(), I, H, 0);
             read(p + "mlp.up_proj.weight", I * H);
@@ -517,9 +571,11 @@ class LlamaModel {
         const int qh = cfg_.num_q_heads, kvh = cfg_.num_kv_heads;
         const int qkv_groups = (qh + 2 * kvh) * (D / 4); // 4 rows each
         hipStream_t st = s.stream;
-        const LlamaLayerWeights &lw = w_.layers[static_cast<size_t>(l)];
-        llama::QkvArgs qa{};
-        qa.hidden_in = l == 0 ? nullptr : s.d_hidden.data();
+        const LlamaLayerWeights<WT> &lw = w_.layers[static_cast<size_t>(l)];
+        llama::QkvArgs<WT> qa{};
+        // layer 0 reads the step token's embedding row: fp32 tables directly in
+        // the qkv kernel, bf16 tables widened into the residual stream first
+        qa.hidden_in = (l == 0 && !kBf16) ? nullptr : s.d_hidden.data();
         qa.embed = w_.embed.data();
         qa.hidden_out = s.d_hidden.data();
         qa.gamma = lw.input_norm.data();
@@ -536,7 +592,10 @@ class LlamaModel {
         qa.cap = s.max_seq_len;
         if (stage_on(0)) {
             tick();
-            launch_async(st, llama::qkv_rope_kernel<kV>, qkv_groups, llama::kBlock, qa);
+            if (kBf16 && l == 0)
+                launch_async(st, llama::embed_token_kernel<WT>, detail::blocks_for64(H, 256), 256, w_.embed.data(),
+                             s.state(), s.d_hidden.data(), H);
+            launch_async(st, llama::qkv_rope_kernel<kV, WT>, qkv_groups, llama::kBlock, qa);
         }
         llama::DecodeAttnArgs aa{};
         aa.q = s.d_q.data();
@@ -557,18 +616,18 @@ class LlamaModel {
         }
         if (stage_on(2)) {
             tick();
-            launch_async(st, llama::gemv_residual_kernel<kV>, detail::blocks_for64(H, llama::kRows),
+            launch_async(st, llama::gemv_residual_kernel<kV, WT>, detail::blocks_for64(H, llama::kRows),
                          llama::kBlock, lw.wo.data(), s.d_attn.data(), s.d_hidden.data(), H);
         }
         if (stage_on(3)) {
             tick();
-            launch_async(st, llama::swiglu_gemv_kernel<kV>, detail::blocks_for64(2 * I, llama::kWavesPerBlock),
+            launch_async(st, llama::swiglu_gemv_kernel<kV, WT>, detail::blocks_for64(2 * I, llama::kWavesPerBlock),
                          llama::kBlock, s.d_hidden.data(), lw.post_norm.data(), cfg_.rms_norm_eps, lw.wgu.data(),
                          s.d_act.data(), I);
         }
         if (stage_on(4)) {
             tick();
-            launch_async(st, llama::down_residual_kernel<kV2>, detail::blocks_for64(H, llama::kRows), llama::kBlock,
+            launch_async(st, llama::down_residual_kernel<kV2, WT>, detail::blocks_for64(H, llama::kRows), llama::kBlock,
                          lw.wdown.data(), s.d_act.data(), s.d_hidden.data(), H);
         }
     }
@@ -588,7 +647,7 @@ class LlamaModel {
     }
 
     template <int kV> void enqueue_lm_head(Session &s, const float *hidden_row) const {
-        llama::LmHeadArgs la{};
+        llama::LmHeadArgs<WT> la{};
         la.hidden_row = hidden_row;
         la.gamma = w_.final_norm.data();
         la.embed = w_.embed.data();
@@ -598,20 +657,29 @@ class LlamaModel {
         la.eps = cfg_.rms_norm_eps;
         la.vocab = cfg_.vocab_size;
         tick();
-        launch_async(s.stream, llama::lm_head_kernel<kV>, s.lm_grid, llama::kBlock, la);
+        launch_async(s.stream, llama::lm_head_kernel<kV, WT>, s.lm_grid, llama::kBlock, la);
         launch_async(s.stream, llama::argmax_records_kernel, 1, 1024, s.lm_best_val.data(), s.lm_best_idx.data(),
                      s.lm_grid, s.state(), s.argmax_out.data());
     }
 
+    // Calls f(IntTag<H / 256>, IntTag<I / 1024>); bf16 rows need whole 8-weight
+    // packs per lane, so the narrowest widths exist for fp32 only (check_supported
+    // rejects them for bf16 before any launch).
     template <typename F> void dispatch_widths(F &&f) const {
         const int v = cfg_.hidden_size / 256, v2 = cfg_.intermediate_size / 1024;
+        auto call = [&](auto vt, auto v2t) {
+            if constexpr (!kBf16 || (decltype(vt)::value % 2 == 0 && decltype(v2t)::value % 2 == 0))
+                f(vt, v2t);
+            else
+                throw std::runtime_error("unsupported widths for bf16 weights");
+        };
         auto with_v2 = [&](auto vt) {
             switch (v2) {
-            case 1: f(vt, detail::IntTag<1>{}); break;
-            case 2: f(vt, detail::IntTag<2>{}); break;
-            case 4: f(vt, detail::IntTag<4>{}); break;
-            case 8: f(vt, detail::IntTag<8>{}); break;
-            case 16: f(vt, detail::IntTag<16>{}); break;
+            case 1: call(vt, detail::IntTag<1>{}); break;
+            case 2: call(vt, detail::IntTag<2>{}); break;
+            case 4: call(vt, detail::IntTag<4>{}); break;
+            case 8: call(vt, detail::IntTag<8>{}); break;
+            case 16: call(vt, detail::IntTag<16>{}); break;
             default: throw std::runtime_error("unsupported intermediate_size");
             }
         };
@@ -694,25 +762,42 @@ class LlamaModel {
         // Layer 0's first kernel writes the embedding row into the residual stream;
         // copy it beforehand so the "after embedding" capture sees it.
         const int H = cfg_.hidden_size;
-        OPWORKS_HIP_CHECK(hipMemcpyAsync(s.d_hidden.data(), w_.embed.data() + int64_t(s.h_state->token) * H,
-                                         sizeof(float) * H, hipMemcpyDeviceToDevice, s.stream));
+        if constexpr (kBf16)
+            launch_async(s.stream, llama::embed_token_kernel<WT>, detail::blocks_for64(H, 256), 256, w_.embed.data(),
+                         s.state(), s.d_hidden.data(), H);
+        else
+            OPWORKS_HIP_CHECK(hipMemcpyAsync(s.d_hidden.data(), w_.embed.data() + int64_t(s.h_state->token) * H,
+                                             sizeof(float) * H, hipMemcpyDeviceToDevice, s.stream));
         hook(-1);
         enqueue_decode(s, hook);
+    }
+
+    // Prefill projection C (per kStore) = A[M][K] W[N][K]^T: the fp32 MFMA GEMM
+    // for fp32 weights; for bf16 weights the bf16 MFMA GEMM with A rounded to
+    // bf16 on load (the reference's linear_mma_bf16 path, models/llama.cuh:190-199;
+    // it takes that path from 16 rows, this build from 2, see the design notes).
+    template <detail::GemmStore kStore = detail::GemmStore::store>
+    void project(const float *A, const WT *W, float *C, int M, int N, int K, hipStream_t st) const {
+        if constexpr (kBf16)
+            detail::gemm_bf16_launch<float, detail::IdentityEpilogue, kStore>(
+                A, reinterpret_cast<const uint16_t *>(W), nullptr, C, M, N, K, detail::IdentityEpilogue{}, st);
+        else
+            detail::gemm_f32_launch<detail::BLayout::nk, detail::IdentityEpilogue, kStore>(
+                A, W, nullptr, C, M, N, K, detail::IdentityEpilogue{}, st);
     }
 
     void enqueue_prefill(Session &s, int n, const std::function<void(int)> &hook) {
         const int H = cfg_.hidden_size, I = cfg_.intermediate_size, D = cfg_.head_dim;
         const int qh = cfg_.num_q_heads, kvh = cfg_.num_kv_heads, qkvw = cfg_.qkv_width();
         hipStream_t st = s.stream;
-        launch_async(st, llama::embedding_kernel, detail::stream_grid(int64_t(n) * H / 4), 256, w_.embed.data(),
+        launch_async(st, llama::embedding_kernel<WT>, detail::stream_grid(int64_t(n) * H / 4), 256, w_.embed.data(),
                      s.ids.data(), s.hidden.data(), n, H);
         if (hook)
             hook(-1);
         for (int l = 0; l < cfg_.num_layers; ++l) {
-            const LlamaLayerWeights &lw = w_.layers[static_cast<size_t>(l)];
+            const LlamaLayerWeights<WT> &lw = w_.layers[static_cast<size_t>(l)];
             ops::rms_norm(s.hidden.data(), lw.input_norm.data(), s.normed.data(), n, H, cfg_.rms_norm_eps, st);
-            detail::gemm_f32_launch<detail::BLayout::nk>(s.normed.data(), lw.wqkv.data(), nullptr, s.qkv.data(), n,
-                                                         qkvw, H, detail::IdentityEpilogue{}, st);
+            project(s.normed.data(), lw.wqkv.data(), s.qkv.data(), n, qkvw, H, st);
             launch_async(st, llama::rope_split_kernel, detail::stream_grid(int64_t(n) * (qh + 2 * kvh) * (D / 2)),
                          256, s.qkv.data(), w_.inv_freq.data(), s.q_heads.data(), layer_k(s, l), layer_v(s, l), n, qh,
                          kvh, D, s.max_seq_len, 0);
@@ -720,18 +805,37 @@ class LlamaModel {
                                    cfg_.kv_rep(), D, s.max_seq_len, st);
             launch_async(st, llama::merge_heads_kernel, detail::stream_grid(int64_t(n) * qh * D), 256,
                          s.attn_heads.data(), s.attn.data(), n, qh, D);
-            detail::gemm_f32_launch<detail::BLayout::nk, detail::IdentityEpilogue, detail::GemmStore::residual>(
-                s.attn.data(), lw.wo.data(), nullptr, s.hidden.data(), n, H, qh * D, detail::IdentityEpilogue{}, st);
+            project<detail::GemmStore::residual>(s.attn.data(), lw.wo.data(), s.hidden.data(), n, H, qh * D, st);
             ops::rms_norm(s.hidden.data(), lw.post_norm.data(), s.normed.data(), n, H, cfg_.rms_norm_eps, st);
-            detail::gemm_f32_launch<detail::BLayout::nk, detail::IdentityEpilogue, detail::GemmStore::swiglu>(
-                s.normed.data(), lw.wgu.data(), nullptr, s.act.data(), n, 2 * I, H, detail::IdentityEpilogue{}, st);
-            detail::gemm_f32_launch<detail::BLayout::nk, detail::IdentityEpilogue, detail::GemmStore::residual>(
-                s.act.data(), lw.wdown.data(), nullptr, s.hidden.data(), n, H, I, detail::IdentityEpilogue{}, st);
+            project<detail::GemmStore::swiglu>(s.normed.data(), lw.wgu.data(), s.act.data(), n, 2 * I, H, st);
+            project<detail::GemmStore::residual>(s.act.data(), lw.wdown.data(), s.hidden.data(), n, H, I, st);
             if (hook)
                 hook(l);
         }
-        dispatch_widths([&](auto v, auto) { enqueue_lm_head<decltype(v)::value>(s, s.hidden.data() + int64_t(n - 1) * H); });
+        dispatch_widths(
+            [&](auto v, auto) { enqueue_lm_head<decltype(v)::value>(s, s.hidden.data() + int64_t(n - 1) * H); });
     }
 };
+
+using LlamaModel = LlamaModelT<float>;
+using LlamaModelBF16 = LlamaModelT<bf16>;
+
+// Loads a pack and picks the model from its dtype (reference: src/llama_c_api.cu:56-73).
+inline std::unique_ptr<LlamaRuntime> load_llama(const std::string &pack_path) {
+    PackReader pack(pack_path);
+    if (pack.dtype() == "float32")
+        return LlamaModel::load(pack);
+    if (pack.dtype() == "bfloat16")
+        return LlamaModelBF16::load(pack);
+    throw std::runtime_error("unsupported pack dtype " + pack.dtype());
+}
+
+// Seeded random weights of either storage type.
+inline std::unique_ptr<LlamaRuntime> load_llama_random(const ModelConfig &cfg, uint64_t seed, float std,
+                                                       NormInit norms, bool bf16_weights) {
+    if (bf16_weights)
+        return LlamaModelBF16::load_random(cfg, seed, std, norms);
+    return LlamaModel::load_random(cfg, seed, std, norms);
+}
 
 } // namespace opworks

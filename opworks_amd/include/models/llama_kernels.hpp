@@ -23,6 +23,9 @@
 #include <cmath>
 #include <cstdint>
 
+#include <type_traits>
+
+#include "../core/bf16.hpp"
 #include "../core/hip_utils.hpp"
 #include "../core/wave.hpp"
 #include "../ops/argmax.hpp"
@@ -45,6 +48,45 @@ constexpr int kRows = 4;       // rows per LM-head wave; rows per workgroup of t
 constexpr int kBlock = 256;    // threads per GEMV workgroup
 constexpr int kWavesPerBlock = kBlock / kWaveSize;
 
+// Weights are streamed in 16-byte packs: 4 fp32 or 8 bf16 values; bf16 is
+// widened exactly (bits << 16) and every product is accumulated in fp32.
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+template <typename WT> struct WPack;
+template <> struct WPack<float> {
+    static constexpr int kElems = 4;
+    using type = f32x4;
+    __device__ static float at(const f32x4 &p, int j) { return p[j]; }
+};
+template <> struct WPack<bf16> {
+    static constexpr int kElems = 8;
+    using type = u32x4;
+    __device__ static float at(const u32x4 &p, int j) {
+        const uint32_t w = p[j >> 1];
+        return __builtin_bit_cast(float, (j & 1) ? (w & 0xffff0000u) : (w << 16));
+    }
+};
+template <typename WT> __device__ __forceinline__ typename WPack<WT>::type load_wpack(const WT *row, int pack) {
+    return __builtin_nontemporal_load(reinterpret_cast<const typename WPack<WT>::type *>(row) + pack);
+}
+template <typename WT> __device__ __forceinline__ float widen(WT v) {
+    if constexpr (std::is_same_v<WT, bf16>)
+        return bf16_to_float(v.bits);
+    else
+        return v;
+}
+// acc += sum_j w[j] * x[j] over one pack (x: the pack's kElems inputs)
+template <typename WT>
+__device__ __forceinline__ float dot_wpack(const typename WPack<WT>::type &w, const f32x4 (&x)[WPack<WT>::kElems / 4],
+                                           float acc) {
+    constexpr int E = WPack<WT>::kElems;
+#pragma unroll
+    for (int q = 0; q < E / 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc = fmaf(WPack<WT>::at(w, 4 * q + j), x[q][j], acc);
+    return acc;
+}
+
 // GEMV of a 4-wave workgroup: each wave owns kR rows of a [*, H] matrix,
 // H = 256 * kV. The input vector is staged once per workgroup: its loads are
 // issued first, then every weight pack of the wave, so with in-order vmcnt
@@ -52,13 +94,16 @@ constexpr int kWavesPerBlock = kBlock / kWaveSize;
 // The (optionally RMS-normalised) vector goes to LDS and each wave reads its
 // kV packs from there. Waves with active == false still take part in the
 // barriers. xn = x * rsqrtf(mean(x^2) + eps) * gamma, ops::rms_norm's order.
-template <int kV, int kR = kRows>
+template <int kV, int kR = kRows, typename WT = float>
 __device__ __forceinline__ void block_gemv(const float *__restrict__ x, const float *__restrict__ gamma, float eps,
-                                           const float *__restrict__ W, const int (&row)[kR], bool active,
+                                           const WT *__restrict__ W, const int (&row)[kR], bool active,
                                            float *__restrict__ copy_x_to, float (&y)[kR]) {
     constexpr int H = 256 * kV;
     constexpr int kPacks = H / 4;
     constexpr int kX = (kPacks + kBlock - 1) / kBlock; // input packs per thread
+    constexpr int E = WPack<WT>::kElems;
+    constexpr int kP = H / (kWaveSize * E); // weight packs per lane per row
+    static_assert(kP * kWaveSize * E == H, "row width must be a multiple of 64 weight packs");
     __shared__ __attribute__((aligned(16))) float xs[H];
     __shared__ float red[kWavesPerBlock];
     const int tid = threadIdx.x, lane = tid % kWaveSize, wave = tid / kWaveSize;
@@ -74,14 +119,13 @@ __device__ __forceinline__ void block_gemv(const float *__restrict__ x, const fl
                 gv[i] = g4[c];
         }
     }
-    f32x4 w[kR][kV];
+    typename WPack<WT>::type w[kR][kP];
     if (active) {
 #pragma unroll
         for (int r = 0; r < kR; ++r)
 #pragma unroll
-            for (int u = 0; u < kV; ++u)
-                w[r][u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(W + int64_t(row[r]) * H) + lane +
-                                                     kWaveSize * u);
+            for (int u = 0; u < kP; ++u)
+                w[r][u] = load_wpack(W + int64_t(row[r]) * H, lane + kWaveSize * u);
     }
     __builtin_amdgcn_sched_barrier(0);
     float inv = 1.f;
@@ -120,11 +164,12 @@ __device__ __forceinline__ void block_gemv(const float *__restrict__ x, const fl
     for (int r = 0; r < kR; ++r) {
         float acc = 0.f;
 #pragma unroll
-        for (int u = 0; u < kV; ++u) {
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(&xs[4 * (lane + kWaveSize * u)]);
+        for (int u = 0; u < kP; ++u) {
+            f32x4 xl[E / 4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc = fmaf(w[r][u][j], v[j], acc);
+            for (int q = 0; q < E / 4; ++q)
+                xl[q] = *reinterpret_cast<const f32x4 *>(&xs[E * (lane + kWaveSize * u) + 4 * q]);
+            acc = dot_wpack<WT>(w[r][u], xl, acc);
         }
         y[r] = wave::sum(acc);
     }
@@ -137,35 +182,35 @@ __device__ __forceinline__ void block_gemv(const float *__restrict__ x, const fl
 // sums go through LDS, combined in the fixed order (w0 + w1) + (w2 + w3).
 // Serves short matrices (o_proj), where it measured faster than one row per
 // wave.
-template <int kV>
-__device__ __forceinline__ void block_gemv_split(const float *__restrict__ x, const float *__restrict__ W,
+template <int kV, typename WT = float>
+__device__ __forceinline__ void block_gemv_split(const float *__restrict__ x, const WT *__restrict__ W,
                                                  const int (&row)[kRows], float (&y)[kRows]) {
-    static_assert(kV % 4 == 0, "the split GEMV needs H to be a multiple of 1024");
     constexpr int H = 256 * kV;
-    constexpr int kX = kV / 4; // packs per thread
+    constexpr int E = WPack<WT>::kElems;
+    constexpr int kX = H / (kBlock * E); // weight packs per thread
+    static_assert(kX * kBlock * E == H, "the split GEMV needs H to be a multiple of 256 weight packs");
     __shared__ float part[kWavesPerBlock][kRows];
     const int tid = threadIdx.x, lane = tid % kWaveSize, wave = tid / kWaveSize;
     const f32x4 *x4 = reinterpret_cast<const f32x4 *>(x);
-    f32x4 xv[kX];
+    f32x4 xv[kX][E / 4];
 #pragma unroll
     for (int i = 0; i < kX; ++i)
-        xv[i] = x4[tid + kBlock * i];
-    f32x4 w[kRows][kX];
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q)
+            xv[i][q] = x4[(E / 4) * (tid + kBlock * i) + q];
+    typename WPack<WT>::type w[kRows][kX];
 #pragma unroll
     for (int r = 0; r < kRows; ++r)
 #pragma unroll
         for (int i = 0; i < kX; ++i)
-            w[r][i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(W + int64_t(row[r]) * H) + tid +
-                                                 kBlock * i);
+            w[r][i] = load_wpack(W + int64_t(row[r]) * H, tid + kBlock * i);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
         float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < kX; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc = fmaf(w[r][i][j], xv[i][j], acc);
+            acc = dot_wpack<WT>(w[r][i], xv[i], acc);
         acc = wave::sum(acc);
         if (lane == 0)
             part[wave][r] = acc;
@@ -181,12 +226,12 @@ __device__ __forceinline__ void block_gemv_split(const float *__restrict__ x, co
 // Workgroup g owns rotary pairs (j, j + D/2) and (j+1, j+1 + D/2) of head
 // slot g / (D/4), j = 2 * (g % (D/4)). Layer 0 reads its input from the
 // embedding row of the step token and also writes it to the residual stream.
-struct QkvArgs {
-    const float *hidden_in; // residual stream (or nullptr: use embed[token])
-    const float *embed;     // [V][H]
+template <typename WT> struct QkvArgs {
+    const float *hidden_in; // residual stream (or nullptr: use embed[token], fp32 weights only)
+    const WT *embed;        // [V][H]
     float *hidden_out;      // written only when reading from the embedding
     const float *gamma;     // input RMSNorm weight
-    const float *wqkv;      // [(qh + 2 kvh) * D][H]
+    const WT *wqkv;         // [(qh + 2 kvh) * D][H]
     const float *inv_freq;  // [D/2]
     float *q_out;           // [qh][D]
     float *kcache, *vcache; // this layer: [kvh][cap][D]
@@ -195,7 +240,8 @@ struct QkvArgs {
     int qh, kvh, D, cap;
 };
 
-__device__ __forceinline__ void qkv_store(const QkvArgs &a, int slot, int j, int pos, const float (&y_in)[4]) {
+template <typename WT>
+__device__ __forceinline__ void qkv_store(const QkvArgs<WT> &a, int slot, int j, int pos, const float (&y_in)[4]) {
     const int half = a.D / 2;
     float y[4] = {y_in[0], y_in[1], y_in[2], y_in[3]};
     if (slot < a.qh + a.kvh) { // rotate q and k: (lo, hi) = (a c - b s, b c + a s)
@@ -223,8 +269,8 @@ __device__ __forceinline__ void qkv_store(const QkvArgs &a, int slot, int j, int
 
 // One workgroup per 4-row group (grid = (qh + 2 kvh) * D / 4), one row per
 // wave: wave w computes row j + (w & 1) + (w >> 1) * D/2 of the head slot.
-template <int kV>
-__global__ __launch_bounds__(kBlock) void qkv_rope_kernel(QkvArgs a) {
+template <int kV, typename WT>
+__global__ __launch_bounds__(kBlock) void qkv_rope_kernel(QkvArgs<WT> a) {
     constexpr int H = 256 * kV;
     __shared__ float res[kWavesPerBlock];
     const int g = blockIdx.x, wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
@@ -232,11 +278,15 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(QkvArgs a) {
     const int slot = g / groups_per_head;
     const int j = 2 * (g % groups_per_head);
     const int pos = a.state->pos;
-    const float *src = a.hidden_in ? a.hidden_in : a.embed + int64_t(a.state->token) * H;
+    const float *src = a.hidden_in;
+    if constexpr (std::is_same_v<WT, float>) // bf16 models gather the row with embed_token_kernel first
+        if (!src)
+            src = a.embed + int64_t(a.state->token) * H;
     const int row[1] = {slot * a.D + j + (wave & 1) + (wave >> 1) * (a.D / 2)};
     float y[1];
     // layer 0: workgroup 0 also writes the embedding row into the residual stream
-    block_gemv<kV, 1>(src, a.gamma, a.eps, a.wqkv, row, true, (!a.hidden_in && g == 0) ? a.hidden_out : nullptr, y);
+    block_gemv<kV, 1, WT>(src, a.gamma, a.eps, a.wqkv, row, true, (!a.hidden_in && g == 0) ? a.hidden_out : nullptr,
+                          y);
     if (lane == 0)
         res[wave] = y[0];
     __syncthreads();
@@ -250,18 +300,18 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(QkvArgs a) {
 using detail::DecodeAttnArgs;
 
 // ---- 3. hidden += W x (in = H) -----------------------------------------------
-template <int kV>
-__global__ __launch_bounds__(kBlock) void gemv_residual_kernel(const float *__restrict__ W,
+template <int kV, typename WT>
+__global__ __launch_bounds__(kBlock) void gemv_residual_kernel(const WT *__restrict__ W,
                                                                const float *__restrict__ x, float *__restrict__ hidden,
                                                                int out) {
-    if constexpr (kV % 4 == 0) { // in >= 1024: 4 rows per workgroup, columns split across the waves
+    if constexpr (kV % WPack<WT>::kElems == 0) { // 4 rows per workgroup, columns split across the waves
         const int r0 = blockIdx.x * kRows;
         int row[kRows];
 #pragma unroll
         for (int r = 0; r < kRows; ++r)
             row[r] = r0 + r < out ? r0 + r : r0;
         float y[kRows];
-        block_gemv_split<kV>(x, W, row, y);
+        block_gemv_split<kV, WT>(x, W, row, y);
         if (threadIdx.x < kRows && r0 + threadIdx.x < out) {
             float v = y[0];
 #pragma unroll
@@ -274,7 +324,7 @@ __global__ __launch_bounds__(kBlock) void gemv_residual_kernel(const float *__re
         const bool active = r < out;
         const int row[1] = {active ? r : 0};
         float y[1];
-        block_gemv<kV, 1>(x, nullptr, 0.f, W, row, active, nullptr, y);
+        block_gemv<kV, 1, WT>(x, nullptr, 0.f, W, row, active, nullptr, y);
         if (active && threadIdx.x % kWaveSize == 0)
             hidden[r] += y[0];
     }
@@ -282,10 +332,10 @@ __global__ __launch_bounds__(kBlock) void gemv_residual_kernel(const float *__re
 
 // ---- 4. act = silu(gate) * up, interleaved [gate_i; up_i] rows ----------------
 // Workgroup b computes pairs 2b and 2b + 1, one row per wave (rows 4b .. 4b+3).
-template <int kV>
+template <int kV, typename WT>
 __global__ __launch_bounds__(kBlock) void swiglu_gemv_kernel(const float *__restrict__ hidden,
                                                              const float *__restrict__ gamma, float eps,
-                                                             const float *__restrict__ wgu, float *__restrict__ act,
+                                                             const WT *__restrict__ wgu, float *__restrict__ act,
                                                              int inter) {
     __shared__ float res[kWavesPerBlock];
     const int wave = threadIdx.x / kWaveSize;
@@ -293,7 +343,7 @@ __global__ __launch_bounds__(kBlock) void swiglu_gemv_kernel(const float *__rest
     const bool active = r < 2 * inter;
     const int row[1] = {active ? r : 0};
     float y[1];
-    block_gemv<kV, 1>(hidden, gamma, eps, wgu, row, active, nullptr, y);
+    block_gemv<kV, 1, WT>(hidden, gamma, eps, wgu, row, active, nullptr, y);
     if (threadIdx.x % kWaveSize == 0)
         res[wave] = y[0];
     __syncthreads();
@@ -305,39 +355,41 @@ __global__ __launch_bounds__(kBlock) void swiglu_gemv_kernel(const float *__rest
 }
 
 // ---- 5. hidden += W_down act (in = I = 1024 * kV2), K split across 4 waves ----
-template <int kV2>
-__global__ __launch_bounds__(kBlock) void down_residual_kernel(const float *__restrict__ W,
+template <int kV2, typename WT>
+__global__ __launch_bounds__(kBlock) void down_residual_kernel(const WT *__restrict__ W,
                                                                const float *__restrict__ act,
                                                                float *__restrict__ hidden, int out) {
     constexpr int I = 1024 * kV2;
     constexpr int Kw = I / kWavesPerBlock; // columns per wave
+    constexpr int E = WPack<WT>::kElems;
+    constexpr int kP = Kw / (kWaveSize * E); // weight packs per lane per row
+    static_assert(kP * kWaveSize * E == Kw, "intermediate size must split into 64-lane weight packs");
     __shared__ float part[kWavesPerBlock][kRows];
     const int lane = threadIdx.x % kWaveSize, wave = threadIdx.x / kWaveSize;
     const int r0 = blockIdx.x * kRows;
     const int c0 = wave * Kw;
-    f32x4 xv[kV2];
+    f32x4 xv[kP][E / 4];
     const f32x4 *a4 = reinterpret_cast<const f32x4 *>(act + c0);
 #pragma unroll
-    for (int u = 0; u < kV2; ++u)
-        xv[u] = a4[lane + kWaveSize * u];
-    f32x4 wv[kRows][kV2];
+    for (int u = 0; u < kP; ++u)
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q)
+            xv[u][q] = a4[(E / 4) * (lane + kWaveSize * u) + q];
+    typename WPack<WT>::type wv[kRows][kP];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
         const int row = r0 + r < out ? r0 + r : r0;
-        const f32x4 *w4 = reinterpret_cast<const f32x4 *>(W + int64_t(row) * I + c0);
 #pragma unroll
-        for (int u = 0; u < kV2; ++u)
-            wv[r][u] = __builtin_nontemporal_load(w4 + lane + kWaveSize * u);
+        for (int u = 0; u < kP; ++u)
+            wv[r][u] = load_wpack(W + int64_t(row) * I + c0, lane + kWaveSize * u);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < kRows; ++r) {
         float acc = 0.f;
 #pragma unroll
-        for (int u = 0; u < kV2; ++u)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc = fmaf(wv[r][u][j], xv[u][j], acc);
+        for (int u = 0; u < kP; ++u)
+            acc = dot_wpack<WT>(wv[r][u], xv[u], acc);
         acc = wave::sum(acc);
         if (lane == 0)
             part[wave][r] = acc;
@@ -360,10 +412,10 @@ __global__ __launch_bounds__(kBlock) void down_residual_kernel(const float *__re
 using detail::argmax_merge;
 using detail::wave_argmax;
 
-struct LmHeadArgs {
+template <typename WT> struct LmHeadArgs {
     const float *hidden_row; // [H]
     const float *gamma;      // final norm
-    const float *embed;      // [V][H]
+    const WT *embed;         // [V][H]
     float *logits;           // [V]
     float *best_val;         // [grid]
     int *best_idx;           // [grid]
@@ -371,8 +423,8 @@ struct LmHeadArgs {
     int vocab;
 };
 
-template <int kV>
-__global__ __launch_bounds__(kBlock) void lm_head_kernel(LmHeadArgs a) {
+template <int kV, typename WT>
+__global__ __launch_bounds__(kBlock) void lm_head_kernel(LmHeadArgs<WT> a) {
     __shared__ float sv[kWavesPerBlock];
     __shared__ int si[kWavesPerBlock];
     const int lane = threadIdx.x % kWaveSize, wave = threadIdx.x / kWaveSize;
@@ -382,7 +434,7 @@ __global__ __launch_bounds__(kBlock) void lm_head_kernel(LmHeadArgs a) {
     for (int r = 0; r < kRows; ++r)
         row[r] = r0 + r < a.vocab ? r0 + r : 0;
     float y[kRows];
-    block_gemv<kV>(a.hidden_row, a.gamma, a.eps, a.embed, row, r0 < a.vocab, nullptr, y);
+    block_gemv<kV, kRows, WT>(a.hidden_row, a.gamma, a.eps, a.embed, row, r0 < a.vocab, nullptr, y);
     float bv = kNegInf;
     int bi = 0x7fffffff;
     if (r0 < a.vocab) {
@@ -446,15 +498,32 @@ __global__ __launch_bounds__(1024) static void argmax_records_kernel(const float
 }
 
 // ---- prefill glue ------------------------------------------------------------
-// hidden[t][:] = embed[ids[t]][:]
-__global__ __launch_bounds__(256) static void embedding_kernel(const float *__restrict__ embed,
-                                                               const int *__restrict__ ids, float *__restrict__ hidden,
-                                                               int rows, int H) {
-    OPWORKS_GRID_LOOP(i, int64_t(rows) * H / 4) {
-        const int64_t t = i / (H / 4), c = i % (H / 4);
-        reinterpret_cast<f32x4 *>(hidden)[i] =
-            reinterpret_cast<const f32x4 *>(embed + int64_t(ids[t]) * H)[c];
+// hidden[t][:] = embed[ids[t]][:] (bf16 rows widened), one 16-byte pack of
+// the table per thread
+template <typename WT>
+__global__ __launch_bounds__(256) void embedding_kernel(const WT *__restrict__ embed, const int *__restrict__ ids,
+                                                        float *__restrict__ hidden, int rows, int H) {
+    constexpr int E = WPack<WT>::kElems;
+    const int per_row = H / E;
+    OPWORKS_GRID_LOOP(i, int64_t(rows) * per_row) {
+        const int64_t t = i / per_row, c = i % per_row;
+        const typename WPack<WT>::type v =
+            reinterpret_cast<const typename WPack<WT>::type *>(embed + int64_t(ids[t]) * H)[c];
+        f32x4 *dst = reinterpret_cast<f32x4 *>(hidden + t * H + c * E);
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q)
+            dst[q] = f32x4{WPack<WT>::at(v, 4 * q), WPack<WT>::at(v, 4 * q + 1), WPack<WT>::at(v, 4 * q + 2),
+                           WPack<WT>::at(v, 4 * q + 3)};
     }
+}
+
+// Decode step of a bf16 model: hidden = embed[state.token] widened to fp32.
+template <typename WT>
+__global__ __launch_bounds__(256) void embed_token_kernel(const WT *__restrict__ embed,
+                                                          const StepState *__restrict__ state,
+                                                          float *__restrict__ hidden, int H) {
+    const WT *row = embed + int64_t(state->token) * H;
+    OPWORKS_GRID_LOOP(i, H) { hidden[i] = widen(row[i]); }
 }
 
 // qkv [T][(qh + 2 kvh) D] -> RoPE(q) into q_heads [qh][T][D]; RoPE(k) and v

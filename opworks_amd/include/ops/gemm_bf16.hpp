@@ -38,7 +38,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return static_cast<uint32_t>(float_to_bf16_rne(lo)) | (static_cast<uint32_t>(float_to_bf16_rne(hi)) << 16);
 }
 
-template <typename TA, bool kVec, typename Epi>
+template <typename TA, bool kVec, typename Epi, GemmStore kStore = GemmStore::store>
 __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__restrict__ A,
                                                                     const uint16_t *__restrict__ W,
                                                                     const float *__restrict__ bias,
@@ -175,22 +175,37 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * 128 + bm * 32 + 8 * (r / 4) + 4 * half + (r % 4);
-                if (row < M && col < N)
-                    C[int64_t(row) * N + col] = epi(acc[bm][bn][r] + bv);
+                const float v = epi(acc[bm][bn][r] + bv);
+                if constexpr (kStore == GemmStore::swiglu) {
+                    const float partner = __shfl_xor(v, 1); // lane l ^ 1 holds column col ^ 1
+                    if ((l32 & 1) == 0 && row < M && col + 1 < N)
+                        C[int64_t(row) * (N / 2) + col / 2] = v / (1.f + expf(-v)) * partner;
+                } else if constexpr (kStore == GemmStore::residual) {
+                    if (row < M && col < N)
+                        C[int64_t(row) * N + col] += v;
+                } else {
+                    if (row < M && col < N)
+                        C[int64_t(row) * N + col] = v;
+                }
             }
         }
     }
 }
 
-template <typename TA, typename Epi>
+// C written per kStore (see GemmStore): store, += (residual), or SwiGLU of
+// interleaved (gate, up) column pairs into C[M][N / 2].
+template <typename TA, typename Epi, GemmStore kStore = GemmStore::store>
 void gemm_bf16_launch(const TA *A, const uint16_t *W, const float *bias, float *C, int M, int N, int K, Epi epi,
                       hipStream_t stream) {
+    require(kStore != GemmStore::swiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
     const int tiles = static_cast<int>(blocks_for64(M, kBfBM) * blocks_for64(N, kBfBN));
     const bool vec = aligned16(A) && aligned16(W) && K % 8 == 0;
     if (vec)
-        launch_async(stream, gemm_bf16_mfma_kernel<TA, true, Epi>, tiles, kBfThreads, A, W, bias, C, M, N, K, epi);
+        launch_async(stream, gemm_bf16_mfma_kernel<TA, true, Epi, kStore>, tiles, kBfThreads, A, W, bias, C, M, N, K,
+                     epi);
     else
-        launch_async(stream, gemm_bf16_mfma_kernel<TA, false, Epi>, tiles, kBfThreads, A, W, bias, C, M, N, K, epi);
+        launch_async(stream, gemm_bf16_mfma_kernel<TA, false, Epi, kStore>, tiles, kBfThreads, A, W, bias, C, M, N, K,
+                     epi);
 }
 
 } // namespace opworks::detail

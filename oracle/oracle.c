@@ -681,6 +681,7 @@ typedef struct {
     float eps;
     float *embed, *final_norm, *inv_freq;
     float **in_norm, **post_norm, **wq, **wk, **wv, **wo, **wg, **wu, **wd;
+    int bf16; /* weights hold bf16 values; projections of >= 16 rows round X to bf16 */
     /* session */
     int cap, length;
     float *kc, *vc; /* [L][kvh][cap][D] */
@@ -770,6 +771,43 @@ void orc_llama_reset(void *p, int cap) {
     m->length = 0;
 }
 
+/* LlamaModelBF16 (include/models/llama.cuh:290-291, runtime/weights.cuh:16-94):
+ * projections and the tied embedding are stored as bf16, and so are the norm
+ * weights of a bf16 pack (widened to fp32 on load); every weight is therefore
+ * rounded to bf16 (nearest-even) in place. The forward then follows
+ * linear_dispatch (models/llama.cuh:190-199). */
+void orc_llama_set_bf16(void *p) {
+    orc_llama *m = (orc_llama *)p;
+    const int64_t H = m->H, I = m->I, qw = (int64_t)m->qh * m->D, kw = (int64_t)m->kvh * m->D;
+    orc_round_bf16(m->embed, m->embed, NULL, (int64_t)m->V * H);
+    orc_round_bf16(m->final_norm, m->final_norm, NULL, H);
+    for (int l = 0; l < m->L; ++l) {
+        orc_round_bf16(m->wq[l], m->wq[l], NULL, qw * H);
+        orc_round_bf16(m->wk[l], m->wk[l], NULL, kw * H);
+        orc_round_bf16(m->wv[l], m->wv[l], NULL, kw * H);
+        orc_round_bf16(m->wo[l], m->wo[l], NULL, H * qw);
+        orc_round_bf16(m->wg[l], m->wg[l], NULL, I * H);
+        orc_round_bf16(m->wu[l], m->wu[l], NULL, I * H);
+        orc_round_bf16(m->wd[l], m->wd[l], NULL, H * I);
+        orc_round_bf16(m->in_norm[l], m->in_norm[l], NULL, H);
+        orc_round_bf16(m->post_norm[l], m->post_norm[l], NULL, H);
+    }
+    m->bf16 = 1;
+}
+
+/* linear_dispatch: a bf16 model with rows >= 16 takes the tensor-core GEMM,
+ * which rounds X to bf16 (ops/linear_mma.cuh:49); otherwise ops::linear. */
+static void llama_project(const orc_llama *m, const float *X, const float *W, float *Y, int rows, int in, int out) {
+    if (m->bf16 && rows >= 16) {
+        float *xr = alloc_f((int64_t)rows * in);
+        orc_round_bf16(X, xr, NULL, (int64_t)rows * in);
+        orc_linear(xr, W, Y, rows, in, out);
+        free(xr);
+    } else {
+        orc_linear(X, W, Y, rows, in, out);
+    }
+}
+
 /* argmax_kernel (include/ops/argmax.cuh:9-51): lowest index on ties, NaN never wins. */
 int orc_argmax(const float *x, int n) {
     float best = -INFINITY;
@@ -798,9 +836,9 @@ static int llama_forward(orc_llama *m, const int *ids, int rows, float *logits, 
     for (int l = 0; l < m->L; ++l) {
         float *kc = m->kc + (int64_t)l * kvh * m->cap * D, *vc = m->vc + (int64_t)l * kvh * m->cap * D;
         orc_rms_norm_rows(hidden, m->in_norm[l], normed, rows, H, m->eps);
-        orc_linear(normed, m->wq[l], q, rows, H, (int)qw);
-        orc_linear(normed, m->wk[l], k, rows, H, (int)kw);
-        orc_linear(normed, m->wv[l], v, rows, H, (int)kw);
+        llama_project(m, normed, m->wq[l], q, rows, H, (int)qw);
+        llama_project(m, normed, m->wk[l], k, rows, H, (int)kw);
+        llama_project(m, normed, m->wv[l], v, rows, H, (int)kw);
         orc_rope(q, m->inv_freq, rows, qh, D, pos0);
         orc_rope(k, m->inv_freq, rows, kvh, D, pos0);
         for (int r = 0; r < rows; ++r) /* split_heads into the cache (include/ops/split_heads.cuh:9-18) */
@@ -820,17 +858,17 @@ static int llama_forward(orc_llama *m, const int *ids, int rows, float *logits, 
                 for (int h = 0; h < qh; ++h)
                     memcpy(attn + (int64_t)r * qw + h * D, aheads + ((int64_t)h * rows + r) * D, sizeof(float) * D);
         }
-        orc_linear(attn, m->wo[l], normed, rows, (int)qw, H);
+        llama_project(m, attn, m->wo[l], normed, rows, (int)qw, H);
         for (int64_t i = 0; i < (int64_t)rows * H; ++i) /* add_kernel */
             hidden[i] = hidden[i] + normed[i];
         orc_rms_norm_rows(hidden, m->post_norm[l], normed, rows, H, m->eps);
-        orc_linear(normed, m->wg[l], gate, rows, H, I);
-        orc_linear(normed, m->wu[l], up, rows, H, I);
+        llama_project(m, normed, m->wg[l], gate, rows, H, I);
+        llama_project(m, normed, m->wu[l], up, rows, H, I);
         for (int64_t i = 0; i < (int64_t)rows * I; ++i) { /* swiglu_kernel (include/ops/swiglu.cuh:7-12) */
             const float g = gate[i];
             gate[i] = g / (1.f + expf(-g)) * up[i];
         }
-        orc_linear(gate, m->wd[l], normed, rows, I, H);
+        llama_project(m, gate, m->wd[l], normed, rows, I, H);
         for (int64_t i = 0; i < (int64_t)rows * H; ++i)
             hidden[i] = hidden[i] + normed[i];
         if (captures)

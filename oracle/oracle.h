@@ -42,6 +42,9 @@
  *                        visible value equals the fp32 product x * scale
  *  orc_llama_*           float64 numpy forward of a tiny model; KV-cache
  *                        decode equals full recompute
+ *  orc_llama_set_bf16    weights equal their bf16 rounding (bit patterns);
+ *                        the >= 16-row projection equals the fp32 one on
+ *                        bf16-rounded inputs; float64 forward of a tiny model
  */
 #ifndef OPWORKS_ORACLE_H
 #define OPWORKS_ORACLE_H
@@ -111,6 +114,7 @@ const float *orc_llama_weight(void *m, int kind, int layer);
 void orc_llama_reset(void *m, int cap);
 int orc_llama_prefill(void *m, const int *ids, int n, float *logits, float *captures);
 int orc_llama_decode(void *m, int token, float *logits);
+void orc_llama_set_bf16(void *p);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,7 @@ _SIGS = {
     "orc_rope": (None, [_F, _F, c_int, c_int, c_int, c_int]),
     "orc_argmax": (c_int, [_F, c_int]),
     "orc_swiglu": (None, [_F, _F, _F, ctypes.c_int64]),
+    "orc_llama_set_bf16": (None, [c_void_p]),
     "orc_causal_scale": (None, [_F, c_int, c_int, ctypes.c_float]),
     "orc_llama_create": (c_void_p, [c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_float, c_int,
                                     c_float, c_float, c_float, c_int, c_uint64, c_float, c_int]),
@@ -241,7 +242,7 @@ def argmax(x):
 class Llama:
     """The oracle's Llama forward on seeded weights (one session)."""
 
-    def __init__(self, cfg: dict, seed: int, sd: float = 0.02, norm_init: str = "ones") -> None:
+    def __init__(self, cfg: dict, seed: int, sd: float = 0.02, norm_init: str = "ones", bf16: bool = False) -> None:
         rs = cfg.get("rope_scaling") or {}
         self.cfg = cfg
         self.V = cfg["vocab_size"]
@@ -252,6 +253,8 @@ class Llama:
             cfg.get("head_dim", self.H // cfg["num_attention_heads"]), self.V, cfg["rms_norm_eps"], cfg["rope_theta"],
             int(bool(rs)), rs.get("factor", 0.0), rs.get("low_freq_factor", 0.0), rs.get("high_freq_factor", 0.0),
             rs.get("original_max_position_embeddings", 0), seed, sd, 1 if norm_init == "uniform" else 0)
+        if bf16 or cfg.get("torch_dtype") == "bfloat16":
+            lib().orc_llama_set_bf16(self.h)
 
     def weight(self, kind: int, layer: int, numel: int) -> np.ndarray:
         p = lib().orc_llama_weight(self.h, kind, layer)

@@ -33,8 +33,10 @@ def write_pack(path, tensors: dict, aliases: dict | None = None, extra: dict | N
             f.write(b)
 
 
-def pack_from_oracle(path, model, cfg: dict):
-    """Writes the oracle model's seeded weights as an HF-named fp32 pack (tied LM head alias)."""
+def pack_from_oracle(path, model, cfg: dict, dtype: str = "float32"):
+    """Writes the oracle model's seeded weights as an HF-named pack (tied LM head alias);
+    dtype "bfloat16" stores every tensor as bf16 bits (the oracle's weights must
+    already be bf16 values, e.g. a bf16 oracle model)."""
     H, I, V = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"]
     qh, kvh = cfg["num_attention_heads"], cfg["num_key_value_heads"]
     D = cfg.get("head_dim", H // qh)
@@ -51,6 +53,11 @@ def pack_from_oracle(path, model, cfg: dict):
         t[p + "mlp.down_proj.weight"] = model.weight(8, l, H * I).reshape(H, I)
         t[p + "input_layernorm.weight"] = model.weight(9, l, H)
         t[p + "post_attention_layernorm.weight"] = model.weight(10, l, H)
+    if dtype == "bfloat16":
+        for k, v in t.items():
+            bits = np.ascontiguousarray(v, np.float32).view(np.uint32)
+            assert np.all(bits & 0xFFFF == 0), k  # exact bf16 values
+            t[k] = (bits >> 16).astype(np.uint16)
     hf = {k: v for k, v in cfg.items() if k != "eos_token_id"}
     write_pack(path, t, aliases={"lm_head.weight": "model.embed_tokens.weight"},
-               extra={"config": hf, "eos_token_ids": cfg.get("eos_token_id", [])})
+               extra={"config": hf, "eos_token_ids": cfg.get("eos_token_id", [])}, dtype=dtype)

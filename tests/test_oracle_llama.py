@@ -94,8 +94,17 @@ def test_linear_orders(orc):
     assert np.array_equal(y1[0], orc.gemv(X[:300], W, 300, 70))
 
 
-def _np_forward(model, cfg, ids):
-    """float64 textbook Llama forward (HF semantics) from the oracle's weights."""
+def _bf16_np(a):
+    """Round to bf16, nearest-even, returned as float64 (textbook bit recipe)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    return u.view(np.float32).astype(np.float64)
+
+
+def _np_forward(model, cfg, ids, round_x=False):
+    """float64 textbook Llama forward (HF semantics) from the oracle's weights.
+    round_x: projection inputs rounded to bf16 (the tensor-core path)."""
+    rx = _bf16_np if round_x else (lambda a: a)
     H, I, V, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"], cfg["num_hidden_layers"]
     qh, kvh = cfg["num_attention_heads"], cfg["num_key_value_heads"]
     D = cfg["head_dim"]
@@ -121,6 +130,7 @@ def _np_forward(model, cfg, ids):
 
     for l in range(L):
         h = rms(x, w(9, l, H))
+        h = rx(h)
         q = rope((h @ w(2, l, qh * D * H).reshape(qh * D, H).T).reshape(T, qh, D))
         k = rope((h @ w(3, l, kvh * D * H).reshape(kvh * D, H).T).reshape(T, kvh, D))
         v = (h @ w(4, l, kvh * D * H).reshape(kvh * D, H).T).reshape(T, kvh, D)
@@ -130,11 +140,11 @@ def _np_forward(model, cfg, ids):
             s = np.where(np.tri(T, dtype=bool), s, -np.inf)
             p = np.exp(s - s.max(1, keepdims=True))
             out[:, hh] = (p / p.sum(1, keepdims=True)) @ v[:, hh // (qh // kvh)]
-        x = x + out.reshape(T, qh * D) @ w(5, l, H * qh * D).reshape(H, qh * D).T
-        h = rms(x, w(10, l, H))
+        x = x + rx(out.reshape(T, qh * D)) @ w(5, l, H * qh * D).reshape(H, qh * D).T
+        h = rx(rms(x, w(10, l, H)))
         g = h @ w(6, l, I * H).reshape(I, H).T
         u = h @ w(7, l, I * H).reshape(I, H).T
-        x = x + (g / (1 + np.exp(-g)) * u) @ w(8, l, H * I).reshape(H, I).T
+        x = x + rx(g / (1 + np.exp(-g)) * u) @ w(8, l, H * I).reshape(H, I).T
     return rms(x[-1], w(1, 0, H)) @ w(0, 0, V * H).reshape(V, H).T
 
 
@@ -150,6 +160,41 @@ def test_tiny_model_vs_float64(orc):
     tok2, logits2 = m.decode(tok)
     ref2 = _np_forward(m, TINY, ids + [tok])
     assert np.sqrt(np.mean((logits2 - ref2) ** 2)) / np.sqrt(np.mean(ref2 ** 2)) < 1e-5
+
+
+def test_bf16_model_weights_are_rounded(orc):
+    """LlamaModelBF16: every stored weight (norms too, as a bf16 pack holds them)
+    equals the nearest-even bf16 rounding of the same seeded fp32 draw."""
+    f = orc.Llama(TINY, 31, norm_init="uniform")
+    b = orc.Llama(TINY, 31, norm_init="uniform", bf16=True)
+    H, I, V = TINY["hidden_size"], TINY["intermediate_size"], TINY["vocab_size"]
+    D, qh, kvh = TINY["head_dim"], TINY["num_attention_heads"], TINY["num_key_value_heads"]
+    sizes = {0: V * H, 1: H, 2: qh * D * H, 3: kvh * D * H, 4: kvh * D * H, 5: H * qh * D, 6: I * H, 7: I * H,
+             8: H * I, 9: H, 10: H}
+    for kind, n in sizes.items():
+        wf, wb = f.weight(kind, 1, n), b.weight(kind, 1, n)
+        assert np.all(wb.view(np.uint32) & 0xFFFF == 0), kind
+        assert np.array_equal(wb, _bf16_np(wf).astype(np.float32)), kind
+
+
+@pytest.mark.parametrize("n,round_x", [(7, False), (20, True)])
+def test_bf16_model_vs_float64(orc, n, round_x):
+    """Projections of fewer than 16 rows keep fp32 inputs; from 16 rows they are
+    rounded to bf16 (linear_dispatch, models/llama.cuh:190-199)."""
+    m = orc.Llama(TINY, 32, norm_init="uniform", bf16=True)
+    m.reset(32)
+    ids = [(37 * i + 5) % TINY["vocab_size"] for i in range(n)]
+    tok, logits = m.prefill(ids)
+    ref = _np_forward(m, TINY, ids, round_x=round_x)
+    nrmse = np.sqrt(np.mean((logits - ref) ** 2)) / np.sqrt(np.mean(ref ** 2))
+    if not round_x:
+        assert nrmse < 1e-5
+    else:
+        # fp32 and float64 activations straddle a bf16 rounding boundary now and
+        # then, so the match is looser; the unrounded forward must be far away
+        plain = _np_forward(m, TINY, ids, round_x=False)
+        far = np.sqrt(np.mean((logits - plain) ** 2)) / np.sqrt(np.mean(plain ** 2))
+        assert nrmse < 5e-4 and far > 5 * nrmse, (nrmse, far)
 
 
 # ---- swiglu / causal_scale restatements (include/ops/swiglu.cuh:7-12,
