@@ -221,20 +221,19 @@ def wl_attention_decode(stream, steps, warmup):
             "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
 
 
-def wl_llama(stream, steps, warmup, bf16=False):
-    """Config 5: Llama-3.2-1B architecture, fp32 weights N(0, 0.02) (seeded), RMSNorm gamma = 1, 512
-    uniform-random prompt ids, greedy 256 tokens with the KV cache, no EOS stop. A step is one full
-    generation through the C ABI's greedy loop; value = 255 decode steps / decode wall time (median over
-    steps, after warmup). The roofline is the gate/up GEMV (the largest decode kernel, 134,266,880 B per
-    launch) timed with HIP events on the session stream."""
+def wl_llama(stream, steps, warmup, bf16=False, prompt_len=512, new_tokens=256, published=None):
+    """Config 5: Llama-3.2-1B architecture, fp32 (or bf16) weights N(0, 0.02) (seeded), RMSNorm gamma = 1,
+    prompt_len uniform-random prompt ids, greedy new_tokens tokens with the KV cache, no EOS stop. A step
+    is one full generation through the C ABI's greedy loop; value = (new_tokens - 1) decode steps / decode
+    wall time (median over steps, after warmup). The roofline is the gate/up GEMV (the largest decode
+    kernel: 134,266,880 B per launch in fp32) timed with HIP events on the session stream."""
     from opworks_amd.llama import LLAMA_3_2_1B, LlamaModel
     cfg = dict(LLAMA_3_2_1B, torch_dtype="bfloat16") if bf16 else dict(LLAMA_3_2_1B)
     wb = 2 if bf16 else 4  # bytes per weight
     model = LlamaModel.load_random(cfg, SEED, 0.02, "ones")
     sess = model.session(1024)
     rng = np.random.default_rng(SEED)
-    prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], 512)]
-    new_tokens = 256
+    prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], prompt_len)]
     runs = []
     for i in range(warmup + steps):
         sess.reset()
@@ -260,22 +259,33 @@ def wl_llama(stream, steps, warmup, bf16=False):
         breakdown[k] = entry
     gu_gbs = kernel_bytes["gate_up"] / (breakdown["gate_up"]["avg_us"] * 1e-6) / 1e9
     weight_bytes = wb * (V * H + L * (qkv_w * H + H * H + 2 * I * H + H * I)) + 4 * (2 * L + 1) * H
-    kv_bytes_avg = 2 * L * cfg["num_key_value_heads"] * cfg["head_dim"] * 4 * (512 + new_tokens / 2)
+    kv_bytes_avg = 2 * L * cfg["num_key_value_heads"] * cfg["head_dim"] * 4 * (prompt_len + new_tokens / 2)
     step_gbs = (weight_bytes + kv_bytes_avg) / (dec / (new_tokens - 1) * 1e-3) / 1e9
-    return {"workload": f"llama3.2-1b_{'bf16' if bf16 else 'fp32'}_greedy_prompt512_gen256", "unit": "tok/s",
-            "value": tok_s,
-            "ms": pre + dec, "ttft_ms": round(pre, 3), "decode_ms_per_token": round(dec / (new_tokens - 1), 4),
-            "kernel": f"swiglu_gemv_kernel<8{', bf16' if bf16 else ''}> (gate/up)",
-            "roofline": roofline(gu_gbs, HBM_PEAK_GBS, "GB/s", "hbm",
-                                 traffic=None if bf16 else profiled_traffic("gate_up")),
-            "decode_step_roofline": roofline(step_gbs, HBM_PEAK_GBS, "GB/s", "hbm"),
-            "weight_bytes_per_token": weight_bytes, "kernels": breakdown,
-            "first_tokens": [int(t) for t in runs[-1][2][:8]]}
+    out = {"workload": f"llama3.2-1b_{'bf16' if bf16 else 'fp32'}_greedy_prompt{prompt_len}_gen{new_tokens}",
+           "unit": "tok/s", "value": tok_s,
+           "ms": pre + dec, "ttft_ms": round(pre, 3), "decode_ms_per_token": round(dec / (new_tokens - 1), 4),
+           "kernel": f"swiglu_gemv_kernel<8{', bf16' if bf16 else ''}> (gate/up)",
+           "roofline": roofline(gu_gbs, HBM_PEAK_GBS, "GB/s", "hbm",
+                                traffic=None if bf16 else profiled_traffic("gate_up")),
+           "decode_step_roofline": roofline(step_gbs, HBM_PEAK_GBS, "GB/s", "hbm"),
+           "weight_bytes_per_token": weight_bytes, "kernels": breakdown,
+           "first_tokens": [int(t) for t in runs[-1][2][:8]]}
+    if published:  # the reference's own figure for this exact configuration (other hardware)
+        out["published"] = published
+        out["vs_published"] = round(tok_s / published["decode_tok_s"], 2)
+    return out
 
 
 WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "gemm": wl_gemm, "gemm_bf16": wl_gemm_bf16, "attention": wl_attention,
              "attention_decode": wl_attention_decode, "llama": wl_llama,
-             "llama_bf16": lambda st, k, w: wl_llama(st, k, w, bf16=True)}
+             # the reference's published configurations (README.md:320-339, RTX 4080 SUPER, 128 new tokens)
+             "llama_fp32_p128": lambda st, k, w: wl_llama(
+                 st, k, w, prompt_len=128, new_tokens=128,
+                 published={"decode_tok_s": 127, "hardware": "RTX 4080 SUPER", "source": "README.md:338-339"}),
+             "llama_bf16": lambda st, k, w: wl_llama(
+                 st, k, w, bf16=True, prompt_len=512, new_tokens=128,
+                 published={"decode_tok_s": 215, "ttft_ms": 103.5, "hardware": "RTX 4080 SUPER",
+                            "source": "README.md:320-326"})}
 HEADLINE = "llama"
 
 

@@ -122,6 +122,7 @@ struct LlamaSession {
     TypedDeviceBuffer<int32_t> lm_best_idx, argmax_out, state_buf, ids;
     // prefill
     TypedDeviceBuffer<float> hidden, normed, qkv, q_heads, attn_heads, attn, act;
+    TypedDeviceBuffer<float> splitk_ws; // partial tiles of split-K projections
     int attn_max_chunks = 0;
     int lm_grid = 0;
     llama::StepState *h_state = nullptr; // pinned
@@ -238,6 +239,8 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         s->attn_heads = TypedDeviceBuffer<float>(T * qh * D);
         s->attn = TypedDeviceBuffer<float>(T * qh * D);
         s->act = TypedDeviceBuffer<float>(T * I);
+        if (T >= 2) // only a multi-row prefill runs the GEMMs
+            s->splitk_ws = TypedDeviceBuffer<float>(kBf16 ? detail::kSplitKWorkspaceBf16 : detail::kSplitKWorkspaceF32);
         OPWORKS_HIP_CHECK(hipMemsetAsync(s->state_buf.data(), 0, sizeof(int32_t) * 4, s->stream));
         OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&s->h_state), sizeof(llama::StepState)));
         OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&s->h_token), sizeof(int32_t)));
@@ -776,14 +779,25 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
     // for fp32 weights; for bf16 weights the bf16 MFMA GEMM with A rounded to
     // bf16 on load (the reference's linear_mma_bf16 path, models/llama.cuh:190-199;
     // it takes that path from 16 rows, this build from 2, see the design notes).
+    // Outputs with too few tiles to fill the GPU (o_proj, down, qkv at a few
+    // hundred rows) split K across workgroups into the session's workspace.
     template <detail::GemmStore kStore = detail::GemmStore::store>
-    void project(const float *A, const WT *W, float *C, int M, int N, int K, hipStream_t st) const {
-        if constexpr (kBf16)
-            detail::gemm_bf16_launch<float, detail::IdentityEpilogue, kStore>(
-                A, reinterpret_cast<const uint16_t *>(W), nullptr, C, M, N, K, detail::IdentityEpilogue{}, st);
+    void project(Session &s, const float *A, const WT *W, float *C, int M, int N, int K, hipStream_t st) const {
+        using detail::IdentityEpilogue;
+        constexpr bool kSplittable = kStore != detail::GemmStore::swiglu;
+        const auto *Wb = reinterpret_cast<const uint16_t *>(W);
+        if constexpr (kBf16 && kSplittable)
+            detail::gemm_bf16_launch_splitk<float, IdentityEpilogue, kStore>(
+                A, Wb, nullptr, C, M, N, K, IdentityEpilogue{}, s.splitk_ws.data(), s.splitk_ws.size(), st);
+        else if constexpr (kBf16)
+            detail::gemm_bf16_launch<float, IdentityEpilogue, kStore>(A, Wb, nullptr, C, M, N, K, IdentityEpilogue{},
+                                                                      st);
+        else if constexpr (kSplittable)
+            detail::gemm_f32_launch_splitk<detail::BLayout::nk, IdentityEpilogue, kStore>(
+                A, W, nullptr, C, M, N, K, IdentityEpilogue{}, s.splitk_ws.data(), s.splitk_ws.size(), st);
         else
-            detail::gemm_f32_launch<detail::BLayout::nk, detail::IdentityEpilogue, kStore>(
-                A, W, nullptr, C, M, N, K, detail::IdentityEpilogue{}, st);
+            detail::gemm_f32_launch<detail::BLayout::nk, IdentityEpilogue, kStore>(A, W, nullptr, C, M, N, K,
+                                                                                  IdentityEpilogue{}, st);
     }
 
     void enqueue_prefill(Session &s, int n, const std::function<void(int)> &hook) {
@@ -797,7 +811,7 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         for (int l = 0; l < cfg_.num_layers; ++l) {
             const LlamaLayerWeights<WT> &lw = w_.layers[static_cast<size_t>(l)];
             ops::rms_norm(s.hidden.data(), lw.input_norm.data(), s.normed.data(), n, H, cfg_.rms_norm_eps, st);
-            project(s.normed.data(), lw.wqkv.data(), s.qkv.data(), n, qkvw, H, st);
+            project(s, s.normed.data(), lw.wqkv.data(), s.qkv.data(), n, qkvw, H, st);
             launch_async(st, llama::rope_split_kernel, detail::stream_grid(int64_t(n) * (qh + 2 * kvh) * (D / 2)),
                          256, s.qkv.data(), w_.inv_freq.data(), s.q_heads.data(), layer_k(s, l), layer_v(s, l), n, qh,
                          kvh, D, s.max_seq_len, 0);
@@ -805,10 +819,11 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
                                    cfg_.kv_rep(), D, s.max_seq_len, st);
             launch_async(st, llama::merge_heads_kernel, detail::stream_grid(int64_t(n) * qh * D), 256,
                          s.attn_heads.data(), s.attn.data(), n, qh, D);
-            project<detail::GemmStore::residual>(s.attn.data(), lw.wo.data(), s.hidden.data(), n, H, qh * D, st);
+            project<detail::GemmStore::residual>(s, s.attn.data(), lw.wo.data(), s.hidden.data(), n, H, qh * D,
+                                                 st);
             ops::rms_norm(s.hidden.data(), lw.post_norm.data(), s.normed.data(), n, H, cfg_.rms_norm_eps, st);
-            project<detail::GemmStore::swiglu>(s.normed.data(), lw.wgu.data(), s.act.data(), n, 2 * I, H, st);
-            project<detail::GemmStore::residual>(s.act.data(), lw.wdown.data(), s.hidden.data(), n, H, I, st);
+            project<detail::GemmStore::swiglu>(s, s.normed.data(), lw.wgu.data(), s.act.data(), n, 2 * I, H, st);
+            project<detail::GemmStore::residual>(s, s.act.data(), lw.wdown.data(), s.hidden.data(), n, H, I, st);
             if (hook)
                 hook(l);
         }

@@ -150,31 +150,42 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
         }
     };
 
-    const int ktiles = (K + kBfBK - 1) / kBfBK;
-    if (ktiles > 0) {
-        global_load(0);
+    // K tiles of this workgroup: all of them, or split blockIdx.y's contiguous share
+    const int ktiles_all = (K + kBfBK - 1) / kBfBK;
+    const int per_split = (ktiles_all + gridDim.y - 1) / gridDim.y;
+    const int kt_begin = blockIdx.y * per_split;
+    const int kt_end = kt_begin + per_split < ktiles_all ? kt_begin + per_split : ktiles_all;
+    if (kt_begin < kt_end) {
+        global_load(kt_begin);
         lds_store(0);
         __syncthreads();
-        for (int kt = 0; kt < ktiles; ++kt) {
-            const int buf = kt & 1;
-            if (kt + 1 < ktiles)
+        for (int kt = kt_begin; kt < kt_end; ++kt) {
+            const int buf = (kt - kt_begin) & 1;
+            if (kt + 1 < kt_end)
                 global_load(kt + 1);
             compute(buf);
-            if (kt + 1 < ktiles)
+            if (kt + 1 < kt_end)
                 lds_store(buf ^ 1);
             __syncthreads();
         }
     }
+    if constexpr (kStore == GemmStore::partial)
+        C += int64_t(blockIdx.y) * M * N;
 
 #pragma unroll
     for (int bn = 0; bn < 2; ++bn) {
         const int col = n0 + wn * 64 + bn * 32 + l32;
-        const float bv = (bias != nullptr && col < N) ? bias[col] : 0.f;
+        const float bv = (bias != nullptr && col < N && kStore != GemmStore::partial) ? bias[col] : 0.f;
 #pragma unroll
         for (int bm = 0; bm < 4; ++bm) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * 128 + bm * 32 + 8 * (r / 4) + 4 * half + (r % 4);
+                if constexpr (kStore == GemmStore::partial) {
+                    if (row < M && col < N)
+                        C[int64_t(row) * N + col] = acc[bm][bn][r];
+                    continue;
+                }
                 const float v = epi(acc[bm][bn][r] + bv);
                 if constexpr (kStore == GemmStore::swiglu) {
                     const float partner = __shfl_xor(v, 1); // lane l ^ 1 holds column col ^ 1
@@ -196,16 +207,38 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
 // interleaved (gate, up) column pairs into C[M][N / 2].
 template <typename TA, typename Epi, GemmStore kStore = GemmStore::store>
 void gemm_bf16_launch(const TA *A, const uint16_t *W, const float *bias, float *C, int M, int N, int K, Epi epi,
-                      hipStream_t stream) {
+                      hipStream_t stream, int splits = 1) {
     require(kStore != GemmStore::swiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
     const int tiles = static_cast<int>(blocks_for64(M, kBfBM) * blocks_for64(N, kBfBN));
+    const dim3 grid(tiles, splits);
     const bool vec = aligned16(A) && aligned16(W) && K % 8 == 0;
     if (vec)
-        launch_async(stream, gemm_bf16_mfma_kernel<TA, true, Epi, kStore>, tiles, kBfThreads, A, W, bias, C, M, N, K,
+        launch_async(stream, gemm_bf16_mfma_kernel<TA, true, Epi, kStore>, grid, kBfThreads, A, W, bias, C, M, N, K,
                      epi);
     else
-        launch_async(stream, gemm_bf16_mfma_kernel<TA, false, Epi, kStore>, tiles, kBfThreads, A, W, bias, C, M, N, K,
+        launch_async(stream, gemm_bf16_mfma_kernel<TA, false, Epi, kStore>, grid, kBfThreads, A, W, bias, C, M, N, K,
                      epi);
+}
+
+// Floats of split-K workspace any launch planned by splitk_factor(tiles, ., 256) needs.
+constexpr int64_t kSplitKWorkspaceBf16 = int64_t(256) * kBfBM * kBfBN;
+
+// Split-K form of gemm_bf16_launch for store / residual outputs (see
+// gemm_f32_launch_splitk); 256-wide tiles, so one round of 256 workgroups.
+template <typename TA, typename Epi, GemmStore kStore>
+void gemm_bf16_launch_splitk(const TA *A, const uint16_t *W, const float *bias, float *C, int M, int N, int K,
+                             Epi epi, float *ws, int64_t ws_floats, hipStream_t stream) {
+    const int tiles = static_cast<int>(blocks_for64(M, kBfBM) * blocks_for64(N, kBfBN));
+    const int splits = splitk_factor(tiles, static_cast<int>(blocks_for64(K, kBfBK)), 256);
+    if (splits == 1 || N % 4 != 0 || !ws || int64_t(splits) * M * N > ws_floats || !aligned16(C) ||
+        (bias && !aligned16(bias))) {
+        gemm_bf16_launch<TA, Epi, kStore>(A, W, bias, C, M, N, K, epi, stream);
+        return;
+    }
+    gemm_bf16_launch<TA, IdentityEpilogue, GemmStore::partial>(A, W, nullptr, ws, M, N, K, IdentityEpilogue{}, stream,
+                                                               splits);
+    launch_async(stream, splitk_reduce_kernel<Epi, kStore>, stream_grid(int64_t(M) * N / 4), 256, ws, splits, bias, C,
+                 M, N, epi);
 }
 
 } // namespace opworks::detail

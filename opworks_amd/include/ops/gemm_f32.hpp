@@ -52,7 +52,10 @@ struct IdentityEpilogue {
 //  residual C[row][col] += v                     (C holds the residual stream)
 //  swiglu   columns (2i, 2i+1) hold (gate_i, up_i): C[row][i] = silu(gate) * up,
 //           C is N/2 wide; silu(g) = g / (1 + expf(-g)).
-enum class GemmStore { store, residual, swiglu };
+//  partial  raw accumulators of K split gridDim.y into C[blockIdx.y][M][N]
+//           (split-K; splitk_reduce_kernel sums the splits in order and
+//           applies bias, epilogue and the final store)
+enum class GemmStore { store, residual, swiglu, partial };
 
 // Maps the dispatch-order workgroup id to a (tile_m, tile_n) pair: a band of
 // consecutive tiles per XCD (dispatch is round-robin over XCDs), then
@@ -191,33 +194,44 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f32_mfma_kernel(const float
         }
     };
 
-    const int ktiles = (K + kGemmBK - 1) / kGemmBK;
-    if (ktiles > 0) {
-        global_load(0);
+    // K tiles of this workgroup: all of them, or split blockIdx.y's contiguous share
+    const int ktiles_all = (K + kGemmBK - 1) / kGemmBK;
+    const int per_split = (ktiles_all + gridDim.y - 1) / gridDim.y;
+    const int kt_begin = blockIdx.y * per_split;
+    const int kt_end = kt_begin + per_split < ktiles_all ? kt_begin + per_split : ktiles_all;
+    if (kt_begin < kt_end) {
+        global_load(kt_begin);
         lds_store(0);
         __syncthreads();
-        for (int kt = 0; kt < ktiles; ++kt) {
-            const int buf = kt & 1;
-            if (kt + 1 < ktiles)
+        for (int kt = kt_begin; kt < kt_end; ++kt) {
+            const int buf = (kt - kt_begin) & 1;
+            if (kt + 1 < kt_end)
                 global_load(kt + 1);
             compute(buf);
-            if (kt + 1 < ktiles)
+            if (kt + 1 < kt_end)
                 lds_store(buf ^ 1);
             __syncthreads();
         }
     }
+    if constexpr (kStore == GemmStore::partial)
+        C += int64_t(blockIdx.y) * M * N;
 
     // ---- epilogue: accumulator register r of a 32x32 tile holds
     // row 8*(r/4) + 4*half + r%4, column l32.
 #pragma unroll
     for (int bn = 0; bn < 2; ++bn) {
         const int col = n0 + wn * 64 + bn * 32 + l32;
-        const float bv = (bias != nullptr && col < N) ? bias[col] : 0.f;
+        const float bv = (bias != nullptr && col < N && kStore != GemmStore::partial) ? bias[col] : 0.f;
 #pragma unroll
         for (int bm = 0; bm < 2; ++bm) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * 64 + bm * 32 + 8 * (r / 4) + 4 * half + (r % 4);
+                if constexpr (kStore == GemmStore::partial) {
+                    if (row < M && col < N)
+                        C[int64_t(row) * N + col] = acc[bm][bn][r];
+                    continue;
+                }
                 const float v = epi(acc[bm][bn][r] + bv);
                 if constexpr (kStore == GemmStore::swiglu) {
                     const float partner = __shfl_xor(v, 1); // lane l ^ 1 holds column col ^ 1
@@ -235,6 +249,43 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f32_mfma_kernel(const float
     }
 }
 
+// Split-K epilogue: C = epi(sum_s part[s] + bias) (store) or C += ... (residual),
+// the splits summed in order s = 0, 1, ...; one thread per 4 columns of a row.
+template <typename Epi, GemmStore kStore>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part, int splits,
+                                                            const float *__restrict__ bias, float *__restrict__ C,
+                                                            int M, int N, Epi epi) {
+    static_assert(kStore == GemmStore::store || kStore == GemmStore::residual, "split-K stores or accumulates");
+    const int64_t mn = int64_t(M) * N;
+    OPWORKS_GRID_LOOP(i4, mn / 4) {
+        const int64_t i = 4 * i4;
+        f32x4 sum = *reinterpret_cast<const f32x4 *>(part + i);
+        for (int sp = 1; sp < splits; ++sp) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(part + sp * mn + i);
+            sum = sum + v;
+        }
+        const int col = static_cast<int>(i % N);
+        f32x4 out;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            out[j] = epi(sum[j] + (bias ? bias[col + j] : 0.f));
+        f32x4 *dst = reinterpret_cast<f32x4 *>(C + i);
+        if constexpr (kStore == GemmStore::residual)
+            *dst = *dst + out;
+        else
+            *dst = out;
+    }
+}
+
+// Splits that bring a launch of `tiles` output tiles to about `target`
+// workgroups: a power of two <= 8 with at least 8 K tiles per split (1 = no split).
+inline int splitk_factor(int tiles, int ktiles, int target) {
+    int s = 1;
+    while (s < 8 && tiles * s * 2 <= target && ktiles / (s * 2) >= 8)
+        s *= 2;
+    return s;
+}
+
 inline bool gemm_vec_ok(const void *a, const void *b, int K, int N, BLayout layout) {
     const bool aligned = aligned16(a) && aligned16(b);
     return aligned && K % 4 == 0 && (layout == BLayout::nk || N % 4 == 0);
@@ -243,15 +294,38 @@ inline bool gemm_vec_ok(const void *a, const void *b, int K, int N, BLayout layo
 // Enqueues C[M][N] = epi(A[M][K] B + bias) (written per kStore). K == 0 writes epi(bias or 0).
 template <BLayout kB, typename Epi, GemmStore kStore = GemmStore::store>
 void gemm_f32_launch(const float *A, const float *B, const float *bias, float *C, int M, int N, int K, Epi epi,
-                     hipStream_t stream) {
+                     hipStream_t stream, int splits = 1) {
     require(kStore != GemmStore::swiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
     const int tiles = static_cast<int>(blocks_for64(M, kGemmBM) * blocks_for64(N, kGemmBN));
+    const dim3 grid(tiles, splits);
     if (gemm_vec_ok(A, B, K, N, kB))
-        launch_async(stream, gemm_f32_mfma_kernel<kB, true, Epi, kStore>, tiles, kGemmThreads, A, B, bias, C, M, N, K,
+        launch_async(stream, gemm_f32_mfma_kernel<kB, true, Epi, kStore>, grid, kGemmThreads, A, B, bias, C, M, N, K,
                      epi);
     else
-        launch_async(stream, gemm_f32_mfma_kernel<kB, false, Epi, kStore>, tiles, kGemmThreads, A, B, bias, C, M, N,
+        launch_async(stream, gemm_f32_mfma_kernel<kB, false, Epi, kStore>, grid, kGemmThreads, A, B, bias, C, M, N,
                      K, epi);
+}
+
+// Floats of split-K workspace any launch planned by splitk_factor(tiles, ., 512) needs.
+constexpr int64_t kSplitKWorkspaceF32 = int64_t(512) * kGemmBM * kGemmBN;
+
+// C (store or residual) = epi(A B + bias) with K split across `splits`
+// workgroup rows when the output alone has too few tiles to fill the GPU;
+// the partial tiles go to `ws` (splits * M * N floats) and are summed in order.
+template <BLayout kB, typename Epi, GemmStore kStore>
+void gemm_f32_launch_splitk(const float *A, const float *B, const float *bias, float *C, int M, int N, int K, Epi epi,
+                            float *ws, int64_t ws_floats, hipStream_t stream) {
+    const int tiles = static_cast<int>(blocks_for64(M, kGemmBM) * blocks_for64(N, kGemmBN));
+    const int splits = splitk_factor(tiles, static_cast<int>(blocks_for64(K, kGemmBK)), 512);
+    if (splits == 1 || N % 4 != 0 || !ws || int64_t(splits) * M * N > ws_floats || !aligned16(C) ||
+        (bias && !aligned16(bias))) {
+        gemm_f32_launch<kB, Epi, kStore>(A, B, bias, C, M, N, K, epi, stream);
+        return;
+    }
+    gemm_f32_launch<kB, IdentityEpilogue, GemmStore::partial>(A, B, nullptr, ws, M, N, K, IdentityEpilogue{}, stream,
+                                                              splits);
+    launch_async(stream, splitk_reduce_kernel<Epi, kStore>, stream_grid(int64_t(M) * N / 4), 256, ws, splits, bias, C,
+                 M, N, epi);
 }
 
 } // namespace opworks::detail
