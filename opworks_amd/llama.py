@@ -103,6 +103,7 @@ class LlamaSession:
             raise OpworksError(err.value.decode())
         self.model = model  # sessions keep their model alive
         self.handle = h
+        self.max_seq_len = max_seq_len
         self._err = err
 
     def _check(self, rc: int) -> int:
@@ -148,6 +149,30 @@ class LlamaSession:
                                                     ctypes.byref(dec), self._err, _ERR_LEN))
         return out, pre.value, dec.value
 
+    def generate(self, prompt: Sequence[int], max_new_tokens: int, temperature: float = 0.0, top_p: float = 1.0,
+                 seed: Optional[int] = None) -> list:
+        """Host generation loop with the reference generator's contract
+        (examples/llama/generate.py:111-135): greedy when temperature == 0,
+        else temperature / nucleus sampling of the last logits on the host;
+        stops after an end-of-sequence token or when the next input position
+        would exceed the session capacity."""
+        if len(prompt) + max_new_tokens > self.max_seq_len:
+            raise ValueError(f"prompt ({len(prompt)}) + max_new_tokens ({max_new_tokens}) exceeds capacity "
+                             f"{self.max_seq_len}")
+        rng = np.random.default_rng(seed) if temperature > 0.0 else None
+        self.reset()
+        greedy = self.prefill(prompt)
+        out = []
+        for _ in range(max_new_tokens):
+            tok = sample_top_p(self.last_logits(), rng, temperature, top_p) if rng is not None else greedy
+            out.append(tok)
+            if self.is_eos(tok):
+                break
+            if len(prompt) + len(out) >= self.max_seq_len and len(out) < max_new_tokens:
+                break
+            greedy = self.decode_step(tok)
+        return out
+
     KERNELS_PER_LAYER = ("qkv_rope", "attention", "o_proj", "gate_up", "down")
 
     def profile_decode_step(self, prev_token: int):
@@ -180,3 +205,25 @@ class LlamaSession:
             self.close()
         except Exception:
             pass
+
+
+def sample_top_p(logits: np.ndarray, rng: np.random.Generator, temperature: float = 1.0, top_p: float = 1.0) -> int:
+    """One token from softmax(logits / temperature) restricted to the nucleus:
+    tokens in descending probability while the running sum stays <= top_p,
+    plus the token whose probability crosses top_p and always the most likely
+    token, renormalised (the reference's host sampler, examples/llama/generate.py:83-109)."""
+    z = np.asarray(logits, np.float64) / max(temperature, 1e-6)
+    p = np.exp(z - z.max())
+    p /= p.sum()
+    if top_p < 1.0:
+        order = np.argsort(p)[::-1]
+        csum = np.cumsum(p[order])
+        kept = csum <= top_p
+        kept[0] = True
+        first_over = int(np.searchsorted(csum, top_p))
+        if first_over < kept.size:
+            kept[first_over] = True
+        q = np.zeros_like(p)
+        q[order[kept]] = p[order[kept]]
+        p = q / q.sum()
+    return int(rng.choice(p.size, p=p))
