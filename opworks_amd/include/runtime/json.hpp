@@ -64,9 +64,13 @@ class Value {
             throw std::runtime_error("json: expected a number");
         return num_;
     }
+    // Integral numbers within +-2^53 (exact in a double); anything else,
+    // including inf / nan from overflowing literals, is rejected before the
+    // conversion, which would be undefined outside int64's range.
     int64_t as_int() const {
         const double d = as_number();
-        if (d != static_cast<double>(static_cast<int64_t>(d)))
+        constexpr double kExact = 9007199254740992.0; // 2^53
+        if (!(d >= -kExact && d <= kExact) || d != static_cast<double>(static_cast<int64_t>(d)))
             throw std::runtime_error("json: expected an integer");
         return static_cast<int64_t>(d);
     }

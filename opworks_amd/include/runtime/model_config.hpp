@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdint>
 #include <stdexcept>
+#include <string>
 #include <vector>
 
 #include "json.hpp"
@@ -34,34 +35,51 @@ struct ModelConfig {
     int kv_rep() const { return num_q_heads / num_kv_heads; }
     int qkv_width() const { return q_width() + 2 * kv_width(); }
 
+    // An integer field that fits an int (sizes, counts, token ids).
+    static int int_field(const json::Value &v, const char *what) {
+        const int64_t x = v.as_int();
+        if (x < INT32_MIN || x > INT32_MAX)
+            throw std::runtime_error(std::string("config field ") + what + " out of range");
+        return static_cast<int>(x);
+    }
+
+    // A finite real field that fits a float.
+    static float float_field(const json::Value &v, const char *what) {
+        const double x = v.as_number();
+        if (!(x >= -3.0e38 && x <= 3.0e38))
+            throw std::runtime_error(std::string("config field ") + what + " out of range");
+        return static_cast<float>(x);
+    }
+
     // `config` is the HF config object; `eos` the manifest's eos_token_ids (may be null).
     static ModelConfig from_json(const json::Value &c, const json::Value *eos) {
         ModelConfig m;
-        m.num_layers = static_cast<int>(c.at("num_hidden_layers").as_int());
-        m.hidden_size = static_cast<int>(c.at("hidden_size").as_int());
-        m.intermediate_size = static_cast<int>(c.at("intermediate_size").as_int());
-        m.num_q_heads = static_cast<int>(c.at("num_attention_heads").as_int());
-        m.num_kv_heads = static_cast<int>(c.at("num_key_value_heads").as_int());
-        m.head_dim = c.find("head_dim") ? static_cast<int>(c.at("head_dim").as_int())
+        m.num_layers = int_field(c.at("num_hidden_layers"), "num_hidden_layers");
+        m.hidden_size = int_field(c.at("hidden_size"), "hidden_size");
+        m.intermediate_size = int_field(c.at("intermediate_size"), "intermediate_size");
+        m.num_q_heads = int_field(c.at("num_attention_heads"), "num_attention_heads");
+        m.num_kv_heads = int_field(c.at("num_key_value_heads"), "num_key_value_heads");
+        m.head_dim = c.find("head_dim") ? int_field(c.at("head_dim"), "head_dim")
                                         : (m.num_q_heads > 0 ? m.hidden_size / m.num_q_heads : 0);
-        m.vocab_size = static_cast<int>(c.at("vocab_size").as_int());
-        m.rms_norm_eps = static_cast<float>(c.at("rms_norm_eps").as_number());
-        m.rope_theta = static_cast<float>(c.at("rope_theta").as_number());
+        m.vocab_size = int_field(c.at("vocab_size"), "vocab_size");
+        m.rms_norm_eps = float_field(c.at("rms_norm_eps"), "rms_norm_eps");
+        m.rope_theta = float_field(c.at("rope_theta"), "rope_theta");
         if (const json::Value *rs = c.find("rope_scaling"); rs && !rs->is_null()) {
             if (rs->at("rope_type").as_string() != "llama3")
                 throw std::runtime_error("unsupported rope_scaling type");
             m.rope_llama3 = true;
-            m.rope_factor = static_cast<float>(rs->at("factor").as_number());
-            m.rope_low_freq = static_cast<float>(rs->at("low_freq_factor").as_number());
-            m.rope_high_freq = static_cast<float>(rs->at("high_freq_factor").as_number());
-            m.rope_original_max_pos = static_cast<int>(rs->at("original_max_position_embeddings").as_int());
+            m.rope_factor = float_field(rs->at("factor"), "factor");
+            m.rope_low_freq = float_field(rs->at("low_freq_factor"), "low_freq_factor");
+            m.rope_high_freq = float_field(rs->at("high_freq_factor"), "high_freq_factor");
+            m.rope_original_max_pos =
+                int_field(rs->at("original_max_position_embeddings"), "original_max_position_embeddings");
         }
         if (eos && !eos->is_null()) {
             if (eos->is_array()) {
                 for (const auto &v : eos->as_array())
-                    m.eos_token_ids.push_back(static_cast<int32_t>(v.as_int()));
+                    m.eos_token_ids.push_back(int_field(v, "eos_token_ids"));
             } else {
-                m.eos_token_ids.push_back(static_cast<int32_t>(eos->as_int()));
+                m.eos_token_ids.push_back(int_field(*eos, "eos_token_ids"));
             }
         }
         m.validate();
@@ -76,7 +94,12 @@ struct ModelConfig {
         if (num_layers <= 0 || hidden_size <= 0 || head_dim <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
             num_q_heads % num_kv_heads != 0 || intermediate_size <= 0 || vocab_size <= 0)
             throw std::runtime_error("invalid model config");
-        if (num_q_heads * head_dim != hidden_size)
+        // widths are multiplied together in int (qkv_width, row strides); 2^24
+        // is far above any released Llama and keeps every product in range
+        constexpr int kMaxDim = 1 << 24;
+        if (num_layers > kMaxDim || hidden_size > kMaxDim || intermediate_size > kMaxDim || vocab_size > kMaxDim)
+            throw std::runtime_error("model config dimension out of range");
+        if (static_cast<int64_t>(num_q_heads) * head_dim != hidden_size)
             throw std::runtime_error("num_attention_heads * head_dim != hidden_size");
         if (head_dim % 2 != 0)
             throw std::runtime_error("head_dim must be even");

@@ -71,18 +71,21 @@ class PackReader {
             throw std::runtime_error(path + ": unsupported dtype " + dtype_);
         for (const auto &[name, meta] : manifest_.at("tensors").as_object()) {
             TensorMeta m;
-            m.offset = static_cast<uint64_t>(meta.at("offset").as_int());
+            const int64_t offset = meta.at("offset").as_int();
+            if (offset < 0)
+                throw std::runtime_error(path + ": negative offset in " + name);
+            m.offset = static_cast<uint64_t>(offset);
             m.numel = 1;
             for (const auto &d : meta.at("shape").as_array()) {
                 const int64_t dim = d.as_int();
                 if (dim <= 0)
                     throw std::runtime_error(path + ": non-positive dim in " + name);
-                m.numel *= dim;
-                if (m.numel > (1ll << 40))
+                if (dim > (1ll << 40) / m.numel)
                     throw std::runtime_error(path + ": absurd tensor size in " + name);
+                m.numel *= dim;
                 m.shape.push_back(dim);
             }
-            if (m.offset + static_cast<uint64_t>(m.numel) * elem_size_ > blob_size_)
+            if (m.offset > blob_size_ || static_cast<uint64_t>(m.numel) * elem_size_ > blob_size_ - m.offset)
                 throw std::runtime_error(path + ": tensor " + name + " overruns the data blob");
             tensors_.emplace(name, std::move(m));
         }
