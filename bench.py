@@ -276,8 +276,55 @@ def wl_llama(stream, steps, warmup, bf16=False, prompt_len=512, new_tokens=256, 
     return out
 
 
+def wl_scan(stream, steps, warmup):
+    """ScanBuilder's kernel: inclusive prefix sum over n = 2^28 fp32. Algorithmic bytes 8 B/element (read x,
+    write out); the reduce-then-scan design moves 12 B/element (x is read twice)."""
+    n = 1 << 28
+    x = ow.DeviceBuffer.empty(n)
+    ow.fill_uniform(x, SEED, 3, -1.0, 1.0, stream=stream)
+    out = ow.DeviceBuffer.empty(n)
+    ws_n = ow.ops.scan_workspace_size(n)
+    ws = ow.DeviceBuffer.empty(ws_n)
+    ms = Timer(stream).run(lambda i: ow.ops.scan(x, out, n, "sum", True, ws, ws_n, stream=stream), steps, warmup)
+    nbytes = 8 * n
+    gbs = nbytes / ms / 1e6
+    return {"workload": "scan_sum_inclusive_n2^28", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
+            "moved_bytes": 12 * n, "kernel": "scan_tile_reduce_kernel+scan_partials_kernel+scan_tile_kernel",
+            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+
+
+def wl_transpose(stream, steps, warmup):
+    """TransformBuilder's transpose: 8192 x 8192 fp32 (256 MiB each way), two buffer pairs rotated;
+    8 B/element."""
+    rows = cols = 8192
+    xs, ys = _rotating(rows, cols, 2, lambda b, k: ow.fill_uniform(b, SEED, 30 + k, -1.0, 1.0, stream=stream))
+    ms = Timer(stream).run(lambda i: ow.ops.transpose(xs[i % 2], ys[i % 2], rows, cols, stream=stream), steps,
+                           warmup)
+    nbytes = 8 * rows * cols
+    gbs = nbytes / ms / 1e6
+    return {"workload": "transpose_8192x8192", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
+            "kernel": "transpose_kernel<true>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+
+
+def wl_gather(stream, steps, warmup):
+    """GatherScatterBuilder's gather: out[i] = in[idx[i]] over n = 2^26 with a random permutation;
+    12 B/element algorithmic (index, source element, output). The source side is random, so each
+    element costs a whole memory sector there."""
+    n = 1 << 26
+    x = ow.DeviceBuffer.empty(n)
+    ow.fill_uniform(x, SEED, 40, -1.0, 1.0, stream=stream)
+    idx = ow.DeviceBuffer.from_host(np.random.default_rng(SEED).permutation(n).astype(np.int32), dtype=np.int32)
+    out = ow.DeviceBuffer.empty(n)
+    ms = Timer(stream).run(lambda i: ow.ops.gather(x, n, idx, out, n, stream=stream), steps, warmup)
+    nbytes = 12 * n
+    gbs = nbytes / ms / 1e6
+    return {"workload": "gather_random_permutation_n2^26", "unit": "GB/s", "value": gbs, "ms": ms,
+            "bytes": nbytes, "kernel": "gather_kernel<true>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+
+
 WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "gemm": wl_gemm, "gemm_bf16": wl_gemm_bf16, "attention": wl_attention,
-             "attention_decode": wl_attention_decode, "llama": wl_llama,
+             "attention_decode": wl_attention_decode, "scan": wl_scan, "transpose": wl_transpose,
+             "gather": wl_gather, "llama": wl_llama,
              # the reference's published configurations (README.md:320-339, RTX 4080 SUPER, 128 new tokens)
              "llama_fp32_p128": lambda st, k, w: wl_llama(
                  st, k, w, prompt_len=128, new_tokens=128,

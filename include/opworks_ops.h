@@ -141,6 +141,25 @@ int opw_rope_f32(float *x, const float *inv_freq, int rows, int heads, int head_
 /* out[0] (device int) = index of the maximum; ties -> lowest index, NaN never wins, all-NaN -> 0x7fffffff. */
 int opw_argmax_f32(const float *x, int n, int *out, void *stream);
 
+/* ---- kernels behind the Scan / Transform / GatherScatter builders. The reference builders
+ *      carry only the operation metadata (include/builders/scan.cuh:7-43, transform.cuh:7-38,
+ *      gather_scatter.cuh:7-36) and leave the kernel to their apply() callback. ---- */
+/* Floats of workspace opw_scan_f32 needs for n elements (0 up to 8192); 16-byte aligned. */
+int opw_scan_workspace_size(int n);
+/* op: 0 = sum, 1 = maximum (fmaxf, identity -inf); inclusive: 1 = out[i] covers x[0..i],
+ * 0 = x[0..i-1] with out[0] = identity. In place (out == in) is allowed. workspace == NULL
+ * selects the stream-ordered-allocation convenience overload. */
+int opw_scan_f32(const float *in, float *out, int n, int op, int inclusive, float *workspace, int workspace_size,
+                 void *stream);
+/* out [cols][rows] = transpose of in [rows][cols]; not in place. */
+int opw_transpose_f32(const float *in, float *out, int rows, int cols, void *stream);
+/* out[i] = in[i], i < n (TransformOp::copy and ::reshape). */
+int opw_copy_f32(const float *in, float *out, int n, void *stream);
+/* out[i] = in[idx[i]], i < count; an index outside [0, in_size) writes NaN. */
+int opw_gather_f32(const float *in, long long in_size, const int *idx, float *out, int count, void *stream);
+/* out[idx[i]] = in[i], i < count; an index outside [0, out_size) is skipped; duplicate indices race. */
+int opw_scatter_f32(const float *in, const int *idx, float *out, long long out_size, int count, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -89,6 +89,12 @@ _SIGNATURES = {
     "opw_merge_heads_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
     "opw_rope_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
     "opw_argmax_f32": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
+    "opw_scan_workspace_size": (c_int, [c_int]),
+    "opw_scan_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_int, c_void_p]),
+    "opw_transpose_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "opw_copy_f32": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
+    "opw_gather_f32": (c_int, [c_void_p, c_int64, c_void_p, c_void_p, c_int, c_void_p]),
+    "opw_scatter_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p]),
 }
 
 
@@ -406,6 +412,28 @@ class _Ops:
 
     def argmax(self, x: Ptr, n: int, out: Ptr, stream=None) -> None:
         check(lib().opw_argmax_f32(_p(x), n, _p(out), _stream(stream)))
+
+    SCAN_OPS = {"sum": 0, "maximum": 1}
+
+    def scan_workspace_size(self, n: int) -> int:
+        return check(lib().opw_scan_workspace_size(n))
+
+    def scan(self, x: Ptr, out: Ptr, n: int, op: str = "sum", inclusive: bool = True, workspace: Ptr = None,
+             workspace_size: int = 0, stream=None) -> None:
+        check(lib().opw_scan_f32(_p(x), _p(out), n, self.SCAN_OPS[op], int(inclusive), _p(workspace),
+                                 workspace_size, _stream(stream)))
+
+    def transpose(self, x: Ptr, out: Ptr, rows: int, cols: int, stream=None) -> None:
+        check(lib().opw_transpose_f32(_p(x), _p(out), rows, cols, _stream(stream)))
+
+    def copy(self, x: Ptr, out: Ptr, n: int, stream=None) -> None:
+        check(lib().opw_copy_f32(_p(x), _p(out), n, _stream(stream)))
+
+    def gather(self, x: Ptr, in_size: int, idx: Ptr, out: Ptr, count: int, stream=None) -> None:
+        check(lib().opw_gather_f32(_p(x), in_size, _p(idx), _p(out), count, _stream(stream)))
+
+    def scatter(self, x: Ptr, idx: Ptr, out: Ptr, out_size: int, count: int, stream=None) -> None:
+        check(lib().opw_scatter_f32(_p(x), _p(idx), _p(out), out_size, count, _stream(stream)))
 
 
 ops = _Ops()

@@ -7,13 +7,16 @@
 #include "../include/core/random.hpp"
 #include "../include/ops/argmax.hpp"
 #include "../include/ops/elementwise.hpp"
+#include "../include/ops/gather_scatter.hpp"
 #include "../include/ops/heads.hpp"
 #include "../include/ops/layer_norm.hpp"
 #include "../include/ops/model_pointwise.hpp"
 #include "../include/ops/reduction.hpp"
 #include "../include/ops/rms_norm.hpp"
 #include "../include/ops/rope.hpp"
+#include "../include/ops/scan.hpp"
 #include "../include/ops/softmax.hpp"
+#include "../include/ops/transform.hpp"
 #include "c_api_common.hpp"
 
 using opworks::capi::guard;
@@ -399,6 +402,53 @@ int opw_rope_f32(float *x, const float *inv_freq, int rows, int heads, int head_
 int opw_argmax_f32(const float *x, int n, int *out, void *stream) {
     return guard([&] {
         opworks::ops::argmax(x, n, out, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_scan_workspace_size(int n) {
+    return guard([&] { return opworks::ops::scan_workspace_size(n); });
+}
+
+int opw_scan_f32(const float *in, float *out, int n, int op, int inclusive, float *workspace, int workspace_size,
+                 void *stream) {
+    return guard([&] {
+        if (op != 0 && op != 1)
+            throw std::invalid_argument("unknown scan op (0 sum, 1 maximum)");
+        hipStream_t s = as_stream(stream);
+        if (workspace)
+            opworks::ops::scan(in, out, n, op == 1, inclusive != 0, opworks::DeviceSpan<float>(workspace, workspace_size),
+                               s);
+        else
+            opworks::ops::scan(in, out, n, op == 1, inclusive != 0, s);
+        return 0;
+    });
+}
+
+int opw_transpose_f32(const float *in, float *out, int rows, int cols, void *stream) {
+    return guard([&] {
+        opworks::ops::transpose(in, out, rows, cols, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_copy_f32(const float *in, float *out, int n, void *stream) {
+    return guard([&] {
+        opworks::ops::copy(in, out, n, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_gather_f32(const float *in, long long in_size, const int *idx, float *out, int count, void *stream) {
+    return guard([&] {
+        opworks::ops::gather(in, in_size, idx, out, count, as_stream(stream));
+        return 0;
+    });
+}
+
+int opw_scatter_f32(const float *in, const int *idx, float *out, long long out_size, int count, void *stream) {
+    return guard([&] {
+        opworks::ops::scatter(in, idx, out, out_size, count, as_stream(stream));
         return 0;
     });
 }

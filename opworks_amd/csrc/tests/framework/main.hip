@@ -308,6 +308,34 @@ void metadata_builders() {
     rejects([&] { TransformBuilder(x.view(), y.view(), 3, 2); }, "transform beyond buffer");
     DeviceSpan<const int> no_idx;
     rejects([&] { GatherScatterBuilder(x.view(), y.view(), no_idx, 2, GatherScatterOp::gather); }, "short indices");
+
+    // run(): the kernels this build adds behind the callback boundary
+    auto expect_y = [&](std::initializer_list<float> want, const char *what) {
+        const auto got = y.to_host();
+        int i = 0;
+        for (float w : want)
+            expect(got[i++] == w, what);
+    };
+    ScanBuilder(x.view(), y.view(), 4).run();
+    expect_y({1, 3, 6, 10}, "inclusive prefix sum");
+    ScanBuilder(x.view(), y.view(), 4).op(ScanOp::maximum).inclusive(false).run();
+    expect_y({-INFINITY, 1, 2, 3}, "exclusive prefix maximum");
+    TransformBuilder(x.view(), y.view(), 2, 2, TransformOp::transpose).run();
+    expect_y({1, 3, 2, 4}, "transpose");
+    TransformBuilder(x.view(), y.view(), 1, 4, TransformOp::reshape).run();
+    expect_y({1, 2, 3, 4}, "reshape copies");
+    auto idx = TypedDeviceBuffer<int>::from_host(std::vector<int>{3, 0, 2, 1});
+    GatherScatterBuilder(x.view(), y.view(), DeviceSpan<const int>(idx.data(), 4), 4, GatherScatterOp::gather).run();
+    expect_y({4, 1, 3, 2}, "gather");
+    GatherScatterBuilder(x.view(), y.view(), DeviceSpan<const int>(idx.data(), 4), 4, GatherScatterOp::scatter).run();
+    expect_y({2, 4, 3, 1}, "scatter");
+    auto big = DeviceBuffer::from_host(std::vector<float>(10000, 1.f));
+    DeviceBuffer big_out(10000);
+    DeviceBuffer ws(ops::scan_workspace_size(10000));
+    ScanBuilder(big.view(), big_out.view(), 10000).run(ws.view());
+    const auto prefix = big_out.to_host();
+    for (int i = 0; i < 10000; i += 999)
+        expect(prefix[i] == float(i + 1), "multi-tile prefix sum with a caller workspace");
 }
 
 } // namespace

@@ -1,10 +1,15 @@
 #pragma once
 
 // Scan, Transform and GatherScatter builders: checked descriptions with the
-// apply(fn) callback and no kernel of their own, the same extension points the
-// reference exposes (interfaces: include/builders/scan.cuh,
-// include/builders/transform.cuh, include/builders/gather_scatter.cuh).
+// apply(fn) callback, the extension points the reference exposes (interfaces:
+// include/builders/scan.cuh, include/builders/transform.cuh,
+// include/builders/gather_scatter.cuh). run() is an addition: the reference
+// leaves these operations to the callback, and run() launches this library's
+// kernel for the configured operation on the builder's stream.
 
+#include "../ops/gather_scatter.hpp"
+#include "../ops/scan.hpp"
+#include "../ops/transform.hpp"
 #include "builder_common.hpp"
 
 namespace opworks {
@@ -32,6 +37,13 @@ class ScanBuilder : public detail::CallbackBuilder<ScanBuilder> {
     ScanOp operation() const { return kind_; }
     bool is_inclusive() const { return inclusive_; }
     hipStream_t stream() const { return stream_; }
+
+    // Scratch comes from the stream-ordered allocator; see ops::scan.
+    void run() const { ops::scan(in_.data(), out_.data(), n_, kind_ == ScanOp::maximum, inclusive_, stream_); }
+    // Allocation-free form: `workspace` holds ops::scan_workspace_size(size()) floats.
+    void run(DeviceSpan<float> workspace) const {
+        ops::scan(in_.data(), out_.data(), n_, kind_ == ScanOp::maximum, inclusive_, workspace, stream_);
+    }
 
   private:
     DeviceSpan<const float> in_;
@@ -61,6 +73,14 @@ class TransformBuilder : public detail::CallbackBuilder<TransformBuilder> {
     TransformOp operation() const { return kind_; }
     hipStream_t stream() const { return stream_; }
 
+    // transpose writes a cols x rows matrix; reshape and copy copy rows * cols elements.
+    void run() const {
+        if (kind_ == TransformOp::transpose)
+            ops::transpose(in_.data(), out_.data(), rows_, cols_, stream_);
+        else
+            ops::copy(in_.data(), out_.data(), rows_ * cols_, stream_);
+    }
+
   private:
     DeviceSpan<const float> in_;
     DeviceSpan<float> out_;
@@ -85,6 +105,16 @@ class GatherScatterBuilder : public detail::CallbackBuilder<GatherScatterBuilder
     int count() const { return count_; }
     GatherScatterOp operation() const { return kind_; }
     hipStream_t stream() const { return stream_; }
+
+    // gather bounds indices by input().size(), scatter by output().size().
+    void run() const {
+        if (kind_ == GatherScatterOp::gather) {
+            ops::gather(in_.data(), in_.size(), idx_.data(), out_.data(), count_, stream_);
+        } else {
+            detail::require(in_.size() >= count_, "scatter input is too small");
+            ops::scatter(in_.data(), idx_.data(), out_.data(), out_.size(), count_, stream_);
+        }
+    }
 
   private:
     DeviceSpan<const float> in_;

@@ -889,3 +889,42 @@ int orc_llama_prefill(void *p, const int *ids, int n, float *logits, float *capt
 }
 
 int orc_llama_decode(void *p, int token, float *logits) { return llama_forward((orc_llama *)p, &token, 1, logits, NULL); }
+
+/* ---- Scan / Transform / GatherScatter (semantics stated in oracle.h) ---- */
+void orc_scan(const float *in, float *out, double *abs_prefix, int64_t n, int op, int inclusive) {
+    double run = 0.0, run_abs = 0.0;
+    float best = -INFINITY;
+    for (int64_t i = 0; i < n; ++i) {
+        const float x = in[i];
+        if (!inclusive) {
+            out[i] = op == 1 ? best : (float)run;
+            if (abs_prefix)
+                abs_prefix[i] = run_abs;
+        }
+        run += (double)x;
+        run_abs += fabs((double)x);
+        best = fmaxf(best, x);
+        if (inclusive) {
+            out[i] = op == 1 ? best : (float)run;
+            if (abs_prefix)
+                abs_prefix[i] = run_abs;
+        }
+    }
+}
+
+void orc_transpose(const float *in, float *out, int rows, int cols) {
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c)
+            out[(int64_t)c * rows + r] = in[(int64_t)r * cols + c];
+}
+
+void orc_gather(const float *in, int64_t in_size, const int *idx, float *out, int64_t count) {
+    for (int64_t i = 0; i < count; ++i)
+        out[i] = (idx[i] >= 0 && idx[i] < in_size) ? in[idx[i]] : NAN;
+}
+
+void orc_scatter(const float *in, const int *idx, float *out, int64_t out_size, int64_t count) {
+    for (int64_t i = 0; i < count; ++i)
+        if (idx[i] >= 0 && idx[i] < out_size)
+            out[idx[i]] = in[i];
+}

@@ -42,6 +42,14 @@
  *                        visible value equals the fp32 product x * scale
  *  orc_llama_*           float64 numpy forward of a tiny model; KV-cache
  *                        decode equals full recompute
+ *  orc_scan              closed forms (ones -> i + 1, integers -> triangular
+ *                        numbers, both exact in fp32), exclusive = inclusive
+ *                        shifted, float64 numpy cumsum, running max of
+ *                        monotone and random inputs vs numpy maximum.accumulate
+ *  orc_transpose         numpy .T on ragged shapes; transposing twice is the
+ *                        identity
+ *  orc_gather/scatter    numpy fancy indexing; scatter of a permutation is its
+ *                        inverse gather; out-of-range indices by hand
  *  orc_llama_set_bf16    weights equal their bf16 rounding (bit patterns);
  *                        the >= 16-row projection equals the fp32 one on
  *                        bf16-rounded inputs; float64 forward of a tiny model
@@ -115,6 +123,21 @@ void orc_llama_reset(void *m, int cap);
 int orc_llama_prefill(void *m, const int *ids, int n, float *logits, float *captures);
 int orc_llama_decode(void *m, int token, float *logits);
 void orc_llama_set_bf16(void *p);
+
+/* Kernels behind the Scan / Transform / GatherScatter builders. The reference defines
+ * only their metadata (include/builders/scan.cuh:7-17, transform.cuh:7-18,
+ * gather_scatter.cuh:7-19); these state the meaning this build gives it. */
+/* op 0: prefix sum, the exact float64 running sum rounded to float per element;
+ * op 1: fmaxf fold from -inf. inclusive 0 shifts by one (out[0] = identity).
+ * abs_prefix (may be NULL) receives the float64 running sum of |x| over the same
+ * range, the scale of the tests' error bound. */
+void orc_scan(const float *in, float *out, double *abs_prefix, int64_t n, int op, int inclusive);
+/* out [cols][rows] = in [rows][cols] transposed */
+void orc_transpose(const float *in, float *out, int rows, int cols);
+/* out[i] = in[idx[i]], NaN for an index outside [0, in_size) */
+void orc_gather(const float *in, int64_t in_size, const int *idx, float *out, int64_t count);
+/* out[idx[i]] = in[i] for indices inside [0, out_size), in increasing i */
+void orc_scatter(const float *in, const int *idx, float *out, int64_t out_size, int64_t count);
 
 #ifdef __cplusplus
 }

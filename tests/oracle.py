@@ -55,6 +55,10 @@ _SIGS = {
     "orc_llama_reset": (None, [c_void_p, c_int]),
     "orc_llama_prefill": (c_int, [c_void_p, POINTER(c_int), c_int, _F, _F]),
     "orc_llama_decode": (c_int, [c_void_p, c_int, _F]),
+    "orc_scan": (None, [_F, _F, POINTER(c_double), c_int64, c_int, c_int]),
+    "orc_transpose": (None, [_F, _F, c_int, c_int]),
+    "orc_gather": (None, [_F, c_int64, POINTER(c_int), _F, c_int64]),
+    "orc_scatter": (None, [_F, POINTER(c_int), _F, c_int64, c_int64]),
 }
 
 
@@ -237,6 +241,41 @@ def rope(x, inv_freq, rows, heads, head_dim, pos_start):
 def argmax(x):
     x = f32(x)
     return lib().orc_argmax(fp(x), x.size)
+
+
+def _ip(a: np.ndarray):
+    assert a.dtype == np.int32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(POINTER(c_int))
+
+
+def scan(x, maximum=False, inclusive=True):
+    """Returns (out, abs_prefix): the exact prefix sum (or running fmaxf) and the
+    float64 running sum of |x| over the same range."""
+    x = f32(x)
+    out = np.empty_like(x)
+    absp = np.empty(x.size, np.float64)
+    lib().orc_scan(fp(x), fp(out), absp.ctypes.data_as(POINTER(c_double)), x.size, int(maximum), int(inclusive))
+    return out, absp
+
+
+def transpose(x, rows, cols):
+    x = f32(x)
+    out = np.empty(rows * cols, np.float32)
+    lib().orc_transpose(fp(x), fp(out), rows, cols)
+    return out
+
+
+def gather(x, idx):
+    x, idx = f32(x), np.ascontiguousarray(idx, np.int32)
+    out = np.empty(idx.size, np.float32)
+    lib().orc_gather(fp(x), x.size, _ip(idx), fp(out), idx.size)
+    return out
+
+
+def scatter(x, idx, out):
+    x, idx, out = f32(x), np.ascontiguousarray(idx, np.int32), f32(out).copy()
+    lib().orc_scatter(fp(x), _ip(idx), fp(out), out.size, idx.size)
+    return out
 
 
 class Llama:

@@ -87,3 +87,34 @@ def test_workspace_sizes(ow):
     assert ow.ops.reduction_workspace_size(8192) == 0  # one chunk: single launch
     assert ow.ops.reduction_workspace_size(8193) == 2
     assert ow.ops.reduction_workspace_size(1 << 28) == (1 << 28) // 8192
+
+
+def test_scan_transform_gather_contracts(ow):
+    E = ow.OpworksError
+    ops = ow.ops
+    assert ops.scan_workspace_size(0) == 0
+    assert ops.scan_workspace_size(8192) == 0  # one tile: single launch
+    assert ops.scan_workspace_size(8193) == 2
+    assert ops.scan_workspace_size(1 << 28) == (1 << 28) // 8192
+    ops.scan(None, None, 0)  # n == 0 is a no-op
+    ops.transpose(None, None, 0, 5)
+    ops.gather(None, 0, None, None, 0)
+    ops.scatter(None, None, None, 0, 0)
+    with pytest.raises(E, match="unknown scan op"):
+        ow.check(ow.lib().opw_scan_f32(1, 1, 4, 7, 1, None, 0, None))
+    with pytest.raises(E, match="non-null"):
+        ops.scan(None, None, 4)
+    with pytest.raises(E, match="workspace is too small"):
+        ops.scan(1, 1, 9000, workspace=1, workspace_size=1)
+    with pytest.raises(E, match="16-byte aligned"):
+        ops.scan(1, 1, 9000, workspace=4, workspace_size=2)
+    with pytest.raises(E, match="nonnegative"):
+        ops.scan(None, None, -1)
+    with pytest.raises(E, match="in place"):
+        ops.transpose(16, 16, 4, 4)
+    with pytest.raises(E, match="nonnegative"):
+        ops.transpose(None, None, -1, 4)
+    with pytest.raises(E, match="non-null"):
+        ops.gather(None, 10, 16, 32, 4)
+    with pytest.raises(E, match="nonnegative"):
+        ops.scatter(16, 32, 48, -1, 4)

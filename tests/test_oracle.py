@@ -272,3 +272,59 @@ def test_attention_decode_equals_last_row(orc, length):
     # the decode query is the prefill row at position length - 1 (T = 1, S = length)
     exp_, bound = orc.attention_explicit(q, k, v, 1, length, qh, kv_rep, D, cap)
     assert np.max(np.abs(dec - exp_[:, 0]) / (bound[:, 0] + 1e-12)) < 1e-5
+
+
+# ---- Scan / Transform / GatherScatter oracle (semantics defined in oracle.h) ----
+
+def test_scan_closed_forms(orc):
+    n = 5000
+    ones = np.ones(n, np.float32)
+    out, absp = orc.scan(ones)
+    assert np.array_equal(out, np.arange(1, n + 1, dtype=np.float32)) and np.array_equal(absp, np.arange(1, n + 1))
+    excl, _ = orc.scan(ones, inclusive=False)
+    assert np.array_equal(excl, np.arange(0, n, dtype=np.float32))
+    ints = np.arange(n, dtype=np.float32)  # triangular numbers stay below 2^24: exact in fp32
+    out, _ = orc.scan(ints)
+    assert np.array_equal(out, (np.arange(n, dtype=np.int64) * (np.arange(n) + 1) // 2).astype(np.float32))
+    assert np.array_equal(orc.scan(np.zeros(0, np.float32))[0], np.zeros(0, np.float32))
+
+
+def test_scan_matches_float64_cumsum_and_running_max(orc):
+    x = orc.fill_normal(10007, 21, 0, 0.0, 1.0)
+    out, absp = orc.scan(x)
+    assert np.array_equal(out, np.cumsum(x.astype(np.float64)).astype(np.float32))
+    assert np.allclose(absp, np.cumsum(np.abs(x.astype(np.float64))))
+    excl, _ = orc.scan(x, inclusive=False)
+    assert excl[0] == 0.0 and np.array_equal(excl[1:], out[:-1])
+    mx, _ = orc.scan(x, maximum=True)
+    assert np.array_equal(mx, np.maximum.accumulate(x))
+    mex, _ = orc.scan(x, maximum=True, inclusive=False)
+    assert mex[0] == -np.inf and np.array_equal(mex[1:], mx[:-1])
+    mono = np.arange(100, dtype=np.float32)
+    assert np.array_equal(orc.scan(mono, maximum=True)[0], mono)
+    assert np.array_equal(orc.scan(mono[::-1].copy(), maximum=True)[0], np.full(100, 99, np.float32))
+    # fmaxf drops NaN: a NaN-only prefix scans to -inf, later values take over
+    nan_first = np.array([np.nan, np.nan, 2.0, np.nan, 1.0], np.float32)
+    assert np.array_equal(orc.scan(nan_first, maximum=True)[0], np.array([-np.inf, -np.inf, 2, 2, 2], np.float32))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 5), (64, 64), (65, 129), (1000, 3)])
+def test_transpose_oracle(orc, rows, cols):
+    x = orc.fill_uniform(rows * cols, 22, rows, -1.0, 1.0)
+    t = orc.transpose(x, rows, cols)
+    assert np.array_equal(t.reshape(cols, rows), x.reshape(rows, cols).T)
+    assert np.array_equal(orc.transpose(t, cols, rows), x)
+
+
+def test_gather_scatter_oracle(orc):
+    x = orc.fill_uniform(1000, 23, 0, -1.0, 1.0)
+    perm = np.random.default_rng(5).permutation(1000).astype(np.int32)
+    g = orc.gather(x, perm)
+    assert np.array_equal(g, x[perm])
+    # scattering the gathered values back through the same permutation restores x
+    assert np.array_equal(orc.scatter(g, perm, np.zeros(1000, np.float32)), x)
+    bad = np.array([0, -1, 999, 1000, 2**31 - 1], np.int32)
+    gb = orc.gather(x, bad)
+    assert gb[0] == x[0] and gb[2] == x[999] and np.isnan(gb[[1, 3, 4]]).all()
+    sb = orc.scatter(np.array([5, 6, 7], np.float32), np.array([1, -3, 1], np.int32), np.zeros(4, np.float32))
+    assert np.array_equal(sb, np.array([0, 7, 0, 0], np.float32))  # in-order: the last duplicate wins
