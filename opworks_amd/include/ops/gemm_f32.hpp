@@ -8,19 +8,26 @@
 //  * BLayout::nk — B[n][k], k contiguous: ops::linear's Y = X W^T with HF
 //    [out, in] weights (reference include/ops/linear.cuh:18-73).
 //
-// Kernel shape (gfx950):
-//  * workgroup tile 128 x 128, K tile 32, 256 threads = 4 waves in 2 x 2,
-//    each wave owns a 64 x 64 block = 2 x 2 v_mfma_f32_32x32x2_f32 tiles
-//    (64 accumulator registers);
+// Kernel shapes (gfx950), both on v_mfma_f32_16x16x4_f32 with K tiles of 16:
+//  * GemmBig: workgroup tile 256 x 256, 512 threads = 8 waves in 4 x 2, each
+//    wave owns 64 x 128 = 4 x 8 MFMA tiles (128 accumulator registers); used
+//    when the output has at least 256 such tiles (one per CU) and K is not
+//    split, e.g. the 4096^3 GEMM;
+//  * GemmSmall: 128 x 128, 256 threads = 4 waves in 2 x 2, each 64 x 64; for
+//    smaller outputs and the split-K partial tiles.
+// Measured on 4096^3 fp32: 256 x 256 / 8 waves / 16x16x4 at 126-128 TFLOP/s,
+// against 117-120 for every 128 x 128 variant of 32x32x2 or 16x16x4 MFMA, K
+// tile 16 or 32, and one or two register staging sets.
 //  * operands are staged through LDS, double buffered, one barrier per K tile;
 //    the next tile's global loads are issued before the current tile's MFMAs;
-//  * K is permuted per lane half: inside a K tile, MFMA step s of lane half h
-//    uses k = 8*(s/4) + 4*h + s%4. A product sum does not depend on the
-//    order of k, and this order lets a k-contiguous operand (A, and B in the
-//    nk layout) keep its global layout in LDS (rows padded to 36 floats) and
-//    deliver four MFMA steps with one ds_read_b128; the kn-layout B is read
-//    one float per step from rows padded to 136 floats, which keeps the two
-//    lane halves (4 rows apart) on disjoint banks;
+//  * K is permuted per 16-lane group: in a K tile, MFMA step j of lane group g
+//    (lanes 16g .. 16g + 15) uses k = 4g + j. A product sum does not depend on
+//    the order of k, and this order lets a k-contiguous operand (A, and B in
+//    the nk layout) keep its global layout in LDS (rows padded to 20 floats,
+//    so 16 consecutive rows fall on disjoint bank groups) and deliver four
+//    MFMA steps with one ds_read_b128; the kn-layout B is read one float per
+//    step from rows padded to BN + 4 floats, which puts the four lane groups
+//    (4 rows apart) on disjoint banks;
 //  * workgroup ids are remapped so each XCD (its own L2) works on a
 //    contiguous band of tiles, then grouped 8 tile-rows at a time.
 // Accumulation is fp32 on the matrix core; the result differs from a
@@ -37,10 +44,20 @@ enum class BLayout { kn, nk };
 
 using f32x16 = float __attribute__((ext_vector_type(16)));
 
-constexpr int kGemmBM = 128, kGemmBN = 128, kGemmBK = 32;
-constexpr int kGemmThreads = 256;
-constexpr int kGemmLdK = kGemmBK + 4;  // padded row of a k-contiguous tile
-constexpr int kGemmLdN = kGemmBN + 8;  // padded row of the kn-layout B tile
+template <int kBM, int kBN, int kWM, int kWN> struct GemmF32Shape {
+    static constexpr int BM = kBM, BN = kBN, BK = 16, WM = kWM, WN = kWN;
+    static constexpr int kThreads = WM * WN * kWaveSize;
+    static constexpr int TM = BM / WM, TN = BN / WN;   // wave tile
+    static constexpr int FM = TM / 16, FN = TN / 16;   // 16 x 16 MFMA tiles per wave
+    static constexpr int LdK = BK + 4;                 // padded row of a k-contiguous tile
+    static constexpr int LdN = BN + 4;                 // padded row of the kn-layout B tile
+    static constexpr int CA = BM * BK / 4 / kThreads;  // 16-byte A chunks per thread per K tile
+    static constexpr int CB = BN * BK / 4 / kThreads;  // 16-byte B chunks per thread per K tile
+    static_assert(CA * kThreads * 4 == BM * BK && CB * kThreads * 4 == BN * BK, "tile / thread mismatch");
+};
+using GemmSmall = GemmF32Shape<128, 128, 2, 2>;
+using GemmBig = GemmF32Shape<256, 256, 4, 2>;
+constexpr int kGemmBK = 16;
 constexpr int kNumXcd = 8;
 
 struct IdentityEpilogue {
@@ -75,38 +92,36 @@ __device__ __forceinline__ void gemm_tile_of(int bid, int tiles_m, int tiles_n, 
     tn = in_group / gsize;
 }
 
-template <BLayout kB, bool kVec> struct GemmF32Tiles {
-    // LDS stage sizes in floats
-    static constexpr int kA = kGemmBM * kGemmLdK;
-    static constexpr int kB_ = kB == BLayout::kn ? kGemmBK * kGemmLdN : kGemmBN * kGemmLdK;
-    static constexpr int kStage = kA + kB_;
-};
+template <typename Shape, BLayout kB, bool kVec, typename Epi, GemmStore kStore = GemmStore::store>
+__global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const float *__restrict__ A,
+                                                                        const float *__restrict__ B,
+                                                                        const float *__restrict__ bias,
+                                                                        float *__restrict__ C, int M, int N, int K,
+                                                                        Epi epi) {
+    constexpr int BM = Shape::BM, BN = Shape::BN, BK = Shape::BK, T = Shape::kThreads;
+    constexpr int TM = Shape::TM, TN = Shape::TN, FM = Shape::FM, FN = Shape::FN;
+    constexpr int LdK = Shape::LdK, LdN = Shape::LdN, CA = Shape::CA, CB = Shape::CB;
+    constexpr int kA = BM * LdK;                                    // floats of the A stage
+    constexpr int kStage = kA + (kB == BLayout::kn ? BK * LdN : BN * LdK);
+    __shared__ __attribute__((aligned(16))) float lds[2 * kStage];
 
-template <BLayout kB, bool kVec, typename Epi, GemmStore kStore = GemmStore::store>
-__global__ __launch_bounds__(kGemmThreads) void gemm_f32_mfma_kernel(const float *__restrict__ A,
-                                                                     const float *__restrict__ B,
-                                                                     const float *__restrict__ bias,
-                                                                     float *__restrict__ C, int M, int N, int K,
-                                                                     Epi epi) {
-    using Tiles = GemmF32Tiles<kB, kVec>;
-    __shared__ __attribute__((aligned(16))) float lds[2 * Tiles::kStage];
-
-    const int tiles_m = (M + kGemmBM - 1) / kGemmBM, tiles_n = (N + kGemmBN - 1) / kGemmBN;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     int tm, tn;
     gemm_tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * kGemmBM, n0 = tn * kGemmBN;
+    const int m0 = tm * BM, n0 = tn * BN;
     const int tid = threadIdx.x, lane = tid % kWaveSize, wave = tid / kWaveSize;
-    const int wm = wave / 2, wn = wave % 2;
-    const int l32 = lane % 32, half = lane / 32;
+    const int wm = wave / Shape::WN, wn = wave % Shape::WN;
+    const int l16 = lane % 16, grp = lane / 16;
 
-    // ---- global -> register staging (4 x 16 B per operand per thread)
-    f32x4 ra[4], rb[4];
+    // ---- global -> register staging: chunk idx = tid + T i of a tile whose
+    // rows hold BK (k-contiguous) or BN (kn-layout B) floats
+    f32x4 ra[CA], rb[CB];
+    static_assert(CA == CB, "A and B stage the same number of chunks per thread");
     auto load_rows_k = [&](const float *src, int row0, int rows_total, int k0, f32x4 *dst) {
-        // tile of 128 rows x 32 k, k contiguous; thread covers float4 idx = tid + 256 i
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int idx = tid + kGemmThreads * i;
-            const int r = idx / 8, c = (idx % 8) * 4;
+        for (int i = 0; i < CA; ++i) {
+            const int idx = tid + T * i;
+            const int r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
             const int gr = row0 + r, gk = k0 + c;
             if constexpr (kVec) {
                 dst[i] = (gr < rows_total && gk < K) ? *reinterpret_cast<const f32x4 *>(src + int64_t(gr) * K + gk)
@@ -119,11 +134,10 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f32_mfma_kernel(const float
         }
     };
     auto load_b_kn = [&](int k0) {
-        // tile of 32 k x 128 n, n contiguous
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int idx = tid + kGemmThreads * i;
-            const int r = idx / 32, c = (idx % 32) * 4;
+        for (int i = 0; i < CB; ++i) {
+            const int idx = tid + T * i;
+            const int r = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
             const int gk = k0 + r, gn = n0 + c;
             if constexpr (kVec) {
                 rb[i] = (gk < K && gn < N) ? *reinterpret_cast<const f32x4 *>(B + int64_t(gk) * N + gn)
@@ -136,7 +150,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f32_mfma_kernel(const float
         }
     };
     auto global_load = [&](int kt) {
-        const int k0 = kt * kGemmBK;
+        const int k0 = kt * BK;
         load_rows_k(A, m0, M, k0, ra);
         if constexpr (kB == BLayout::kn)
             load_b_kn(k0);
@@ -144,58 +158,60 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f32_mfma_kernel(const float
             load_rows_k(B, n0, N, k0, rb);
     };
     auto lds_store = [&](int buf) {
-        float *As = lds + buf * Tiles::kStage;
-        float *Bs = As + Tiles::kA;
+        float *As = lds + buf * kStage;
+        float *Bs = As + kA;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int idx = tid + kGemmThreads * i;
-            *reinterpret_cast<f32x4 *>(As + (idx / 8) * kGemmLdK + (idx % 8) * 4) = ra[i];
+        for (int i = 0; i < CA; ++i) {
+            const int idx = tid + T * i;
+            *reinterpret_cast<f32x4 *>(As + (idx / (BK / 4)) * LdK + (idx % (BK / 4)) * 4) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < CB; ++i) {
+            const int idx = tid + T * i;
             if constexpr (kB == BLayout::kn)
-                *reinterpret_cast<f32x4 *>(Bs + (idx / 32) * kGemmLdN + (idx % 32) * 4) = rb[i];
+                *reinterpret_cast<f32x4 *>(Bs + (idx / (BN / 4)) * LdN + (idx % (BN / 4)) * 4) = rb[i];
             else
-                *reinterpret_cast<f32x4 *>(Bs + (idx / 8) * kGemmLdK + (idx % 8) * 4) = rb[i];
+                *reinterpret_cast<f32x4 *>(Bs + (idx / (BK / 4)) * LdK + (idx % (BK / 4)) * 4) = rb[i];
         }
     };
 
-    f32x16 acc[2][2];
+    f32x4 acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-            acc[i][j] = f32x16{};
+        for (int j = 0; j < FN; ++j)
+            acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // One K tile = four MFMA steps; lane group g reads k = 4g .. 4g + 3.
     auto compute = [&](int buf) {
-        const float *As = lds + buf * Tiles::kStage;
-        const float *Bs = As + Tiles::kA;
+        const float *As = lds + buf * kStage;
+        const float *Bs = As + kA;
+        const int kk = 4 * grp;
+        f32x4 a[FM], b[FN];
 #pragma unroll
-        for (int g = 0; g < kGemmBK / 8; ++g) {
-            const int kk = 8 * g + 4 * half;
-            f32x4 a[2], b[2];
+        for (int i = 0; i < FM; ++i)
+            a[i] = *reinterpret_cast<const f32x4 *>(As + (wm * TM + i * 16 + l16) * LdK + kk);
 #pragma unroll
-            for (int bm = 0; bm < 2; ++bm)
-                a[bm] = *reinterpret_cast<const f32x4 *>(As + (wm * 64 + bm * 32 + l32) * kGemmLdK + kk);
+        for (int j = 0; j < FN; ++j) {
+            if constexpr (kB == BLayout::kn) {
 #pragma unroll
-            for (int bn = 0; bn < 2; ++bn) {
-                if constexpr (kB == BLayout::kn) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        b[bn][j] = Bs[(kk + j) * kGemmLdN + wn * 64 + bn * 32 + l32];
-                } else {
-                    b[bn] = *reinterpret_cast<const f32x4 *>(Bs + (wn * 64 + bn * 32 + l32) * kGemmLdK + kk);
-                }
+                for (int e = 0; e < 4; ++e)
+                    b[j][e] = Bs[(kk + e) * LdN + wn * TN + j * 16 + l16];
+            } else {
+                b[j] = *reinterpret_cast<const f32x4 *>(Bs + (wn * TN + j * 16 + l16) * LdK + kk);
             }
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int bm = 0; bm < 2; ++bm)
-#pragma unroll
-                    for (int bn = 0; bn < 2; ++bn)
-                        acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[bm][j], b[bn][j], acc[bm][bn], 0, 0, 0);
         }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
     };
 
     // K tiles of this workgroup: all of them, or split blockIdx.y's contiguous share
-    const int ktiles_all = (K + kGemmBK - 1) / kGemmBK;
+    const int ktiles_all = (K + BK - 1) / BK;
     const int per_split = (ktiles_all + gridDim.y - 1) / gridDim.y;
     const int kt_begin = blockIdx.y * per_split;
     const int kt_end = kt_begin + per_split < ktiles_all ? kt_begin + per_split : ktiles_all;
@@ -216,26 +232,26 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_f32_mfma_kernel(const float
     if constexpr (kStore == GemmStore::partial)
         C += int64_t(blockIdx.y) * M * N;
 
-    // ---- epilogue: accumulator register r of a 32x32 tile holds
-    // row 8*(r/4) + 4*half + r%4, column l32.
+    // ---- epilogue: accumulator register r of a 16 x 16 tile holds row
+    // 4 * grp + r, column l16.
 #pragma unroll
-    for (int bn = 0; bn < 2; ++bn) {
-        const int col = n0 + wn * 64 + bn * 32 + l32;
+    for (int j = 0; j < FN; ++j) {
+        const int col = n0 + wn * TN + j * 16 + l16;
         const float bv = (bias != nullptr && col < N && kStore != GemmStore::partial) ? bias[col] : 0.f;
 #pragma unroll
-        for (int bm = 0; bm < 2; ++bm) {
+        for (int i = 0; i < FM; ++i) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * 64 + bm * 32 + 8 * (r / 4) + 4 * half + (r % 4);
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wm * TM + i * 16 + 4 * grp + r;
                 if constexpr (kStore == GemmStore::partial) {
                     if (row < M && col < N)
-                        C[int64_t(row) * N + col] = acc[bm][bn][r];
+                        C[int64_t(row) * N + col] = acc[i][j][r];
                     continue;
                 }
-                const float v = epi(acc[bm][bn][r] + bv);
+                const float v = epi(acc[i][j][r] + bv);
                 if constexpr (kStore == GemmStore::swiglu) {
                     const float partner = __shfl_xor(v, 1); // lane l ^ 1 holds column col ^ 1
-                    if ((l32 & 1) == 0 && row < M && col + 1 < N)
+                    if ((l16 & 1) == 0 && row < M && col + 1 < N)
                         C[int64_t(row) * (N / 2) + col / 2] = v / (1.f + expf(-v)) * partner;
                 } else if constexpr (kStore == GemmStore::residual) {
                     if (row < M && col < N)
@@ -291,23 +307,34 @@ inline bool gemm_vec_ok(const void *a, const void *b, int K, int N, BLayout layo
     return aligned && K % 4 == 0 && (layout == BLayout::nk || N % 4 == 0);
 }
 
+template <typename Shape, BLayout kB, typename Epi, GemmStore kStore>
+void gemm_f32_launch_shape(const float *A, const float *B, const float *bias, float *C, int M, int N, int K, Epi epi,
+                           hipStream_t stream, int splits) {
+    const int tiles = static_cast<int>(blocks_for64(M, Shape::BM) * blocks_for64(N, Shape::BN));
+    const dim3 grid(tiles, splits);
+    if (gemm_vec_ok(A, B, K, N, kB))
+        launch_async(stream, gemm_f32_mfma_kernel<Shape, kB, true, Epi, kStore>, grid, Shape::kThreads, A, B, bias, C,
+                     M, N, K, epi);
+    else
+        launch_async(stream, gemm_f32_mfma_kernel<Shape, kB, false, Epi, kStore>, grid, Shape::kThreads, A, B, bias, C,
+                     M, N, K, epi);
+}
+
 // Enqueues C[M][N] = epi(A[M][K] B + bias) (written per kStore). K == 0 writes epi(bias or 0).
+// GemmBig when K is not split and its tiles alone cover every CU, else GemmSmall.
 template <BLayout kB, typename Epi, GemmStore kStore = GemmStore::store>
 void gemm_f32_launch(const float *A, const float *B, const float *bias, float *C, int M, int N, int K, Epi epi,
                      hipStream_t stream, int splits = 1) {
     require(kStore != GemmStore::swiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
-    const int tiles = static_cast<int>(blocks_for64(M, kGemmBM) * blocks_for64(N, kGemmBN));
-    const dim3 grid(tiles, splits);
-    if (gemm_vec_ok(A, B, K, N, kB))
-        launch_async(stream, gemm_f32_mfma_kernel<kB, true, Epi, kStore>, grid, kGemmThreads, A, B, bias, C, M, N, K,
-                     epi);
+    const int64_t big_tiles = blocks_for64(M, GemmBig::BM) * blocks_for64(N, GemmBig::BN);
+    if (splits == 1 && big_tiles >= 256)
+        gemm_f32_launch_shape<GemmBig, kB, Epi, kStore>(A, B, bias, C, M, N, K, epi, stream, splits);
     else
-        launch_async(stream, gemm_f32_mfma_kernel<kB, false, Epi, kStore>, grid, kGemmThreads, A, B, bias, C, M, N,
-                     K, epi);
+        gemm_f32_launch_shape<GemmSmall, kB, Epi, kStore>(A, B, bias, C, M, N, K, epi, stream, splits);
 }
 
 // Floats of split-K workspace any launch planned by splitk_factor(tiles, ., 512) needs.
-constexpr int64_t kSplitKWorkspaceF32 = int64_t(512) * kGemmBM * kGemmBN;
+constexpr int64_t kSplitKWorkspaceF32 = int64_t(512) * GemmSmall::BM * GemmSmall::BN;
 
 // C (store or residual) = epi(A B + bias) with K split across `splits`
 // workgroup rows when the output alone has too few tiles to fill the GPU;
@@ -315,7 +342,7 @@ constexpr int64_t kSplitKWorkspaceF32 = int64_t(512) * kGemmBM * kGemmBN;
 template <BLayout kB, typename Epi, GemmStore kStore>
 void gemm_f32_launch_splitk(const float *A, const float *B, const float *bias, float *C, int M, int N, int K, Epi epi,
                             float *ws, int64_t ws_floats, hipStream_t stream) {
-    const int tiles = static_cast<int>(blocks_for64(M, kGemmBM) * blocks_for64(N, kGemmBN));
+    const int tiles = static_cast<int>(blocks_for64(M, GemmSmall::BM) * blocks_for64(N, GemmSmall::BN));
     const int splits = splitk_factor(tiles, static_cast<int>(blocks_for64(K, kGemmBK)), 512);
     if (splits == 1 || N % 4 != 0 || !ws || int64_t(splits) * M * N > ws_floats || !aligned16(C) ||
         (bias && !aligned16(bias))) {
