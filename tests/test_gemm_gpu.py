@@ -55,6 +55,22 @@ def test_fused_matmul_matches_oracle(ow, orc, M, N, K, b_t, act):
     check_kscaled(C.to_host().reshape(M, K), ref, absdot)
 
 
+@pytest.mark.parametrize("M,N,K", [(4100, 40, 4000), (4100, 37, 3999), (4096, 64, 4096)])
+@pytest.mark.parametrize("b_t", [False, True])
+def test_big_tile_path_every_element(ow, orc, M, N, K, b_t):
+    """Outputs with at least 256 tiles of 256 x 256 take the 8-wave kernel; ragged edges, the
+    scalar-load variant (inner dim 37) and both B layouts, every output element checked."""
+    A = orc.fill_normal(M * N, SEED, 6, 0.0, 1.0)
+    B = orc.fill_normal(N * K, SEED, 7, 0.0, 1.0)
+    bias = orc.fill_uniform(K, SEED, 8, -0.1, 0.1)
+    C = ow.DeviceBuffer.empty(M * K)
+    dA, dB, dbias = upload(ow, A), upload(ow, B), upload(ow, bias)
+    ow.ops.mat_mul_fused(dA, dB, dbias, C, M, N, K, b_transposed=b_t, activation="relu")
+    orc.set_threads(16)
+    ref, absdot = orc.mat_mul_rows(A, B, M, N, K, bias=bias, b_transposed=b_t, act="relu")
+    check_kscaled(C.to_host().reshape(M, K), ref, absdot)
+
+
 @pytest.mark.parametrize("M,N,K", [(5, 7, 9), (129, 130, 131), (256, 512, 128)])
 def test_plain_matmul_and_misaligned(ow, orc, M, N, K):
     A = orc.fill_normal(M * N + 1, SEED, 4, 0.0, 1.0)
@@ -85,7 +101,7 @@ def test_linear_matches_oracle(ow, orc, rows, in_f, out_f):
 @pytest.mark.slow
 def test_config3_full_size_sampled(ow, orc):
     """Config 3: C = relu(A @ B + bias), M = N = K = 4096, A, B ~ N(0, 1/64), bias ~ U[-0.1, 0.1];
-    every 32nd row (128 rows x 4096 columns) checked against the oracle."""
+    every 31st row (133 rows x 4096 columns) checked against the oracle."""
     M = N = K = 4096
     orc.set_threads(16)
     dA, dB, dbias, dC = (ow.DeviceBuffer.empty(s) for s in (M * N, N * K, K, M * K))
@@ -96,7 +112,7 @@ def test_config3_full_size_sampled(ow, orc):
     A = orc.fill_normal(M * N, SEED, 300, 0.0, 1.0 / 64, mt=True)
     B = orc.fill_normal(N * K, SEED, 301, 0.0, 1.0 / 64, mt=True)
     bias = orc.fill_uniform(K, SEED, 302, -0.1, 0.1)
-    rows = np.arange(0, M, 32)
+    rows = np.arange(0, M, 31)  # 133 rows covering every row residue of the 16- and 256-row tiles
     ref, absdot = orc.mat_mul_rows(A, B, M, N, K, rows=rows, bias=bias, act="relu")
     got = dC.to_host().reshape(M, K)[rows]
     check_kscaled(got, ref, absdot)
