@@ -193,3 +193,54 @@ def test_scatter_skips_out_of_range(ow):
     out = upload(ow, np.zeros(6, np.float32))
     ow.ops.scatter(upload(ow, x), upload(ow, idx, np.int32), out, 6, 5)
     assert np.array_equal(out.to_host(), np.array([4, 0, 0, 0, 1, 0], np.float32))
+
+
+# ------------------------------------------------------------- maximum sizes
+INT_MAX = 2**31 - 1
+CHUNK = 1 << 27
+
+
+@pytest.mark.slow
+def test_scan_at_int_max_exact(ow):
+    """n = INT_MAX (262144 tiles, 8 GiB each way): x[i] = (i mod 3) - 1, whose prefix sums are -1 or 0
+    in any summation order, so every output is checked bit for bit; 8192 mod 3 != 0, so a tile
+    given a neighbour's prefix shows up."""
+    n = INT_MAX
+    d = ow.DeviceBuffer.empty(n)
+    for s in range(0, n, CHUNK):
+        m = min(CHUNK, n - s)
+        d.offset(s, m).copy_from_host((np.arange(s, s + m, dtype=np.int64) % 3 - 1).astype(np.float32))
+    out = ow.DeviceBuffer.empty(n)
+    for inclusive in (True, False):
+        ow.ops.scan(d, out, n, "sum", inclusive)
+        for s in range(0, n, CHUNK):
+            m = min(CHUNK, n - s)
+            i = np.arange(s, s + m, dtype=np.int64) + (1 if inclusive else 0)  # elements covered
+            want = np.where(i % 3 == 0, 0.0, -1.0).astype(np.float32)
+            got = out.offset(s, m).to_host()
+            assert np.array_equal(got, want), (inclusive, s)
+    ow.ops.scan(d, out, n, "maximum", True)
+    got = out.offset(0, 4).to_host()
+    assert np.array_equal(got, np.array([-1, 0, 1, 1], np.float32))
+    assert np.all(out.offset(n - CHUNK, CHUNK).to_host() == 1.0)
+
+
+@pytest.mark.slow
+def test_transpose_at_int_max_elements(ow):
+    """46341 x 46340 (2,147,441,940 elements, 8 GiB each way, ragged tiles on both sides); element
+    values are their own index bits, so every output element names its source."""
+    rows, cols = 46341, 46340
+    n = rows * cols
+    d = ow.DeviceBuffer.empty(n)
+    for s in range(0, n, CHUNK):
+        m = min(CHUNK, n - s)
+        d.offset(s, m).copy_from_host(np.arange(s, s + m, dtype=np.uint32).view(np.float32))
+    out = ow.DeviceBuffer.empty(n)
+    ow.ops.transpose(d, out, rows, cols)
+    # output row c holds in[:, c]; check whole output rows in chunks
+    per = CHUNK // rows
+    for c0 in range(0, cols, per):
+        c1 = min(cols, c0 + per)
+        got = out.offset(c0 * rows, (c1 - c0) * rows).to_host().view(np.uint32).reshape(c1 - c0, rows)
+        want = (np.arange(rows, dtype=np.uint64)[None, :] * cols + np.arange(c0, c1, dtype=np.uint64)[:, None])
+        assert np.array_equal(got, want.astype(np.uint32)), c0
