@@ -53,6 +53,32 @@ template <int kW> __device__ __forceinline__ int pack_index(const RowPos &p, int
     return (k * kW + p.wave_in_row) * kWaveSize + p.lane;
 }
 
+// True when pack k of this lane lies inside the row (always, for exact plans).
+template <int kW, bool kExact> __device__ __forceinline__ bool pack_valid(const RowPos &p, int k, int n4) {
+    return kExact || pack_index<kW>(p, k) < n4;
+}
+
+// Loads this lane's kV packs of its row as one unpredicated batch: a wave past
+// the last row reads the last row and a pack past the row end reads the row's
+// last pack, so every address is valid and no load sits behind a branch.
+// Used by softmax, where the predicated form compiled to one branch and one
+// vmcnt(0) wait per pack (4096 x 1024: 6.13 against 6.96 us). RMSNorm keeps
+// its predicated loads, which measured faster for its 8 packs per lane
+// (8192 x 2048: 21.4 against 22.9 us). Callers mask invalid packs with
+// pack_valid and store only for active waves.
+template <int kW, int kV, bool kExact>
+__device__ __forceinline__ void load_row_packs(const float *__restrict__ in, int rows, int cols, const RowPos &p,
+                                               f32x4 (&v)[kV]) {
+    const int64_t row = p.active ? p.row : rows - 1;
+    const int n4 = cols / 4;
+    const f32x4 *src = reinterpret_cast<const f32x4 *>(in + row * cols);
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+        const int q = pack_index<kW>(p, k);
+        v[k] = __builtin_nontemporal_load(src + (kExact || q < n4 ? q : n4 - 1));
+    }
+}
+
 // Combines one value per wave across the kW waves of a row (fixed order).
 template <int kW, typename Combine>
 __device__ __forceinline__ float row_combine(float v, const RowPos &p, Combine combine) {

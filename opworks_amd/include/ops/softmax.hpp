@@ -16,23 +16,18 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void softmax_rows_reg_kernel(
                                                                                  int cols) {
     const RowPos p = row_position<kW>(rows);
     const int n4 = cols / 4;
-    const f32x4 *src = reinterpret_cast<const f32x4 *>(in + p.row * cols);
     f32x4 x[kV];
+    load_row_packs<kW, kV, kExact>(in, rows, cols, p, x);
     float local_max = kNegInf;
 #pragma unroll
-    for (int k = 0; k < kV; ++k) {
-        const int q = pack_index<kW>(p, k);
-        if (p.active && (kExact || q < n4)) {
-            x[k] = __builtin_nontemporal_load(src + q);
+    for (int k = 0; k < kV; ++k)
+        if (pack_valid<kW, kExact>(p, k, n4))
             local_max = fmaxf(local_max, fmaxf(fmaxf(x[k][0], x[k][1]), fmaxf(x[k][2], x[k][3])));
-        }
-    }
     const float m = row_combine<kW>(wave::max(local_max), p, wave::Max{});
     float local_sum = 0.f;
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
-        const int q = pack_index<kW>(p, k);
-        if (p.active && (kExact || q < n4)) {
+        if (pack_valid<kW, kExact>(p, k, n4)) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 x[k][j] = expf(x[k][j] - m);
