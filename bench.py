@@ -42,16 +42,33 @@ def cpu_threads() -> int:
 
 
 class Timer:
-    """K launches between two events on `stream`, synchronized on both sides."""
+    """K launches between two events on `stream`, synchronized on both sides.
+
+    A launch from Python (ctypes + the HIP runtime) takes several microseconds of host time, longer
+    than a softmax step runs on the GPU. So before the first event an untimed filler (a copy over
+    512 MiB, ~0.17 ms per pass, enough passes to cover the host's enqueue time for the K steps) is
+    queued on the same stream. The K steps then wait in the queue while the filler runs, and the
+    events measure the GPU's back-to-back execution of the K steps, not the host's launch rate."""
+
+    _filler = None
+    FILL_N = 1 << 27  # floats per filler buffer (512 MiB)
 
     def __init__(self, stream):
         self.stream = stream
         self.t0, self.t1 = ow.Event(), ow.Event()
 
+    def _fill(self, steps: int) -> None:
+        if Timer._filler is None:
+            Timer._filler = (ow.DeviceBuffer.empty(self.FILL_N), ow.DeviceBuffer.empty(self.FILL_N))
+        src, dst = Timer._filler
+        for _ in range(1 + steps // 4):  # ~0.17 ms of GPU time per 4 steps of host enqueue
+            ow.ops.copy(src, dst, self.FILL_N, stream=self.stream)
+
     def run(self, fn, steps: int, warmup: int) -> float:
         for i in range(warmup):
             fn(i)
         ow.check(ow.lib().opw_device_synchronize())
+        self._fill(steps)
         self.t0.record(self.stream)
         for i in range(steps):
             fn(i)
