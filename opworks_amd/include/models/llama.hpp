@@ -786,6 +786,19 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         using detail::IdentityEpilogue;
         constexpr bool kSplittable = kStore != detail::GemmStore::swiglu;
         const auto *Wb = reinterpret_cast<const uint16_t *>(W);
+        if constexpr (kBf16) {
+            // 2..15 rows: fp32 inputs against the widened bf16 weights, as the reference's
+            // linear_dispatch does below 16 rows (include/models/llama.cuh:190-199)
+            if (M < 16) {
+                if constexpr (kSplittable)
+                    detail::gemm_f32_launch_splitk<detail::BLayout::nk, IdentityEpilogue, kStore, uint16_t>(
+                        A, Wb, nullptr, C, M, N, K, IdentityEpilogue{}, s.splitk_ws.data(), s.splitk_ws.size(), st);
+                else
+                    detail::gemm_f32_launch<detail::BLayout::nk, IdentityEpilogue, kStore, uint16_t>(
+                        A, Wb, nullptr, C, M, N, K, IdentityEpilogue{}, st);
+                return;
+            }
+        }
         if constexpr (kBf16 && kSplittable)
             detail::gemm_bf16_launch_splitk<float, IdentityEpilogue, kStore>(
                 A, Wb, nullptr, C, M, N, K, IdentityEpilogue{}, s.splitk_ws.data(), s.splitk_ws.size(), st);

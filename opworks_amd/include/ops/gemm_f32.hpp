@@ -34,6 +34,7 @@
 // k-ascending fmaf chain only by summation order.
 
 #include <cstdint>
+#include <type_traits>
 
 #include "../core/hip_utils.hpp"
 #include "elementwise.hpp"
@@ -92,13 +93,17 @@ __device__ __forceinline__ void gemm_tile_of(int bid, int tiles_m, int tiles_n, 
     tn = in_group / gsize;
 }
 
-template <typename Shape, BLayout kB, bool kVec, typename Epi, GemmStore kStore = GemmStore::store>
+// TB: float, or uint16_t for bf16 weights in the nk layout, widened exactly to
+// fp32 (bits << 16) while staged, so the products are fp32 x fp32 on the
+// matrix core (the reference's rows 2..15 path for bf16 weights).
+template <typename Shape, BLayout kB, bool kVec, typename Epi, GemmStore kStore = GemmStore::store,
+          typename TB = float>
 __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const float *__restrict__ A,
-                                                                        const float *__restrict__ B,
+                                                                        const TB *__restrict__ B,
                                                                         const float *__restrict__ bias,
                                                                         float *__restrict__ C, int M, int N, int K,
                                                                         Epi epi) {
-    constexpr int BM = Shape::BM, BN = Shape::BN, BK = Shape::BK, T = Shape::kThreads;
+    constexpr int BM = Shape::BM, BN = Shape::BN, BK = Shape::BK, T_ = Shape::kThreads;
     constexpr int TM = Shape::TM, TN = Shape::TN, FM = Shape::FM, FN = Shape::FN;
     constexpr int LdK = Shape::LdK, LdN = Shape::LdN, CA = Shape::CA, CB = Shape::CB;
     constexpr int kA = BM * LdK;                                    // floats of the A stage
@@ -117,26 +122,43 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
     // rows hold BK (k-contiguous) or BN (kn-layout B) floats
     f32x4 ra[CA], rb[CB];
     static_assert(CA == CB, "A and B stage the same number of chunks per thread");
-    auto load_rows_k = [&](const float *src, int row0, int rows_total, int k0, f32x4 *dst) {
+    static_assert(std::is_same_v<TB, float> || (std::is_same_v<TB, uint16_t> && kB == BLayout::nk),
+                  "bf16 B is supported in the nk layout");
+    // 4 consecutive k of one row: 16 bytes of fp32 or 8 bytes of bf16 (widened)
+    auto load_rows_k = [&](const auto *src, int row0, int rows_total, int k0, f32x4 *dst) {
+        using T = std::remove_cv_t<std::remove_pointer_t<decltype(src)>>;
 #pragma unroll
         for (int i = 0; i < CA; ++i) {
-            const int idx = tid + T * i;
+            const int idx = tid + T_ * i;
             const int r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
             const int gr = row0 + r, gk = k0 + c;
-            if constexpr (kVec) {
-                dst[i] = (gr < rows_total && gk < K) ? *reinterpret_cast<const f32x4 *>(src + int64_t(gr) * K + gk)
-                                                     : f32x4{0.f, 0.f, 0.f, 0.f};
+            const bool in = gr < rows_total;
+            if constexpr (kVec && std::is_same_v<T, float>) {
+                dst[i] = (in && gk < K) ? *reinterpret_cast<const f32x4 *>(src + int64_t(gr) * K + gk)
+                                        : f32x4{0.f, 0.f, 0.f, 0.f};
+            } else if constexpr (kVec) {
+                using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+                const u32x2 b = (in && gk < K) ? *reinterpret_cast<const u32x2 *>(src + int64_t(gr) * K + gk)
+                                               : u32x2{0u, 0u};
+                dst[i] = f32x4{__builtin_bit_cast(float, b[0] << 16), __builtin_bit_cast(float, b[0] & 0xffff0000u),
+                               __builtin_bit_cast(float, b[1] << 16), __builtin_bit_cast(float, b[1] & 0xffff0000u)};
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    dst[i][j] = (gr < rows_total && gk + j < K) ? src[int64_t(gr) * K + gk + j] : 0.f;
+                for (int j = 0; j < 4; ++j) {
+                    if constexpr (std::is_same_v<T, float>)
+                        dst[i][j] = (in && gk + j < K) ? src[int64_t(gr) * K + gk + j] : 0.f;
+                    else
+                        dst[i][j] = (in && gk + j < K)
+                                        ? __builtin_bit_cast(float, uint32_t(src[int64_t(gr) * K + gk + j]) << 16)
+                                        : 0.f;
+                }
             }
         }
     };
     auto load_b_kn = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < CB; ++i) {
-            const int idx = tid + T * i;
+            const int idx = tid + T_ * i;
             const int r = idx / (BN / 4), c = (idx % (BN / 4)) * 4;
             const int gk = k0 + r, gn = n0 + c;
             if constexpr (kVec) {
@@ -162,12 +184,12 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
         float *Bs = As + kA;
 #pragma unroll
         for (int i = 0; i < CA; ++i) {
-            const int idx = tid + T * i;
+            const int idx = tid + T_ * i;
             *reinterpret_cast<f32x4 *>(As + (idx / (BK / 4)) * LdK + (idx % (BK / 4)) * 4) = ra[i];
         }
 #pragma unroll
         for (int i = 0; i < CB; ++i) {
-            const int idx = tid + T * i;
+            const int idx = tid + T_ * i;
             if constexpr (kB == BLayout::kn)
                 *reinterpret_cast<f32x4 *>(Bs + (idx / (BN / 4)) * LdN + (idx % (BN / 4)) * 4) = rb[i];
             else
@@ -307,30 +329,30 @@ inline bool gemm_vec_ok(const void *a, const void *b, int K, int N, BLayout layo
     return aligned && K % 4 == 0 && (layout == BLayout::nk || N % 4 == 0);
 }
 
-template <typename Shape, BLayout kB, typename Epi, GemmStore kStore>
-void gemm_f32_launch_shape(const float *A, const float *B, const float *bias, float *C, int M, int N, int K, Epi epi,
+template <typename Shape, BLayout kB, typename Epi, GemmStore kStore, typename TB = float>
+void gemm_f32_launch_shape(const float *A, const TB *B, const float *bias, float *C, int M, int N, int K, Epi epi,
                            hipStream_t stream, int splits) {
     const int tiles = static_cast<int>(blocks_for64(M, Shape::BM) * blocks_for64(N, Shape::BN));
     const dim3 grid(tiles, splits);
     if (gemm_vec_ok(A, B, K, N, kB))
-        launch_async(stream, gemm_f32_mfma_kernel<Shape, kB, true, Epi, kStore>, grid, Shape::kThreads, A, B, bias, C,
-                     M, N, K, epi);
+        launch_async(stream, gemm_f32_mfma_kernel<Shape, kB, true, Epi, kStore, TB>, grid, Shape::kThreads, A, B, bias,
+                     C, M, N, K, epi);
     else
-        launch_async(stream, gemm_f32_mfma_kernel<Shape, kB, false, Epi, kStore>, grid, Shape::kThreads, A, B, bias, C,
-                     M, N, K, epi);
+        launch_async(stream, gemm_f32_mfma_kernel<Shape, kB, false, Epi, kStore, TB>, grid, Shape::kThreads, A, B,
+                     bias, C, M, N, K, epi);
 }
 
 // Enqueues C[M][N] = epi(A[M][K] B + bias) (written per kStore). K == 0 writes epi(bias or 0).
 // GemmBig when K is not split and its tiles alone cover every CU, else GemmSmall.
-template <BLayout kB, typename Epi, GemmStore kStore = GemmStore::store>
-void gemm_f32_launch(const float *A, const float *B, const float *bias, float *C, int M, int N, int K, Epi epi,
+template <BLayout kB, typename Epi, GemmStore kStore = GemmStore::store, typename TB = float>
+void gemm_f32_launch(const float *A, const TB *B, const float *bias, float *C, int M, int N, int K, Epi epi,
                      hipStream_t stream, int splits = 1) {
     require(kStore != GemmStore::swiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
     const int64_t big_tiles = blocks_for64(M, GemmBig::BM) * blocks_for64(N, GemmBig::BN);
     if (splits == 1 && big_tiles >= 256)
-        gemm_f32_launch_shape<GemmBig, kB, Epi, kStore>(A, B, bias, C, M, N, K, epi, stream, splits);
+        gemm_f32_launch_shape<GemmBig, kB, Epi, kStore, TB>(A, B, bias, C, M, N, K, epi, stream, splits);
     else
-        gemm_f32_launch_shape<GemmSmall, kB, Epi, kStore>(A, B, bias, C, M, N, K, epi, stream, splits);
+        gemm_f32_launch_shape<GemmSmall, kB, Epi, kStore, TB>(A, B, bias, C, M, N, K, epi, stream, splits);
 }
 
 // Floats of split-K workspace any launch planned by splitk_factor(tiles, ., 512) needs.
@@ -339,18 +361,18 @@ constexpr int64_t kSplitKWorkspaceF32 = int64_t(512) * GemmSmall::BM * GemmSmall
 // C (store or residual) = epi(A B + bias) with K split across `splits`
 // workgroup rows when the output alone has too few tiles to fill the GPU;
 // the partial tiles go to `ws` (splits * M * N floats) and are summed in order.
-template <BLayout kB, typename Epi, GemmStore kStore>
-void gemm_f32_launch_splitk(const float *A, const float *B, const float *bias, float *C, int M, int N, int K, Epi epi,
+template <BLayout kB, typename Epi, GemmStore kStore, typename TB = float>
+void gemm_f32_launch_splitk(const float *A, const TB *B, const float *bias, float *C, int M, int N, int K, Epi epi,
                             float *ws, int64_t ws_floats, hipStream_t stream) {
     const int tiles = static_cast<int>(blocks_for64(M, GemmSmall::BM) * blocks_for64(N, GemmSmall::BN));
     const int splits = splitk_factor(tiles, static_cast<int>(blocks_for64(K, kGemmBK)), 512);
     if (splits == 1 || N % 4 != 0 || !ws || int64_t(splits) * M * N > ws_floats || !aligned16(C) ||
         (bias && !aligned16(bias))) {
-        gemm_f32_launch<kB, Epi, kStore>(A, B, bias, C, M, N, K, epi, stream);
+        gemm_f32_launch<kB, Epi, kStore, TB>(A, B, bias, C, M, N, K, epi, stream);
         return;
     }
-    gemm_f32_launch<kB, IdentityEpilogue, GemmStore::partial>(A, B, nullptr, ws, M, N, K, IdentityEpilogue{}, stream,
-                                                              splits);
+    gemm_f32_launch<kB, IdentityEpilogue, GemmStore::partial, TB>(A, B, nullptr, ws, M, N, K, IdentityEpilogue{},
+                                                                  stream, splits);
     launch_async(stream, splitk_reduce_kernel<Epi, kStore>, stream_grid(int64_t(M) * N / 4), 256, ws, splits, bias, C,
                  M, N, epi);
 }

@@ -73,6 +73,23 @@ def test_bf16_debug_prefill_layers(small_bf, n):
     assert nrmse(s.last_logits(), clog) <= BAR
 
 
+@pytest.mark.parametrize("n", [2, 9, 15])
+def test_bf16_short_prefill_uses_fp32_inputs(small_bf, n):
+    """2..15 rows: projections take fp32 inputs against the widened bf16 weights, as the
+    reference's linear_dispatch does below 16 rows, so the GPU agrees with the oracle to fp32
+    summation-order noise, not to the bf16 bar."""
+    gpu, cpu = small_bf
+    ids = prompt(n, SMALL_BF["vocab_size"], 100 + n)
+    s = gpu.session(64)
+    tok, caps = s.debug_prefill(ids)
+    cpu.reset(64)
+    ctok, clog, ccaps = cpu.prefill(ids, capture=True)
+    for layer in range(SMALL_BF["num_hidden_layers"] + 1):
+        assert nrmse(caps[layer], ccaps[layer]) <= 1e-5, layer
+    assert nrmse(s.last_logits(), clog) <= 1e-5
+    assert tok == ctok or margin(clog) < 1e-3
+
+
 def test_bf16_kv_decode_vs_recompute(mid_bf):
     """Decoding token by token equals prefilling the whole sequence (within the bar)."""
     gpu, _ = mid_bf
@@ -108,3 +125,19 @@ def test_bf16_rejects_narrow_widths(ow):
     from tests.test_llama_gpu import TINY
     with pytest.raises(ow.OpworksError, match="bf16"):
         LlamaModel.load_random(dict(TINY, torch_dtype="bfloat16"), 1, 0.02, "ones")
+
+
+@pytest.mark.slow
+def test_config5_bf16_llama_3_2_1b(ow):
+    """Config 5's architecture with bf16 weights (the reference's LlamaModelBF16 path at full size):
+    N(0, 0.02) weights rounded to bf16, gamma = 1, 128 prompt ids, 24 greedy tokens; logits within
+    the bf16 bar at every step, ids identical up to a near tie (margin < 1e-2)."""
+    from opworks_amd.llama import LLAMA_3_2_1B, LlamaModel
+    from tests import oracle as orc
+    orc.set_threads(16)
+    cfg = dict(LLAMA_3_2_1B, torch_dtype="bfloat16")
+    gpu = LlamaModel.load_random(cfg, 1234, 0.02, "ones")
+    cpu = orc.Llama(cfg, 1234, 0.02, "ones")
+    worst, n_same = greedy_bf16(gpu, cpu, prompt(128, cfg["vocab_size"], 1234), 24, cap=256)
+    print(f"config5 bf16: {n_same} identical tokens, worst logits nrmse {worst:.2e}")
+    assert worst <= BAR
