@@ -100,7 +100,11 @@ int opw_device_name(char *out, int out_len) {
         OPWORKS_HIP_CHECK(hipGetDevice(&dev));
         hipDeviceProp_t prop;
         OPWORKS_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
-        std::snprintf(out, static_cast<size_t>(out_len), "%s (%s)", prop.name, prop.gcnArchName);
+        // some driver stacks leave the marketing name empty: then the architecture and CU count name it
+        if (prop.name[0] != '\0')
+            std::snprintf(out, static_cast<size_t>(out_len), "%s (%s)", prop.name, prop.gcnArchName);
+        else
+            std::snprintf(out, static_cast<size_t>(out_len), "%s, %d CUs", prop.gcnArchName, prop.multiProcessorCount);
         return 0;
     });
 }
