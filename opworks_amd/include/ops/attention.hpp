@@ -11,18 +11,23 @@
 // 1/sqrt(D); a row that sees no key writes zeros.
 //
 // ---- prefill (flash) -----------------------------------------------------
-// One workgroup = one kv head x one 32-query tile, with one wave per q head of
-// the GQA group, so each K/V tile is read from HBM once per group and shared
-// through LDS (double buffered). Each wave computes the transposed products
+// One workgroup = one kv head x one 16-query tile, with one wave per q head of
+// the GQA group, so each 32-key K/V tile is read from HBM once per group and
+// shared through LDS (double buffered). Each wave computes the transposed
+// products
 //   S^T = K Q^T  and  O^T += V^T P^T
-// on v_mfma_f32_32x32x2_f32. In that orientation lane l owns query l % 32:
-// the online-softmax max and sum are register reductions plus one exchange
-// between the two lane halves, and the rescale of O is a
-// per-lane multiply. Inside an MFMA chain, step s = 4g + j of lane half h
-// uses reduction index 8g + 4h + j; with that order the S^T accumulator
-// register r = 4g + j of a lane is exactly the P^T operand that lane supplies
-// at step s of the P V chain, so P never moves. Q stays in registers.
-// Workgroups start with the longest (last) query tiles.
+// on v_mfma_f32_16x16x4_f32. In that orientation lane l owns query l % 16 in
+// every tile: the running max is a register reduction plus a combine over the
+// four 16-lane rows (permlane swaps), the row sum stays per lane until the
+// end, and the rescale of O is a per-lane multiply. In the QK^T chain lane
+// group g supplies reduction index (D/4) g + s at step s; its S^T accumulator
+// register r is key 4g + r of the block, which is exactly the P^T operand it
+// supplies at step r of the P V chain, so P never moves. Q stays in registers,
+// pre-scaled by scale * log2(e) so the softmax is exp2.
+// 16-query tiles keep the longest serial chain (the last tile, over all S
+// keys) at half the MFMA work of a 32-query tile and give four resident
+// workgroups per CU; tiles are dispatched heaviest first in alternating passes
+// (prefill_tile_of_rank) so each CU's share of KV tiles is about equal.
 //
 // ---- decode (split-KV) ---------------------------------------------------
 // One workgroup = one kv head x one chunk of kAttnChunk keys: the chunk's K/V
@@ -41,227 +46,276 @@
 
 namespace opworks::detail {
 
-constexpr int kAttnTile = 32;      // queries per wave, keys per KV tile
+constexpr int kAttnQTile = 16;     // queries per wave (columns of a 16x16 MFMA tile)
+constexpr int kAttnKTile = 32;     // keys per staged K/V tile (two 16-key MFMA row blocks)
 constexpr int kAttnMaxD = 64;
-constexpr int kAttnLdK = 64 + 4;   // padded K row (floats)
-constexpr int kAttnLdV = 64 + 8;   // padded V row (floats)
-constexpr int kAttnMaxRep = 16;    // q heads per kv head (waves per workgroup)
+constexpr int kAttnMaxRep = 16;    // q heads per kv head (waves per decode workgroup)
+constexpr float kLog2e = 1.4426950408889634f;
 
-// v[l] (+) v[l ^ 32] in every lane (ds_bpermute exchange between the lane halves).
-template <typename Combine> __device__ __forceinline__ float half_combine(float v, Combine c) {
-    return c(v, __shfl_xor(v, 32));
+// c(x[l], x[l ^ 16]) then c(., .[l ^ 32]): the combine over the four 16-lane
+// rows of a wave, by gfx950's v_permlane16_swap / v_permlane32_swap (a VGPR
+// exchange between rows, no LDS round trip). Both lanes of a pair combine the
+// operands in the same order, so every lane of a column ends bit-identical.
+template <typename Combine> __device__ __forceinline__ float column_combine(float v, Combine c) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = c(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return c(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-// kDT = number of 32-wide head-dim tiles (D padded to 32 * kDT); kWaves = q
-// heads handled by one workgroup (a GQA group, or an 8-head slice of a larger one).
+// kDT = head_dim / 16 (16-wide head-dim tiles); kWaves = q heads handled by
+// one workgroup (a GQA group, or an 8-head slice of a larger one).
 template <int kDT, int kWaves> struct PrefillShape {
-    static constexpr int kDp = 32 * kDT;
-    static constexpr int kStage = kAttnTile * (kAttnLdK + kAttnLdV); // floats per K/V stage
-    static constexpr int kOut = kWaves * kAttnTile * (kDp + 1);      // floats of the output transpose
-    static constexpr int kLdsFloats = 2 * kStage > kOut ? 2 * kStage : kOut;
-    static constexpr int kChunks = kAttnTile * kDp / 4;               // float4 chunks per K (or V) tile
-    static constexpr int kPerThread = (kChunks + kWaves * kWaveSize - 1) / (kWaves * kWaveSize);
+    static constexpr int kD = 16 * kDT;                        // head_dim
+    static constexpr int kLd = kD + 4;                         // LDS row stride of K and V (floats)
+    static constexpr int kLdsFloats = 4 * kAttnKTile * kLd;    // K and V, double buffered
+    static constexpr int kThreads = kWaves * kWaveSize;
+    static constexpr int kChunks = kAttnKTile * kD / 4;        // 16-byte chunks per K (or V) tile
+    static constexpr int kPerThread = (kChunks + kThreads - 1) / kThreads;
+    static constexpr int kQ = kD / 4;                          // Q values per lane = QK^T MFMA steps per block
 };
 
+// Dispatch order of query tiles. Work per tile grows with its index (causal),
+// and the grid is the query tiles x kv heads (x head slices). Ranks go out in
+// passes of `pass_width` tiles (one workgroup per CU per pass); passes run
+// from the heaviest tiles down, alternating direction, so the workgroups one
+// CU receives from successive passes sum to about the same number of KV tiles.
+__device__ __forceinline__ int prefill_tile_of_rank(int rank, int ntq, int pass_width) {
+    const int pass = rank / pass_width, c = rank % pass_width;
+    const int width = min(pass_width, ntq - pass * pass_width);
+    const int pos = pass * pass_width + ((pass & 1) ? width - 1 - c : c);
+    return ntq - 1 - pos;
+}
+
+// amdgpu_waves_per_eu: with four or more waves per workgroup the register budget is 128
+// (four resident waves per SIMD, as many as the LDS allows); the bound also makes the
+// compiler keep the MFMA accumulators in VGPRs rather than AGPRs.
 template <int kDT, int kWaves>
-__global__ __launch_bounds__(kWaves *kWaveSize) void attention_prefill_kernel(
+__global__ __launch_bounds__(kWaves *kWaveSize)
+__attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) void attention_prefill_kernel(
     const float *__restrict__ q_heads, const float *__restrict__ kcache, const float *__restrict__ vcache,
-    float *__restrict__ out, int T, int S, int q_offset, int head_dim, int kv_rep, int num_kv_heads, int cap,
-    float scale) {
+    float *__restrict__ out, int T, int S, int q_offset, int kv_rep, int num_kv_heads, int cap, float qscale,
+    int pass_width) {
     using Shape = PrefillShape<kDT, kWaves>;
-    constexpr int kDp = Shape::kDp;
-    constexpr int kStage = Shape::kStage;
+    constexpr int D = Shape::kD, kLd = Shape::kLd, kQ = Shape::kQ;
     extern __shared__ __attribute__((aligned(16))) float lds[];
 
     const int slices = (kv_rep + kWaves - 1) / kWaves; // workgroups per GQA group
-    const int ntq = (T + kAttnTile - 1) / kAttnTile;
     const int per_tile = num_kv_heads * slices;
-    const int qt = ntq - 1 - static_cast<int>(blockIdx.x) / per_tile; // longest tiles first
+    const int ntq = (T + kAttnQTile - 1) / kAttnQTile;
+    const int qt = prefill_tile_of_rank(static_cast<int>(blockIdx.x) / per_tile, ntq, pass_width);
     const int kvh = (static_cast<int>(blockIdx.x) % per_tile) / slices;
     const int slice = static_cast<int>(blockIdx.x) % slices;
     const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
-    const int l32 = lane % 32, half = lane / 32;
-    const int rep = slice * kWaves + wave;               // head within the group
-    const bool head_ok = rep < kv_rep;                   // idle waves still join barriers
+    const int l16 = lane % 16, g = lane / 16;
+    const int rep = slice * kWaves + wave;  // head within the group
+    const bool head_ok = rep < kv_rep;      // idle waves still stage K/V and join barriers
     const int h = kvh * kv_rep + (head_ok ? rep : 0);
-    const int q0 = qt * kAttnTile;
+    const int q0 = qt * kAttnQTile;
+    const int q = q0 + l16;                 // this lane's query row (column of every MFMA tile)
+    const int qpos = q_offset + q;          // its absolute position
+    const int lim = qpos < S - 1 ? qpos : S - 1; // last key it sees
 
-    const float *kh = kcache + int64_t(kvh) * cap * head_dim;
-    const float *vh = vcache + int64_t(kvh) * cap * head_dim;
+    const float *kh = kcache + int64_t(kvh) * cap * D;
+    const float *vh = vcache + int64_t(kvh) * cap * D;
 
-    // Q^T operand: lane (q = l32, half) keeps Q[q][8g + 4*half + 0..3].
-    constexpr int kG = kDp / 8;
-    f32x4 qreg[kG];
+    // Q^T operand: lane (l16, g) keeps Q[q][kQ*g + s] * scale * log2(e), s < kQ, so the
+    // scores come out in the base-2 exponent domain. Rows past T read row T-1 and are not stored.
+    float qreg[kQ];
     {
-        const int q = q0 + l32;
-        const float *qrow = q_heads + (int64_t(h) * T + (q < T ? q : 0)) * head_dim;
+        const float *qrow = q_heads + (int64_t(h) * T + (q < T ? q : T - 1)) * D + kQ * g;
 #pragma unroll
-        for (int g = 0; g < kG; ++g) {
-            const int d = 8 * g + 4 * half;
+        for (int c = 0; c < kQ / 4; ++c) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(qrow + 4 * c);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                qreg[g][j] = (q < T && d + j < head_dim) ? qrow[d + j] : 0.f;
+                qreg[4 * c + j] = v[j] * qscale;
         }
     }
 
-    const int kv_end = (q_offset + q0 + kAttnTile) < S ? (q_offset + q0 + kAttnTile) : S;
-    const int ntiles = (kv_end + kAttnTile - 1) / kAttnTile;
+    const int kv_end = (q_offset + q0 + kAttnQTile) < S ? (q_offset + q0 + kAttnQTile) : S;
+    const int ntiles = (kv_end + kAttnKTile - 1) / kAttnKTile;
 
-    // K/V tile staging through registers: chunk c = tid + i * threads covers row c / (kDp/4).
-    constexpr int kChunksPerRow = kDp / 4;
-    const bool vec = (head_dim % 4 == 0);
+    // K/V tile staging through registers: chunk c = tid + i * threads is row c / (D/4).
+    // Loads are unconditional (rows past S read row S-1 and are zeroed when staged, chunks
+    // past the tile read its last row and are not staged): a load under a branch makes the
+    // compiler wait for every load in flight before the next one.
+    constexpr int kChunksPerRow = D / 4;
+    constexpr int kStage = 2 * kAttnKTile * kLd; // floats of one K+V stage
     f32x4 kst[Shape::kPerThread], vst[Shape::kPerThread];
+    auto chunk_row = [&](int i) {
+        const int r = (threadIdx.x + i * Shape::kThreads) / kChunksPerRow;
+        return r < kAttnKTile ? r : kAttnKTile - 1;
+    };
     auto fetch = [&](int kt) {
 #pragma unroll
         for (int i = 0; i < Shape::kPerThread; ++i) {
-            const int c = threadIdx.x + i * kWaves * kWaveSize;
-            const int r = c / kChunksPerRow, d = (c % kChunksPerRow) * 4;
-            const int key = kt * kAttnTile + r;
-            kst[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            vst[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (c < Shape::kChunks && key < S) {
-                if (vec) {
-                    if (d < head_dim) {
-                        kst[i] = *reinterpret_cast<const f32x4 *>(kh + int64_t(key) * head_dim + d);
-                        vst[i] = *reinterpret_cast<const f32x4 *>(vh + int64_t(key) * head_dim + d);
-                    }
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        kst[i][j] = d + j < head_dim ? kh[int64_t(key) * head_dim + d + j] : 0.f;
-                        vst[i][j] = d + j < head_dim ? vh[int64_t(key) * head_dim + d + j] : 0.f;
-                    }
-                }
-            }
+            const int key = kt * kAttnKTile + chunk_row(i);
+            const int64_t row = int64_t(key < S ? key : S - 1) * D;
+            const int d = ((threadIdx.x + i * Shape::kThreads) % kChunksPerRow) * 4;
+            kst[i] = *reinterpret_cast<const f32x4 *>(kh + row + d);
+            vst[i] = *reinterpret_cast<const f32x4 *>(vh + row + d);
         }
     };
-    auto commit = [&](int buf) {
+    auto commit = [&](int buf, int kt) {
         float *Ks = lds + buf * kStage;
-        float *Vs = Ks + kAttnTile * kAttnLdK;
+        float *Vs = Ks + kAttnKTile * kLd;
 #pragma unroll
         for (int i = 0; i < Shape::kPerThread; ++i) {
-            const int c = threadIdx.x + i * kWaves * kWaveSize;
-            if (c < Shape::kChunks) {
-                const int r = c / kChunksPerRow, d = (c % kChunksPerRow) * 4;
-                *reinterpret_cast<f32x4 *>(Ks + r * kAttnLdK + d) = kst[i];
-                *reinterpret_cast<f32x4 *>(Vs + r * kAttnLdV + d) = vst[i];
+            const int c = threadIdx.x + i * Shape::kThreads;
+            const bool live = kt * kAttnKTile + chunk_row(i) < S;
+            f32x4 kv, vv;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                kv[j] = live ? kst[i][j] : 0.f;
+                vv[j] = live ? vst[i][j] : 0.f;
+            }
+            if (Shape::kChunks % Shape::kThreads == 0 || c < Shape::kChunks) {
+                const int off = (c / kChunksPerRow) * kLd + (c % kChunksPerRow) * 4;
+                *reinterpret_cast<f32x4 *>(Ks + off) = kv;
+                *reinterpret_cast<f32x4 *>(Vs + off) = vv;
             }
         }
     };
 
-    f32x16 oacc[kDT];
+    f32x4 oacc[kDT];
 #pragma unroll
     for (int t = 0; t < kDT; ++t)
-        oacc[t] = f32x16{};
-    float m_run = kNegInf, l_run = 0.f;
-    const int qpos = q_offset + q0 + l32; // this lane's query position
+        oacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = kNegInf, l_part = 0.f; // l_part: this lane's share of the row sum
 
-    if (ntiles > 0) {
-        fetch(0);
-        commit(0);
-        __syncthreads();
-    }
+    fetch(0);
+    commit(0, 0);
+    __syncthreads();
     for (int kt = 0; kt < ntiles; ++kt) {
         const int buf = kt & 1;
-        if (kt + 1 < ntiles)
-            fetch(kt + 1); // global loads in flight during this tile's MFMAs
+        fetch(kt + 1); // in flight during this tile's MFMAs (all zeros past the last tile)
+        __builtin_amdgcn_sched_barrier(0); // keep the loads at the top
         const float *Ks = lds + buf * kStage;
-        const float *Vs = Ks + kAttnTile * kAttnLdK;
+        const float *Vs = Ks + kAttnKTile * kLd;
 
-        // S^T[key][q] = sum_d K[key][d] Q[q][d]
-        f32x16 sacc = f32x16{};
+        // Operands first: the K fragments of both 16-key blocks and the V^T operands of the
+        // P V chain, so one LDS latency covers the tile.
+        f32x4 kf[2][kQ / 4];
 #pragma unroll
-        for (int g = 0; g < kG; ++g) {
-            const f32x4 kv = *reinterpret_cast<const f32x4 *>(Ks + l32 * kAttnLdK + 8 * g + 4 * half);
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int c = 0; c < kQ / 4; ++c)
+                kf[u][c] = *reinterpret_cast<const f32x4 *>(Ks + (16 * u + l16) * kLd + kQ * g + 4 * c);
+        float vf[2][4][kDT];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int t = 0; t < kDT; ++t)
+                    vf[u][s][t] = Vs[(16 * u + 4 * g + s) * kLd + 16 * t + l16];
+
+        // S^T[key][q] = sum_d K[key][d] Q[q][d] for the two 16-key blocks u; at step s lane
+        // group g supplies reduction index kQ*g + s to both operands, and sacc[u][r] is key
+        // 16u + 4g + r. The blocks' chains alternate so consecutive MFMAs are independent.
+        f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int c = 0; c < kQ / 4; ++c)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[j], qreg[g][j], sacc, 0, 0, 0);
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+                    sacc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[u][c][j], qreg[4 * c + j], sacc[u], 0, 0, 0);
+
+        // Causal mask, only on tiles that reach past the tile's first query position (a
+        // wave-uniform branch: the mask's VALU work sits on the wave's critical path).
+        if (kt * kAttnKTile + kAttnKTile - 1 > q_offset + q0) {
+            const int key0 = kt * kAttnKTile + 4 * g;
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sacc[u][r] = key0 + 16 * u + r > lim ? kNegInf : sacc[u][r];
         }
-        // scale, mask, online softmax (register r holds key 8*(r/4) + 4*half + r%4 of this tile)
+        // Online softmax in base 2. Key 0 is in every row's first tile, so m_new is finite.
         float tmax = kNegInf;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = kt * kAttnTile + 8 * (r / 4) + 4 * half + (r % 4);
-            const float s = (key < S && key <= qpos) ? sacc[r] * scale : kNegInf;
-            sacc[r] = s;
-            tmax = fmaxf(tmax, s);
-        }
-        tmax = half_combine(tmax, wave::Max{});
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                tmax = fmaxf(tmax, sacc[u][r]);
+        tmax = column_combine(tmax, wave::Max{});
         const float m_new = fmaxf(m_run, tmax);
-        const float corr = m_run == kNegInf ? 0.f : expf(m_run - m_new);
+        const float corr = __builtin_amdgcn_exp2f(m_run - m_new); // 0 on the first tile
         float psum = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float p = sacc[r] == kNegInf ? 0.f : expf(sacc[r] - m_new);
-            sacc[r] = p;
-            psum += p;
-        }
-        psum = half_combine(psum, wave::Add{});
-        l_run = l_run * corr + psum;
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = __builtin_amdgcn_exp2f(sacc[u][r] - m_new);
+                sacc[u][r] = p;
+                psum += p;
+            }
+        l_part = l_part * corr + psum;
         m_run = m_new;
 #pragma unroll
         for (int t = 0; t < kDT; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
+            for (int r = 0; r < 4; ++r)
                 oacc[t][r] *= corr;
-        // O^T[d][q] += sum_key V[key][d] P^T[key][q]
+        // O^T[d][q] += sum_key V[key][d] P^T[key][q]: at step s of block u lane group g
+        // supplies key 16u + 4g + s, which is its own S^T register sacc[u][s].
 #pragma unroll
-        for (int t = 0; t < kDT; ++t) {
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
+            for (int s = 0; s < 4; ++s)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float v = Vs[(8 * g + 4 * half + j) * kAttnLdV + 32 * t + l32];
-                    oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(v, sacc[4 * g + j], oacc[t], 0, 0, 0);
-                }
-            }
-        }
-        if (kt + 1 < ntiles)
-            commit(buf ^ 1); // that buffer was last read before the previous barrier
+                for (int t = 0; t < kDT; ++t)
+                    oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[u][s][t], sacc[u][s], oacc[t], 0, 0, 0);
+        // Stage the next tile into the other buffer (last read before the previous barrier);
+        // the fence keeps the staging, which waits for the loads, at the end.
+        __builtin_amdgcn_sched_barrier(0);
+        commit(buf ^ 1, kt + 1);
         __syncthreads();
     }
 
-    // Transpose O^T through LDS (a private 32 x kDp block per wave), then store rows.
-    float *Os = lds + wave * kAttnTile * (kDp + 1);
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    // oacc[t][r] = O^T[16t + 4g + r][q]: four consecutive head-dim values of row q.
+    const float l = column_combine(l_part, wave::Add{});
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    if (head_ok && q < T) {
+        float *orow = out + (int64_t(h) * T + q) * D;
 #pragma unroll
-    for (int t = 0; t < kDT; ++t)
+        for (int t = 0; t < kDT; ++t) {
+            f32x4 o;
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-            Os[l32 * (kDp + 1) + 32 * t + 8 * (r / 4) + 4 * half + (r % 4)] = oacc[t][r] * inv;
-    __syncthreads();
-    if (head_ok) {
-        for (int i = lane; i < kAttnTile * head_dim; i += kWaveSize) {
-            const int q = i / head_dim, d = i % head_dim;
-            if (q0 + q < T)
-                out[(int64_t(h) * T + q0 + q) * head_dim + d] = Os[q * (kDp + 1) + d];
+            for (int r = 0; r < 4; ++r)
+                o[r] = oacc[t][r] * inv;
+            *reinterpret_cast<f32x4 *>(orow + 16 * t + 4 * g) = o;
         }
     }
 }
 
 template <int kDT, int kWaves>
 inline void attention_prefill_launch(const float *q, const float *k, const float *v, float *out, int T, int S,
-                                     int q_offset, int head_dim, int kv_rep, int kvh, int cap, float scale,
-                                     hipStream_t stream) {
+                                     int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream) {
     using Shape = PrefillShape<kDT, kWaves>;
     const int slices = (kv_rep + kWaves - 1) / kWaves;
-    const int grid = static_cast<int>(blocks_for64(T, kAttnTile)) * kvh * slices;
-    launch_async_lds(stream, sizeof(float) * Shape::kLdsFloats, attention_prefill_kernel<kDT, kWaves>, grid,
-                     kWaves * kWaveSize, q, k, v, out, T, S, q_offset, head_dim, kv_rep, kvh, cap, scale);
+    const int per_tile = kvh * slices;
+    const int64_t ntq = blocks_for64(T, kAttnQTile);
+    require(ntq * per_tile <= INT32_MAX, "attention_prefill: grid too large");
+    const int pass_width = cu_count() / per_tile > 0 ? cu_count() / per_tile : 1;
+    launch_async_lds(stream, sizeof(float) * Shape::kLdsFloats, attention_prefill_kernel<kDT, kWaves>,
+                     static_cast<int>(ntq * per_tile), Shape::kThreads, q, k, v, out, T, S, q_offset, kv_rep, kvh,
+                     cap, scale * kLog2e, pass_width);
 }
 
 template <int kDT>
 inline void attention_prefill_dispatch(const float *q, const float *k, const float *v, float *out, int T, int S,
-                                       int q_offset, int head_dim, int kv_rep, int kvh, int cap, float scale,
-                                       hipStream_t stream) {
+                                       int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream) {
     if (kv_rep == 1)
-        attention_prefill_launch<kDT, 1>(q, k, v, out, T, S, q_offset, head_dim, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_launch<kDT, 1>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
     else if (kv_rep == 2)
-        attention_prefill_launch<kDT, 2>(q, k, v, out, T, S, q_offset, head_dim, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_launch<kDT, 2>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
     else if (kv_rep <= 4)
-        attention_prefill_launch<kDT, 4>(q, k, v, out, T, S, q_offset, head_dim, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_launch<kDT, 4>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
     else
-        attention_prefill_launch<kDT, 8>(q, k, v, out, T, S, q_offset, head_dim, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_launch<kDT, 8>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
 }
 
 // ---------------------------------------------------------------- decode
@@ -461,12 +515,12 @@ inline void attention_prefill(const float *q_heads, const float *kcache, const f
     detail::require(q_heads && kcache && vcache && out, "attention_prefill requires non-null pointers");
     const float scale = 1.f / std::sqrt(static_cast<float>(head_dim));
     const int kvh = num_q_heads / kv_rep;
-    if (head_dim <= 32)
-        detail::attention_prefill_dispatch<1>(q_heads, kcache, vcache, out, T, S, q_offset, head_dim, kv_rep, kvh, cap,
-                                              scale, stream);
-    else
-        detail::attention_prefill_dispatch<2>(q_heads, kcache, vcache, out, T, S, q_offset, head_dim, kv_rep, kvh, cap,
-                                              scale, stream);
+    switch (head_dim / 16) {
+    case 1: detail::attention_prefill_dispatch<1>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream); break;
+    case 2: detail::attention_prefill_dispatch<2>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream); break;
+    case 3: detail::attention_prefill_dispatch<3>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream); break;
+    default: detail::attention_prefill_dispatch<4>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream); break;
+    }
 }
 
 // Same contract as the reference's chunked prefill (name kept for drop-in callers).
