@@ -50,13 +50,17 @@ class Timer:
     queued on the same stream. The K steps then wait in the queue while the filler runs, and the
     events measure the GPU's back-to-back execution of the K steps, not the host's launch rate.
 
-    The engine clock of an idle MI355X ramps up over roughly 100 ms of load, so before the W warmup
-    steps the op itself runs back to back, untimed, for PREWARM_S of wall time: the K steps are
-    then timed at the clocks of a busy GPU (the steady state a serving loop sees)."""
+    The engine clock of an idle MI355X ramps up over roughly 100 ms of load, so an op whose step
+    keeps the GPU busy for longer than a host launch takes (>= PREWARM_MIN_MS) first runs back to
+    back, untimed, for PREWARM_S of wall time: its K steps are then timed at the clocks of a busy
+    GPU (the steady state a serving loop sees). Shorter ops are not pre-run: launched from Python
+    they would leave the GPU idle between steps, which is not a steady state of theirs (softmax
+    measured slower after such a run, not faster)."""
 
     _filler = None
     FILL_N = 1 << 27  # floats per filler buffer (512 MiB)
     PREWARM_S = 0.25
+    PREWARM_MIN_MS = 0.05
 
     def __init__(self, stream):
         self.stream = stream
@@ -70,7 +74,13 @@ class Timer:
             ow.ops.copy(src, dst, self.FILL_N, stream=self.stream)
 
     def _prewarm(self, fn) -> None:
-        t0, i = time.perf_counter(), 0
+        self.t0.record(self.stream)
+        fn(0)
+        self.t1.record(self.stream)
+        self.t1.synchronize()
+        if self.t0.elapsed_ms(self.t1) < self.PREWARM_MIN_MS:
+            return
+        t0, i = time.perf_counter(), 1
         while time.perf_counter() - t0 < self.PREWARM_S:
             for _ in range(8):  # bounded queue: at most 8 steps ahead of the host
                 fn(i)
