@@ -64,8 +64,11 @@ int opw_llama_debug_prefill(void *session, const int32_t *tokens, int n, float *
                             char *err, int err_len);
 /* Greedy generation on a fresh session, as examples/llama/generate.py:111-135
  * runs it with no EOS stop: out_tokens[0] is the prefill's token, then
- * max_new - 1 decode steps. Wall times of the prefill and of the decode steps
- * are returned in milliseconds. Returns the number of tokens written, -1 on error. */
+ * max_new - 1 decode steps. The decode steps are chained on the device (each
+ * step's argmax is the next step's input; the host waits once), with the same
+ * tokens as max_new - 1 opw_llama_decode_step calls; the prompt plus max_new - 1
+ * positions must fit the session. Wall times of the prefill and of the decode
+ * steps are returned in milliseconds. Returns the number of tokens written, -1 on error. */
 int opw_llama_generate_greedy(void *session, const int32_t *prompt, int n, int max_new, int32_t *out_tokens,
                               double *prefill_ms, double *decode_ms, char *err, int err_len);
 

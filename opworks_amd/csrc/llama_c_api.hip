@@ -220,10 +220,7 @@ int opw_llama_generate_greedy(void *session, const int32_t *prompt, int n, int m
             int32_t tok = m.prefill(*s->session, ids);
             const auto t1 = clock::now();
             out_tokens[0] = tok;
-            for (int i = 1; i < max_new; ++i) {
-                tok = m.decode_step(*s->session, tok);
-                out_tokens[i] = tok;
-            }
+            m.decode_greedy(*s->session, tok, max_new - 1, out_tokens + 1);
             const auto t2 = clock::now();
             if (prefill_ms)
                 *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();

@@ -119,7 +119,7 @@ struct LlamaSession {
     TypedDeviceBuffer<float> kcache, vcache;
     // decode step
     TypedDeviceBuffer<float> d_hidden, d_q, d_attn, d_act, logits, attn_partial, lm_best_val;
-    TypedDeviceBuffer<int32_t> lm_best_idx, argmax_out, state_buf, ids;
+    TypedDeviceBuffer<int32_t> lm_best_idx, gen, state_buf, ids; // gen[pos]: token chained decode produced at pos
     // prefill
     TypedDeviceBuffer<float> hidden, normed, qkv, q_heads, attn_heads, attn, act;
     TypedDeviceBuffer<float> splitk_ws; // partial tiles of split-K projections
@@ -163,6 +163,7 @@ class LlamaRuntime {
     virtual std::unique_ptr<Session> create_session(int max_seq_len) const = 0;
     virtual int32_t prefill(Session &s, const std::vector<int32_t> &ids) = 0;
     virtual int32_t decode_step(Session &s, int32_t token) = 0;
+    virtual void decode_greedy(Session &s, int32_t token, int n, int32_t *out) = 0;
     virtual std::vector<float> profile_decode_step(Session &s, int32_t token, int32_t *next) = 0;
     virtual float time_decode_stage(Session &s, int stage, int reps) = 0;
     virtual bool is_eos(int32_t token) const = 0;
@@ -229,7 +230,7 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         s->lm_grid = static_cast<int>(detail::blocks_for64(cfg_.vocab_size, llama::kRows * llama::kWavesPerBlock));
         s->lm_best_val = TypedDeviceBuffer<float>(s->lm_grid);
         s->lm_best_idx = TypedDeviceBuffer<int32_t>(s->lm_grid);
-        s->argmax_out = TypedDeviceBuffer<int32_t>(1);
+        s->gen = TypedDeviceBuffer<int32_t>(T);
         s->state_buf = TypedDeviceBuffer<int32_t>(4);
         s->ids = TypedDeviceBuffer<int32_t>(T);
         s->hidden = TypedDeviceBuffer<float>(T * H);
@@ -243,6 +244,7 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
             s->splitk_ws = TypedDeviceBuffer<float>(kBf16 ? detail::kSplitKWorkspaceBf16 : detail::kSplitKWorkspaceF32);
         OPWORKS_HIP_CHECK(hipMemsetAsync(s->state_buf.data(), 0, sizeof(int32_t) * 4, s->stream));
         OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&s->h_state), sizeof(llama::StepState)));
+        *s->h_state = llama::StepState{0, 0, -1, 0};
         OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&s->h_token), sizeof(int32_t)));
         synchronize(s->stream);
         return s;
@@ -273,6 +275,40 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         s.length += 1;
         s.last_prefill_rows = 0;
         return s.h_state->next;
+    }
+
+    // n greedy decode steps from `token` (appended at position length): out[i]
+    // is the token step i produces, the input of step i + 1. The argmax kernel
+    // of each step records its token in gen[pos] and advances the device step
+    // state (chain = 1), so the steps are launched back to back and the host
+    // waits once, instead of once per token as decode_step does. The kernels
+    // and results are those of n decode_step calls.
+    void decode_greedy(Session &s, int32_t token, int n, int32_t *out) override {
+        if (n <= 0)
+            return;
+        if (!out)
+            throw std::invalid_argument("decode_greedy needs an output buffer");
+        if (token < 0 || token >= cfg_.vocab_size)
+            throw std::invalid_argument("token id outside the vocabulary");
+        if (n > s.max_seq_len - s.length)
+            throw std::invalid_argument("session capacity exhausted");
+        struct ChainOff { // every other path runs with chain = 0
+            llama::StepState *h;
+            ~ChainOff() { h->chain = 0; }
+        } chain_off{s.h_state};
+        const int pos0 = s.length;
+        *s.h_state = llama::StepState{token, pos0, -1, 1};
+        OPWORKS_HIP_CHECK(hipMemcpyAsync(s.state(), s.h_state, sizeof(llama::StepState), hipMemcpyHostToDevice,
+                                         s.stream));
+        for (int i = 0; i < n; ++i)
+            launch_decode(s);
+        OPWORKS_HIP_CHECK(hipMemcpyAsync(out, s.gen.data() + pos0, sizeof(int32_t) * static_cast<size_t>(n),
+                                         hipMemcpyDeviceToHost, s.stream));
+        OPWORKS_HIP_CHECK(hipMemcpyAsync(s.h_state, s.state(), sizeof(llama::StepState), hipMemcpyDeviceToHost,
+                                         s.stream));
+        synchronize(s.stream);
+        s.length += n;
+        s.last_prefill_rows = 0;
     }
 
     // One decode step launched eagerly with an event before every kernel and
@@ -662,7 +698,7 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         tick();
         launch_async(s.stream, llama::lm_head_kernel<kV, WT>, s.lm_grid, llama::kBlock, la);
         launch_async(s.stream, llama::argmax_records_kernel, 1, 1024, s.lm_best_val.data(), s.lm_best_idx.data(),
-                     s.lm_grid, s.state(), s.argmax_out.data());
+                     s.lm_grid, s.state(), s.gen.data());
     }
 
     // Calls f(IntTag<H / 256>, IntTag<I / 1024>); bf16 rows need whole 8-weight

@@ -41,7 +41,7 @@ struct StepState {
     int32_t token; // input token id of this step
     int32_t pos;   // its position (= KV length before the step)
     int32_t next;  // argmax result
-    int32_t pad;
+    int32_t chain; // nonzero: the argmax kernel also records `next` in gen[pos] and advances to it
 };
 
 constexpr int kRows = 4;       // rows per LM-head wave; rows per workgroup of the other GEMVs
@@ -463,7 +463,7 @@ __global__ __launch_bounds__(kBlock) void lm_head_kernel(LmHeadArgs<WT> a) {
 // One workgroup of 1024 threads reduces the per-workgroup records.
 __global__ __launch_bounds__(1024) static void argmax_records_kernel(const float *__restrict__ best_val,
                                                                      const int *__restrict__ best_idx, int count,
-                                                                     StepState *state, int *argmax_out) {
+                                                                     StepState *state, int *gen) {
     __shared__ float sv[16];
     __shared__ int si[16];
     const int lane = threadIdx.x % kWaveSize, wave = threadIdx.x / kWaveSize;
@@ -492,8 +492,12 @@ __global__ __launch_bounds__(1024) static void argmax_records_kernel(const float
     if (threadIdx.x == 0) {
         for (int k = 0; k < static_cast<int>(blockDim.x) / kWaveSize; ++k)
             argmax_merge(bv, bi, sv[k], si[k]);
-        argmax_out[0] = bi;
         state->next = bi;
+        if (state->chain) { // greedy chaining: the next launch decodes this token at pos + 1
+            gen[state->pos] = bi;
+            state->token = bi;
+            state->pos += 1;
+        }
     }
 }
 

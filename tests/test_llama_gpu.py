@@ -142,6 +142,29 @@ def test_reset_repeat_is_deterministic(tiny):
     assert outs[0][0] == outs[1][0] and np.array_equal(outs[0][1], outs[1][1])
 
 
+@pytest.mark.parametrize("fixture,n,steps", [("tiny", 1, 30), ("tiny", 9, 2), ("small", 33, 20)])
+def test_generate_greedy_chains_like_decode_steps(request, fixture, n, steps):
+    """opw_llama_generate_greedy chains the steps on the device (the argmax kernel feeds the next step);
+    its tokens, the last logits and the state it leaves (a further decode_step) must be bit-identical to a
+    prefill + decode_step loop on another session."""
+    gpu, _ = request.getfixturevalue(fixture)
+    cfg = {"tiny": TINY, "small": SMALL}[fixture]
+    ids = prompt(n, cfg["vocab_size"], 17 + n)
+    a, b = gpu.session(128), gpu.session(128)
+    toks, _, _ = a.generate_greedy(ids, steps)
+    tok = b.prefill(ids)
+    want = [tok]
+    for _ in range(steps - 1):
+        tok = b.decode_step(tok)
+        want.append(tok)
+    assert [int(t) for t in toks] == want
+    assert np.array_equal(a.last_logits(), b.last_logits())
+    assert a.decode_step(want[-1]) == b.decode_step(want[-1])
+    assert np.array_equal(a.last_logits(), b.last_logits())
+    with pytest.raises(Exception):
+        gpu.session(8).generate_greedy(prompt(4, cfg["vocab_size"], 5), 6)  # 4 + 5 positions > 8
+
+
 def test_stage_timing_leaves_the_sequence_unchanged(tiny, ow):
     """time_decode_stage runs stages out of order against the live session; the
     tokens and logits that follow must equal an untimed run's."""
