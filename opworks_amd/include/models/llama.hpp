@@ -120,6 +120,7 @@ struct LlamaSession {
     // decode step
     TypedDeviceBuffer<float> d_hidden, d_q, d_attn, d_act, logits, attn_partial, lm_best_val;
     TypedDeviceBuffer<int32_t> lm_best_idx, gen, state_buf, ids; // gen[pos]: token chained decode produced at pos
+    TypedDeviceBuffer<int32_t> attn_counters; // [kvh] arrival counters of the fused decode attention, zero at rest
     // prefill
     TypedDeviceBuffer<float> hidden, normed, qkv, q_heads, attn_heads, attn, act;
     TypedDeviceBuffer<float> splitk_ws; // partial tiles of split-K projections
@@ -231,6 +232,7 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         s->lm_best_val = TypedDeviceBuffer<float>(s->lm_grid);
         s->lm_best_idx = TypedDeviceBuffer<int32_t>(s->lm_grid);
         s->gen = TypedDeviceBuffer<int32_t>(T);
+        s->attn_counters = TypedDeviceBuffer<int32_t>(kvh);
         s->state_buf = TypedDeviceBuffer<int32_t>(4);
         s->ids = TypedDeviceBuffer<int32_t>(T);
         s->hidden = TypedDeviceBuffer<float>(T * H);
@@ -243,6 +245,7 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         if (T >= 2) // only a multi-row prefill runs the GEMMs
             s->splitk_ws = TypedDeviceBuffer<float>(kBf16 ? detail::kSplitKWorkspaceBf16 : detail::kSplitKWorkspaceF32);
         OPWORKS_HIP_CHECK(hipMemsetAsync(s->state_buf.data(), 0, sizeof(int32_t) * 4, s->stream));
+        OPWORKS_HIP_CHECK(hipMemsetAsync(s->attn_counters.data(), 0, sizeof(int32_t) * kvh, s->stream));
         OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&s->h_state), sizeof(llama::StepState)));
         *s->h_state = llama::StepState{0, 0, -1, 0};
         OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&s->h_token), sizeof(int32_t)));
@@ -642,6 +645,7 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         aa.vcache = layer_v(s, l);
         aa.out = s.d_attn.data();
         aa.partial = s.attn_partial.data();
+        aa.counters = s.attn_counters.data(); // fused merge: one launch per layer
         aa.len_ptr = s.state_buf.data() + offsetof(llama::StepState, pos) / sizeof(int32_t); // length pos + 1
         aa.len_bias = 1;
         aa.kv_rep = cfg_.kv_rep();

@@ -338,16 +338,86 @@ inline int attention_decode_workspace_floats(int num_q_heads, int max_len, int h
 // records in chunk order: M = max m_c, L = sum l_c e^(m_c - M),
 // out = sum acc_c e^(m_c - M) / L, loading 16 chunk rows per round trip.
 // The length is a host value or, for graph replay, read on the device.
+//
+// Fused form (counters set): the partial kernel also merges. Records are
+// written with agent-coherent stores (relaxed agent-scope atomics, which
+// write through the XCD's L2), each workgroup waits for its stores to
+// complete and then counts itself in on counters[kvh]; the workgroup that
+// arrives last reads its kv head's records with agent-coherent loads, merges
+// them as the combine kernel does, and resets the counter to zero for the next
+// launch. No workgroup waits on another, and no cache-wide writeback or
+// invalidate is needed. The counters must be zero before the first launch.
 struct DecodeAttnArgs {
     const float *q;               // [qh][D]
     const float *kcache, *vcache; // [kvh][cap][D]
     float *out;                   // [qh][D]
     float *partial;               // [qh][max_chunks][D + 2]
     const int *len_ptr;           // if set, length = *len_ptr + len_bias
+    int *counters;                // [kvh], zero between launches; null: separate combine kernel
     int len, len_bias;
     int kv_rep, D, cap, max_chunks;
     float scale;
 };
+
+template <bool kCoherent> __device__ __forceinline__ float record_load(const float *p) {
+    if constexpr (kCoherent)
+        return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        return *p;
+}
+template <bool kCoherent> __device__ __forceinline__ void record_store(float *p, float v) {
+    if constexpr (kCoherent)
+        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *p = v;
+}
+
+// One wave merges q head h's records in chunk order: M = max m_c,
+// L = sum l_c e^(m_c - M), out = sum acc_c e^(m_c - M) / L, 16 chunk rows per
+// round trip.
+template <bool kCoherent>
+__device__ __forceinline__ void decode_combine_head(const DecodeAttnArgs &a, int h, int nchunks, int lane) {
+    const int D = a.D;
+    const float *base = a.partial + int64_t(h) * a.max_chunks * (D + 2);
+    float m0 = kNegInf, l0 = 0.f, m1 = kNegInf, l1 = 0.f;
+    if (lane < nchunks) {
+        m0 = record_load<kCoherent>(base + int64_t(lane) * (D + 2));
+        l0 = record_load<kCoherent>(base + int64_t(lane) * (D + 2) + 1);
+    }
+    if (lane + kWaveSize < nchunks) {
+        m1 = record_load<kCoherent>(base + int64_t(lane + kWaveSize) * (D + 2));
+        l1 = record_load<kCoherent>(base + int64_t(lane + kWaveSize) * (D + 2) + 1);
+    }
+    // The first batch of output rows is loaded together with the (max, sum) pairs, so a
+    // merge of up to kBatch chunks (1024 keys) costs one memory round trip.
+    constexpr int kBatch = 16;
+    float v[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+        v[j] = j < nchunks && lane < D ? record_load<kCoherent>(base + int64_t(j) * (D + 2) + 2 + lane) : 0.f;
+    const float M = wave::max(fmaxf(m0, m1));
+    const float w0 = lane < nchunks ? expf(m0 - M) : 0.f;
+    const float w1 = lane + kWaveSize < nchunks ? expf(m1 - M) : 0.f;
+    const float L = wave::sum(l0 * w0 + l1 * w1);
+    float acc = 0.f;
+    for (int c0 = 0; c0 < nchunks; c0 += kBatch) {
+        if (c0 > 0) {
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j)
+                v[j] = c0 + j < nchunks && lane < D
+                           ? record_load<kCoherent>(base + int64_t(c0 + j) * (D + 2) + 2 + lane)
+                           : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int c = c0 + j;
+            const float wc = wave::readlane(c < kWaveSize ? w0 : w1, c % kWaveSize);
+            acc = c < nchunks ? fmaf(v[j], wc, acc) : acc;
+        }
+    }
+    if (lane < D)
+        a.out[int64_t(h) * D + lane] = L > 0.f ? acc / L : 0.f;
+}
 
 __device__ __forceinline__ int decode_len(const DecodeAttnArgs &a) {
     int len = a.len_ptr ? *a.len_ptr + a.len_bias : a.len;
@@ -431,57 +501,51 @@ __global__ __launch_bounds__(kWaves *kWaveSize) void attention_decode_partial_ke
         }
         if (head_ok) {
             float *rec = a.partial + (int64_t(h) * a.max_chunks + chunk) * (D + 2);
-            if (lane == 0) {
-                rec[0] = m;
-                rec[1] = l;
+            const float o = (o0 + o1) + (o2 + o3);
+            if (a.counters) {
+                if (lane == 0) {
+                    record_store<true>(rec, m);
+                    record_store<true>(rec + 1, l);
+                }
+                record_store<true>(rec + 2 + lane, o);
+            } else {
+                if (lane == 0) {
+                    rec[0] = m;
+                    rec[1] = l;
+                }
+                rec[2 + lane] = o;
             }
-            rec[2 + lane] = (o0 + o1) + (o2 + o3);
         }
     }
+    if (!a.counters)
+        return;
+    // Fused merge: count in once this workgroup's records are complete; the last one merges.
+    __shared__ int last;
+    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): the record stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(a.counters + kvh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               nchunks - 1;
+    __syncthreads();
+    if (!last)
+        return;
+    if (head_ok)
+        decode_combine_head<true>(a, h, nchunks, lane);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(a.counters + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // grid kvh, block kv_rep waves; wave w merges q head kvh * kv_rep + w.
 __global__ __launch_bounds__(kAttnMaxRep *kWaveSize) static void attention_decode_combine_kernel(DecodeAttnArgs a) {
-    constexpr int C = kAttnChunk;
     const int len = decode_len(a);
-    const int nchunks = (len + C - 1) / C; // <= max_chunks <= 2 * kWaveSize
+    const int nchunks = (len + kAttnChunk - 1) / kAttnChunk; // <= max_chunks <= 2 * kWaveSize
     const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
-    const int h = blockIdx.x * a.kv_rep + wave;
-    const int D = a.D;
-    const float *base = a.partial + int64_t(h) * a.max_chunks * (D + 2);
-    float m0 = kNegInf, l0 = 0.f, m1 = kNegInf, l1 = 0.f;
-    if (lane < nchunks) {
-        m0 = base[int64_t(lane) * (D + 2)];
-        l0 = base[int64_t(lane) * (D + 2) + 1];
-    }
-    if (lane + kWaveSize < nchunks) {
-        m1 = base[int64_t(lane + kWaveSize) * (D + 2)];
-        l1 = base[int64_t(lane + kWaveSize) * (D + 2) + 1];
-    }
-    const float M = wave::max(fmaxf(m0, m1));
-    const float w0 = lane < nchunks ? expf(m0 - M) : 0.f;
-    const float w1 = lane + kWaveSize < nchunks ? expf(m1 - M) : 0.f;
-    const float L = wave::sum(l0 * w0 + l1 * w1);
-    constexpr int kBatch = 16;
-    float acc = 0.f;
-    for (int c0 = 0; c0 < nchunks; c0 += kBatch) {
-        float v[kBatch];
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j)
-            v[j] = c0 + j < nchunks && lane < D ? base[int64_t(c0 + j) * (D + 2) + 2 + lane] : 0.f;
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) {
-            const int c = c0 + j;
-            const float wc = wave::readlane(c < kWaveSize ? w0 : w1, c % kWaveSize);
-            acc = c < nchunks ? fmaf(v[j], wc, acc) : acc;
-        }
-    }
-    if (lane < D)
-        a.out[int64_t(h) * D + lane] = L > 0.f ? acc / L : 0.f;
+    decode_combine_head<false>(a, blockIdx.x * a.kv_rep + wave, nchunks, lane);
 }
 
-// Enqueues the partial and combine kernels: grid (kvh, max_chunks) with
-// kv_rep rounded up to a power of two waves per workgroup.
+// Enqueues the partial and combine kernels (or the fused partial kernel alone
+// when a.counters is set): grid (kvh, max_chunks) with kv_rep rounded up to a
+// power of two waves per workgroup.
 inline void attention_decode_launch(const DecodeAttnArgs &a, int kvh, hipStream_t stream) {
     const dim3 grid(kvh, a.max_chunks);
     const int rep = a.kv_rep;
@@ -495,7 +559,8 @@ inline void attention_decode_launch(const DecodeAttnArgs &a, int kvh, hipStream_
         launch_async(stream, attention_decode_partial_kernel<8>, grid, 8 * kWaveSize, a);
     else
         launch_async(stream, attention_decode_partial_kernel<16>, grid, 16 * kWaveSize, a);
-    launch_async(stream, attention_decode_combine_kernel, kvh, rep * kWaveSize, a);
+    if (!a.counters)
+        launch_async(stream, attention_decode_combine_kernel, kvh, rep * kWaveSize, a);
 }
 
 } // namespace opworks::detail
