@@ -57,66 +57,76 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     const int l32 = lane % 32, half = lane / 32;
 
     // Staging: each operand tile is 256 rows x 32 k = 1024 chunks of 8 k; 2 chunks per thread.
-    u32x4 ra[2], rb[2];
+    // The vector path loads unconditionally from clamped addresses into raw registers (fp32 A
+    // is rounded to bf16 only when staged): a load under a branch makes the compiler wait for
+    // every load in flight before the next one. Rows past M or N then hold copies of the last
+    // row, which only feed outputs that are not stored; the K tail is zeroed when staged.
+    constexpr bool kF32A = std::is_same_v<TA, float>;
+    using AStage = std::conditional_t<kF32A, f32x4, u32x4>;
+    constexpr int kAParts = kF32A ? 2 : 1;
+    AStage ra[2][kAParts];
+    u32x4 rb[2];
+    auto chunk_row = [&](int i) { return (tid + kBfThreads * i) / 4; };
+    auto chunk_k = [&](int i) { return ((tid + kBfThreads * i) % 4) * 8; };
     auto load_chunk_bf16 = [&](const uint16_t *src, int row, int rows_total, int k) -> u32x4 {
-        if constexpr (kVec) {
-            return (row < rows_total && k < K) ? *reinterpret_cast<const u32x4 *>(src + int64_t(row) * K + k)
-                                               : u32x4{0u, 0u, 0u, 0u};
-        } else {
-            uint16_t e[8];
+        uint16_t e[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                e[j] = (row < rows_total && k + j < K) ? src[int64_t(row) * K + k + j] : uint16_t(0);
-            return u32x4{e[0] | (uint32_t(e[1]) << 16), e[2] | (uint32_t(e[3]) << 16), e[4] | (uint32_t(e[5]) << 16),
-                         e[6] | (uint32_t(e[7]) << 16)};
-        }
-    };
-    auto load_chunk_f32 = [&](const float *src, int row, int k) -> u32x4 {
-        float e[8];
-        if constexpr (kVec) {
-            if (row < M && k < K) {
-                const f32x4 lo = *reinterpret_cast<const f32x4 *>(src + int64_t(row) * K + k);
-                const f32x4 hi = *reinterpret_cast<const f32x4 *>(src + int64_t(row) * K + k + 4);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    e[j] = lo[j];
-                    e[4 + j] = hi[j];
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    e[j] = 0.f;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                e[j] = (row < M && k + j < K) ? src[int64_t(row) * K + k + j] : 0.f;
-        }
-        return u32x4{pack_bf16x2(e[0], e[1]), pack_bf16x2(e[2], e[3]), pack_bf16x2(e[4], e[5]),
-                     pack_bf16x2(e[6], e[7])};
+        for (int j = 0; j < 8; ++j)
+            e[j] = (row < rows_total && k + j < K) ? src[int64_t(row) * K + k + j] : uint16_t(0);
+        return u32x4{e[0] | (uint32_t(e[1]) << 16), e[2] | (uint32_t(e[3]) << 16), e[4] | (uint32_t(e[5]) << 16),
+                     e[6] | (uint32_t(e[7]) << 16)};
     };
     auto global_load = [&](int kt) {
         const int k0 = kt * kBfBK;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int idx = tid + kBfThreads * i;
-            const int r = idx / 4, c = (idx % 4) * 8;
-            if constexpr (std::is_same_v<TA, float>)
-                ra[i] = load_chunk_f32(A, m0 + r, k0 + c);
-            else
-                ra[i] = load_chunk_bf16(A, m0 + r, M, k0 + c);
-            rb[i] = load_chunk_bf16(W, n0 + r, N, k0 + c);
+            const int r = chunk_row(i), k = k0 + chunk_k(i);
+            if constexpr (kVec) {
+                const int ar = m0 + r < M ? m0 + r : M - 1, br = n0 + r < N ? n0 + r : N - 1;
+                const int kc = k < K ? k : K - 8;
+#pragma unroll
+                for (int p = 0; p < kAParts; ++p)
+                    ra[i][p] = *reinterpret_cast<const AStage *>(A + int64_t(ar) * K + kc + 4 * p);
+                rb[i] = *reinterpret_cast<const u32x4 *>(W + int64_t(br) * K + kc);
+            } else {
+                if constexpr (kF32A) {
+#pragma unroll
+                    for (int p = 0; p < 2; ++p)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const int kk = k + 4 * p + j;
+                            ra[i][p][j] = (m0 + r < M && kk < K) ? A[int64_t(m0 + r) * K + kk] : 0.f;
+                        }
+                } else {
+                    ra[i][0] = load_chunk_bf16(A, m0 + r, M, k);
+                }
+                rb[i] = load_chunk_bf16(W, n0 + r, N, k);
+            }
         }
     };
-    auto lds_store = [&](int buf) {
+    auto lds_store = [&](int buf, int kt, bool zero_tail) {
         uint16_t *As = lds + buf * kStage;
         uint16_t *Bs = As + kBfBM * kBfLd;
+        const int k0 = kt * kBfBK;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int idx = tid + kBfThreads * i;
-            const int off = (idx / 4) * kBfLd + (idx % 4) * 8;
-            *reinterpret_cast<u32x4 *>(As + off) = ra[i];
-            *reinterpret_cast<u32x4 *>(Bs + off) = rb[i];
+            const int k = k0 + chunk_k(i);
+            u32x4 av, bv = rb[i];
+            if constexpr (kF32A)
+                av = u32x4{pack_bf16x2(ra[i][0][0], ra[i][0][1]), pack_bf16x2(ra[i][0][2], ra[i][0][3]),
+                           pack_bf16x2(ra[i][1][0], ra[i][1][1]), pack_bf16x2(ra[i][1][2], ra[i][1][3])};
+            else
+                av = ra[i][0];
+            if (zero_tail) { // the partial last K tile only: k >= K contributes nothing
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    av[j] = k < K ? av[j] : 0u;
+                    bv[j] = k < K ? bv[j] : 0u;
+                }
+            }
+            const int off = chunk_row(i) * kBfLd + chunk_k(i);
+            *reinterpret_cast<u32x4 *>(As + off) = av;
+            *reinterpret_cast<u32x4 *>(Bs + off) = bv;
         }
     };
 
@@ -155,19 +165,30 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     const int per_split = (ktiles_all + gridDim.y - 1) / gridDim.y;
     const int kt_begin = blockIdx.y * per_split;
     const int kt_end = kt_begin + per_split < ktiles_all ? kt_begin + per_split : ktiles_all;
-    if (kt_begin < kt_end) {
+    // The vector path pipelines its full K tiles and runs a partial last tile (K not a multiple
+    // of the K tile) after the loop, with the tail zeroed; the scalar path bounds every element.
+    const int kt_full = kVec ? (K / kBfBK < kt_end ? (K / kBfBK > kt_begin ? K / kBfBK : kt_begin) : kt_end) : kt_end;
+    if (kt_begin < kt_full) {
         global_load(kt_begin);
-        lds_store(0);
+        lds_store(0, kt_begin, false);
         __syncthreads();
-        for (int kt = kt_begin; kt < kt_end; ++kt) {
+        for (int kt = kt_begin; kt < kt_full; ++kt) {
             const int buf = (kt - kt_begin) & 1;
-            if (kt + 1 < kt_end)
-                global_load(kt + 1);
+            // past the last tile: a reload of a valid tile, staged into the idle buffer
+            const int next = kt + 1 < kt_full ? kt + 1 : kt;
+            global_load(next);
+            __builtin_amdgcn_sched_barrier(0); // the loads stay at the top, in flight during the MFMAs
             compute(buf);
-            if (kt + 1 < kt_end)
-                lds_store(buf ^ 1);
+            __builtin_amdgcn_sched_barrier(0); // the staging, which waits for them, stays at the end
+            lds_store(buf ^ 1, next, false);   // that buffer was last read before the previous barrier
             __syncthreads();
         }
+    }
+    if (kt_full < kt_end) { // the partial last K tile (vector path)
+        global_load(kt_full);
+        lds_store(0, kt_full, true);
+        __syncthreads();
+        compute(0);
     }
     if constexpr (kStore == GemmStore::partial)
         C += int64_t(blockIdx.y) * M * N;
