@@ -130,12 +130,15 @@ struct LlamaSession {
     int32_t *h_token = nullptr;          // pinned
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+    std::vector<hipEvent_t> step_events; // chained decode: completion of the steps in flight
     int last_prefill_rows = 0;
 
     LlamaSession() = default;
     LlamaSession(const LlamaSession &) = delete;
     LlamaSession &operator=(const LlamaSession &) = delete;
     ~LlamaSession() {
+        for (hipEvent_t e : step_events)
+            (void)hipEventDestroy(e);
         if (graph_exec)
             (void)hipGraphExecDestroy(graph_exec);
         if (graph)
@@ -303,8 +306,23 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         *s.h_state = llama::StepState{token, pos0, -1, 1};
         OPWORKS_HIP_CHECK(hipMemcpyAsync(s.state(), s.h_state, sizeof(llama::StepState), hipMemcpyHostToDevice,
                                          s.stream));
-        for (int i = 0; i < n; ++i)
+        // At most 16 steps are queued ahead of the GPU: enough that it never waits for the host,
+        // few enough that eager mode (82 kernels per step) keeps a short queue. An event closes
+        // every group of 4 steps; a group starts once the group 4 before it has completed.
+        constexpr int kGroup = 4, kGroups = 4;
+        while (static_cast<int>(s.step_events.size()) < kGroups) {
+            hipEvent_t e;
+            OPWORKS_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+            s.step_events.push_back(e);
+        }
+        for (int i = 0; i < n; ++i) {
+            const int g = i / kGroup;
+            if (i % kGroup == 0 && g >= kGroups)
+                OPWORKS_HIP_CHECK(hipEventSynchronize(s.step_events[g % kGroups]));
             launch_decode(s);
+            if (i % kGroup == kGroup - 1)
+                OPWORKS_HIP_CHECK(hipEventRecord(s.step_events[g % kGroups], s.stream));
+        }
         OPWORKS_HIP_CHECK(hipMemcpyAsync(out, s.gen.data() + pos0, sizeof(int32_t) * static_cast<size_t>(n),
                                          hipMemcpyDeviceToHost, s.stream));
         OPWORKS_HIP_CHECK(hipMemcpyAsync(s.h_state, s.state(), sizeof(llama::StepState), hipMemcpyDeviceToHost,
