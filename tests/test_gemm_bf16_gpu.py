@@ -30,7 +30,8 @@ def test_convert_bits_match_oracle(ow, orc):
     assert np.array_equal(db.to_host(), orc.round_bf16(x)[1])
 
 
-SHAPES = [(1, 8, 1), (16, 64, 64), (100, 200, 300), (256, 256, 256), (300, 2048, 520), (512, 1024, 3072)]
+SHAPES = [(1, 8, 1), (16, 64, 64), (100, 200, 300), (256, 256, 256), (300, 2048, 520), (512, 1024, 3072),
+          (257, 40, 513), (3, 4104, 7)]  # a full K tile + an 8-wide tail; tiles one row/column past 256
 
 
 @pytest.mark.parametrize("rows,in_f,out_f", SHAPES)
