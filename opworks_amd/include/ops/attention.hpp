@@ -64,12 +64,15 @@ template <typename Combine> __device__ __forceinline__ float column_combine(floa
 }
 
 // kDT = head_dim / 16 (16-wide head-dim tiles); kWaves = q heads handled by
-// one workgroup (a GQA group, or an 8-head slice of a larger one).
-template <int kDT, int kWaves> struct PrefillShape {
+// one workgroup (a GQA group, or an 8-head slice of a larger one); kTiles =
+// adjacent query tiles per workgroup, one wave per (tile, head): with 2 every
+// staged K/V tile feeds twice as many MFMA chains (used when the grid still
+// fills every CU's four workgroup slots).
+template <int kDT, int kWaves, int kTiles> struct PrefillShape {
     static constexpr int kD = 16 * kDT;                        // head_dim
     static constexpr int kLd = kD + 4;                         // LDS row stride of K and V (floats)
     static constexpr int kLdsFloats = 4 * kAttnKTile * kLd;    // K and V, double buffered
-    static constexpr int kThreads = kWaves * kWaveSize;
+    static constexpr int kThreads = kTiles * kWaves * kWaveSize;
     static constexpr int kChunks = kAttnKTile * kD / 4;        // 16-byte chunks per K (or V) tile
     static constexpr int kPerThread = (kChunks + kThreads - 1) / kThreads;
     static constexpr int kQ = kD / 4;                          // Q values per lane = QK^T MFMA steps per block
@@ -90,27 +93,31 @@ __device__ __forceinline__ int prefill_tile_of_rank(int rank, int ntq, int pass_
 // amdgpu_waves_per_eu: with four or more waves per workgroup the register budget is 128
 // (four resident waves per SIMD, as many as the LDS allows); the bound also makes the
 // compiler keep the MFMA accumulators in VGPRs rather than AGPRs.
-template <int kDT, int kWaves>
-__global__ __launch_bounds__(kWaves *kWaveSize)
+template <int kDT, int kWaves, int kTiles>
+__global__ __launch_bounds__(kTiles *kWaves *kWaveSize)
 __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) void attention_prefill_kernel(
     const float *__restrict__ q_heads, const float *__restrict__ kcache, const float *__restrict__ vcache,
     float *__restrict__ out, int T, int S, int q_offset, int kv_rep, int num_kv_heads, int cap, float qscale,
     int pass_width) {
-    using Shape = PrefillShape<kDT, kWaves>;
+    using Shape = PrefillShape<kDT, kWaves, kTiles>;
     constexpr int D = Shape::kD, kLd = Shape::kLd, kQ = Shape::kQ;
     extern __shared__ __attribute__((aligned(16))) float lds[];
 
     const int slices = (kv_rep + kWaves - 1) / kWaves; // workgroups per GQA group
     const int per_tile = num_kv_heads * slices;
     const int ntq = (T + kAttnQTile - 1) / kAttnQTile;
-    const int qt = prefill_tile_of_rank(static_cast<int>(blockIdx.x) / per_tile, ntq, pass_width);
+    const int ngroups = (ntq + kTiles - 1) / kTiles; // query-tile groups
+    const int grp = prefill_tile_of_rank(static_cast<int>(blockIdx.x) / per_tile, ngroups, pass_width);
     const int kvh = (static_cast<int>(blockIdx.x) % per_tile) / slices;
     const int slice = static_cast<int>(blockIdx.x) % slices;
     const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
     const int l16 = lane % 16, g = lane / 16;
-    const int rep = slice * kWaves + wave;  // head within the group
-    const bool head_ok = rep < kv_rep;      // idle waves still stage K/V and join barriers
+    const int rep = slice * kWaves + wave % kWaves; // head within the group
+    const bool head_ok = rep < kv_rep;              // idle waves still stage K/V and join barriers
     const int h = kvh * kv_rep + (head_ok ? rep : 0);
+    const int qt_raw = grp * kTiles + wave / kWaves; // this wave's query tile
+    const bool tile_ok = qt_raw < ntq;
+    const int qt = tile_ok ? qt_raw : ntq - 1;
     const int q0 = qt * kAttnQTile;
     const int q = q0 + l16;                 // this lane's query row (column of every MFMA tile)
     const int qpos = q_offset + q;          // its absolute position
@@ -133,8 +140,12 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
         }
     }
 
+    // KV tiles: this wave's own, and the workgroup's (those of its last query tile).
     const int kv_end = (q_offset + q0 + kAttnQTile) < S ? (q_offset + q0 + kAttnQTile) : S;
-    const int ntiles = (kv_end + kAttnKTile - 1) / kAttnKTile;
+    const int my_ntiles = tile_ok ? (kv_end + kAttnKTile - 1) / kAttnKTile : 0;
+    const int q0_last = (grp * kTiles + kTiles - 1 < ntq ? grp * kTiles + kTiles - 1 : ntq - 1) * kAttnQTile;
+    const int kv_end_last = (q_offset + q0_last + kAttnQTile) < S ? (q_offset + q0_last + kAttnQTile) : S;
+    const int ntiles = (kv_end_last + kAttnKTile - 1) / kAttnKTile;
 
     // K/V tile staging through registers: chunk c = tid + i * threads is row c / (D/4).
     // Loads are unconditional (rows past S read row S-1 and are zeroed when staged, chunks
@@ -194,80 +205,82 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
         const float *Ks = lds + buf * kStage;
         const float *Vs = Ks + kAttnKTile * kLd;
 
-        // Operands first: the K fragments of both 16-key blocks and the V^T operands of the
-        // P V chain, so one LDS latency covers the tile.
-        f32x4 kf[2][kQ / 4];
+        if (kt < my_ntiles) { // wave-uniform: the group's shorter tile skips its last K/V tile
+            // Operands first: the K fragments of both 16-key blocks and the V^T operands of the
+            // P V chain, so one LDS latency covers the tile.
+            f32x4 kf[2][kQ / 4];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int c = 0; c < kQ / 4; ++c)
+                    kf[u][c] = *reinterpret_cast<const f32x4 *>(Ks + (16 * u + l16) * kLd + kQ * g + 4 * c);
+            float vf[2][4][kDT];
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int t = 0; t < kDT; ++t)
+                        vf[u][s][t] = Vs[(16 * u + 4 * g + s) * kLd + 16 * t + l16];
+
+            // S^T[key][q] = sum_d K[key][d] Q[q][d] for the two 16-key blocks u; at step s lane
+            // group g supplies reduction index kQ*g + s to both operands, and sacc[u][r] is key
+            // 16u + 4g + r. The blocks' chains alternate so consecutive MFMAs are independent.
+            f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
             for (int c = 0; c < kQ / 4; ++c)
-                kf[u][c] = *reinterpret_cast<const f32x4 *>(Ks + (16 * u + l16) * kLd + kQ * g + 4 * c);
-        float vf[2][4][kDT];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+                for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int t = 0; t < kDT; ++t)
-                    vf[u][s][t] = Vs[(16 * u + 4 * g + s) * kLd + 16 * t + l16];
+                    for (int u = 0; u < 2; ++u)
+                        sacc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[u][c][j], qreg[4 * c + j], sacc[u], 0, 0, 0);
 
-        // S^T[key][q] = sum_d K[key][d] Q[q][d] for the two 16-key blocks u; at step s lane
-        // group g supplies reduction index kQ*g + s to both operands, and sacc[u][r] is key
-        // 16u + 4g + r. The blocks' chains alternate so consecutive MFMAs are independent.
-        f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-        for (int c = 0; c < kQ / 4; ++c)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
+            // Causal mask, only on tiles that reach past the tile's first query position (a
+            // wave-uniform branch: the mask's VALU work sits on the wave's critical path).
+            if (kt * kAttnKTile + kAttnKTile - 1 > q_offset + q0) {
+                const int key0 = kt * kAttnKTile + 4 * g;
 #pragma unroll
                 for (int u = 0; u < 2; ++u)
-                    sacc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[u][c][j], qreg[4 * c + j], sacc[u], 0, 0, 0);
-
-        // Causal mask, only on tiles that reach past the tile's first query position (a
-        // wave-uniform branch: the mask's VALU work sits on the wave's critical path).
-        if (kt * kAttnKTile + kAttnKTile - 1 > q_offset + q0) {
-            const int key0 = kt * kAttnKTile + 4 * g;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        sacc[u][r] = key0 + 16 * u + r > lim ? kNegInf : sacc[u][r];
+            }
+            // Online softmax in base 2. Key 0 is in every row's first tile, so m_new is finite.
+            float tmax = kNegInf;
 #pragma unroll
             for (int u = 0; u < 2; ++u)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    sacc[u][r] = key0 + 16 * u + r > lim ? kNegInf : sacc[u][r];
+                    tmax = fmaxf(tmax, sacc[u][r]);
+            tmax = column_combine(tmax, wave::Max{});
+            const float m_new = fmaxf(m_run, tmax);
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new); // 0 on the first tile
+            float psum = 0.f;
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float p = __builtin_amdgcn_exp2f(sacc[u][r] - m_new);
+                    sacc[u][r] = p;
+                    psum += p;
+                }
+            l_part = l_part * corr + psum;
+            m_run = m_new;
+#pragma unroll
+            for (int t = 0; t < kDT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    oacc[t][r] *= corr;
+            // O^T[d][q] += sum_key V[key][d] P^T[key][q]: at step s of block u lane group g
+            // supplies key 16u + 4g + s, which is its own S^T register sacc[u][s].
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int t = 0; t < kDT; ++t)
+                        oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[u][s][t], sacc[u][s], oacc[t], 0, 0, 0);
         }
-        // Online softmax in base 2. Key 0 is in every row's first tile, so m_new is finite.
-        float tmax = kNegInf;
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                tmax = fmaxf(tmax, sacc[u][r]);
-        tmax = column_combine(tmax, wave::Max{});
-        const float m_new = fmaxf(m_run, tmax);
-        const float corr = __builtin_amdgcn_exp2f(m_run - m_new); // 0 on the first tile
-        float psum = 0.f;
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float p = __builtin_amdgcn_exp2f(sacc[u][r] - m_new);
-                sacc[u][r] = p;
-                psum += p;
-            }
-        l_part = l_part * corr + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int t = 0; t < kDT; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                oacc[t][r] *= corr;
-        // O^T[d][q] += sum_key V[key][d] P^T[key][q]: at step s of block u lane group g
-        // supplies key 16u + 4g + s, which is its own S^T register sacc[u][s].
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int t = 0; t < kDT; ++t)
-                    oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[u][s][t], sacc[u][s], oacc[t], 0, 0, 0);
         // Stage the next tile into the other buffer (last read before the previous barrier);
         // the fence keeps the staging, which waits for the loads, at the end.
         __builtin_amdgcn_sched_barrier(0);
@@ -278,7 +291,7 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
     // oacc[t][r] = O^T[16t + 4g + r][q]: four consecutive head-dim values of row q.
     const float l = column_combine(l_part, wave::Add{});
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    if (head_ok && q < T) {
+    if (head_ok && tile_ok && q < T) {
         float *orow = out + (int64_t(h) * T + q) * D;
 #pragma unroll
         for (int t = 0; t < kDT; ++t) {
@@ -291,31 +304,44 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
     }
 }
 
-template <int kDT, int kWaves>
+template <int kDT, int kWaves, int kTiles>
 inline void attention_prefill_launch(const float *q, const float *k, const float *v, float *out, int T, int S,
                                      int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream) {
-    using Shape = PrefillShape<kDT, kWaves>;
+    using Shape = PrefillShape<kDT, kWaves, kTiles>;
     const int slices = (kv_rep + kWaves - 1) / kWaves;
     const int per_tile = kvh * slices;
-    const int64_t ntq = blocks_for64(T, kAttnQTile);
-    require(ntq * per_tile <= INT32_MAX, "attention_prefill: grid too large");
+    const int64_t ngroups = blocks_for64(blocks_for64(T, kAttnQTile), kTiles);
+    require(ngroups * per_tile <= INT32_MAX, "attention_prefill: grid too large");
     const int pass_width = cu_count() / per_tile > 0 ? cu_count() / per_tile : 1;
-    launch_async_lds(stream, sizeof(float) * Shape::kLdsFloats, attention_prefill_kernel<kDT, kWaves>,
-                     static_cast<int>(ntq * per_tile), Shape::kThreads, q, k, v, out, T, S, q_offset, kv_rep, kvh,
+    launch_async_lds(stream, sizeof(float) * Shape::kLdsFloats, attention_prefill_kernel<kDT, kWaves, kTiles>,
+                     static_cast<int>(ngroups * per_tile), Shape::kThreads, q, k, v, out, T, S, q_offset, kv_rep, kvh,
                      cap, scale * kLog2e, pass_width);
+}
+
+// Two query tiles per workgroup when the one-tile grid would fill every CU's four
+// workgroup slots (measured on near-uniform work: 76 -> 79.5% of the MFMA peak); one
+// otherwise, so short prompts still spread over all CUs.
+template <int kDT, int kWaves>
+inline void attention_prefill_tiles(const float *q, const float *k, const float *v, float *out, int T, int S,
+                                    int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream) {
+    const int64_t wgs = blocks_for64(T, kAttnQTile) * kvh * ((kv_rep + kWaves - 1) / kWaves);
+    if (wgs >= 4 * int64_t(cu_count()))
+        attention_prefill_launch<kDT, kWaves, 2>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
+    else
+        attention_prefill_launch<kDT, kWaves, 1>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
 }
 
 template <int kDT>
 inline void attention_prefill_dispatch(const float *q, const float *k, const float *v, float *out, int T, int S,
                                        int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream) {
     if (kv_rep == 1)
-        attention_prefill_launch<kDT, 1>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_tiles<kDT, 1>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
     else if (kv_rep == 2)
-        attention_prefill_launch<kDT, 2>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_tiles<kDT, 2>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
     else if (kv_rep <= 4)
-        attention_prefill_launch<kDT, 4>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_tiles<kDT, 4>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
     else
-        attention_prefill_launch<kDT, 8>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_tiles<kDT, 8>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
 }
 
 // ---------------------------------------------------------------- decode
