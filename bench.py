@@ -236,7 +236,7 @@ def wl_attention(stream, steps, warmup):
     flop = 4.0 * qh * D * (T * (T + 1) / 2)
     tf = flop / ms / 1e9
     return {"workload": "attention_prefill_causal_gqa_32q8kv_d64_t2048", "unit": "TFLOP/s", "value": tf, "ms": ms,
-            "flop": flop, "kernel": "attention_prefill_kernel<4,4>",
+            "flop": flop, "kernel": "attention_prefill_kernel<4,4,2>",
             "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma")}
 
 
