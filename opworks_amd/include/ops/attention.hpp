@@ -385,6 +385,11 @@ struct DecodeAttnArgs {
     float scale;
 };
 
+// s_waitcnt operand of gfx9 for vmcnt(0) with expcnt and lgkmcnt left at their maxima
+// (vmcnt bits [3:0] and [15:14] = 0, expcnt [6:4] = 7, lgkmcnt [11:8] = 15): waits until
+// every vector memory access of the wave, stores included, has completed.
+constexpr int kWaitVmcnt0 = 0x0F70;
+
 template <bool kCoherent> __device__ __forceinline__ float record_load(const float *p) {
     if constexpr (kCoherent)
         return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -547,7 +552,7 @@ __global__ __launch_bounds__(kWaves *kWaveSize) void attention_decode_partial_ke
         return;
     // Fused merge: count in once this workgroup's records are complete; the last one merges.
     __shared__ int last;
-    __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): the record stores have completed
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); // the record stores have completed
     __syncthreads();
     if (threadIdx.x == 0)
         last = __hip_atomic_fetch_add(a.counters + kvh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
