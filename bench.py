@@ -42,7 +42,8 @@ def cpu_threads() -> int:
 
 
 class Timer:
-    """K launches between two events on `stream`, synchronized on both sides.
+    """K launches (more for short ops: at least MIN_TIMED_MS of them, at most MAX_LAUNCHES) between two
+    events on `stream`, synchronized on both sides; returns the average per launch.
 
     A launch from Python (ctypes + the HIP runtime) takes several microseconds of host time, longer
     than a softmax step runs on the GPU. So before the first event an untimed filler (a copy over
@@ -61,6 +62,8 @@ class Timer:
     FILL_N = 1 << 27  # floats per filler buffer (512 MiB)
     PREWARM_S = 0.25
     PREWARM_MIN_MS = 0.05
+    MIN_TIMED_MS = 2.0
+    MAX_LAUNCHES = 1024
 
     def __init__(self, stream):
         self.stream = stream
@@ -73,34 +76,40 @@ class Timer:
         for _ in range(1 + steps // 4):  # ~0.17 ms of GPU time per 4 steps of host enqueue
             ow.ops.copy(src, dst, self.FILL_N, stream=self.stream)
 
-    def _prewarm(self, fn) -> None:
-        fn(0)  # the first launch also loads the code object; the decision uses the second
+    def _prewarm(self, fn) -> float:
+        """Returns one launch's duration in ms (the second launch: the first also loads the code object)."""
+        fn(0)
         self.t0.record(self.stream)
         fn(1)
         self.t1.record(self.stream)
         self.t1.synchronize()
-        if self.t0.elapsed_ms(self.t1) < self.PREWARM_MIN_MS:
-            return
+        est = self.t0.elapsed_ms(self.t1)
+        if est < self.PREWARM_MIN_MS:
+            return est
         t0, i = time.perf_counter(), 2
         while time.perf_counter() - t0 < self.PREWARM_S:
             for _ in range(8):  # bounded queue: at most 8 steps ahead of the host
                 fn(i)
                 i += 1
             ow.check(ow.lib().opw_device_synchronize())
+        return est
 
     def run(self, fn, steps: int, warmup: int) -> float:
-        self._prewarm(fn)
+        est = self._prewarm(fn)
+        # Short ops are timed over at least MIN_TIMED_MS of back-to-back launches (K if that is more):
+        # a 20-launch window of a 6 us kernel varied by 15% between runs.
+        timed = max(steps, min(self.MAX_LAUNCHES, int(self.MIN_TIMED_MS / max(est, 1e-3)) + 1))
         for i in range(warmup):
             fn(i)
         ow.check(ow.lib().opw_device_synchronize())
-        self._fill(steps)
+        self._fill(timed)
         self.t0.record(self.stream)
-        for i in range(steps):
+        for i in range(timed):
             fn(i)
         self.t1.record(self.stream)
         self.t1.synchronize()
         ow.check(ow.lib().opw_device_synchronize())
-        return self.t0.elapsed_ms(self.t1) / steps
+        return self.t0.elapsed_ms(self.t1) / timed
 
 
 def roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) -> dict:
