@@ -69,16 +69,18 @@ def test_prefill_long_lcg_case(ow, orc):
     run_prefill(ow, orc, L, L, qh, qh // kvh, D, L, rows=rows, data=(q, k, v))
 
 
-@pytest.mark.parametrize("qh,kv_rep,D,T", [(8, 1, 64, 2048), (16, 2, 64, 2048), (32, 4, 32, 2048),
-                                           (32, 4, 48, 2048), (64, 8, 64, 2048), (32, 16, 64, 4096),
-                                           (32, 4, 64, 2064)])
-def test_prefill_two_tile_workgroups(ow, orc, qh, kv_rep, D, T):
+@pytest.mark.parametrize("qh,kv_rep,D,T,S", [(8, 1, 64, 2048, 2048), (16, 2, 64, 2048, 2048),
+                                             (32, 4, 32, 2048, 2048), (32, 4, 48, 2048, 2048),
+                                             (64, 8, 64, 2048, 2048), (32, 16, 64, 4096, 4096),
+                                             (32, 4, 64, 2064, 2064), (32, 4, 64, 2048, 3000)])
+def test_prefill_two_tile_workgroups(ow, orc, qh, kv_rep, D, T, S):
     """Grids of >= 4 workgroups per CU (on 256 CUs) take the two-query-tile workgroups, for every
     wave count (1, 2, 4 and 8 heads per workgroup, 8-head slices of a 16-head group) and head
-    size; T = 2064 leaves the last group's second tile idle. Sampled rows of every head."""
+    size; T = 2064 leaves the last group's second tile idle; S > T is a chunk of a longer prompt
+    (queries at S - T ..). Sampled rows of every head."""
     rows = np.unique(np.concatenate([np.arange(0, 24), np.arange(T - 24, T),
                                      np.linspace(24, T - 25, 16).astype(np.int64)])).astype(np.int32)
-    run_prefill(ow, orc, T, T, qh, kv_rep, D, T, rows=rows)
+    run_prefill(ow, orc, T, S, qh, kv_rep, D, S, rows=rows)
 
 
 @pytest.mark.slow
