@@ -137,27 +137,39 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
         for (int j = 0; j < 2; ++j)
             acc[i][j] = f32x16{};
 
+    // Both MFMA steps' fragments are read up front; the schedule below issues the first step's
+    // six reads, then one second-step read per first-step MFMA, so the second step's operands
+    // arrive while the first step's MFMAs run.
     auto compute = [&](int buf) {
         const uint16_t *As = lds + buf * kStage;
         const uint16_t *Bs = As + kBfBM * kBfLd;
+        bf16x8 a[kBfBK / 16][4], b[kBfBK / 16][2];
 #pragma unroll
         for (int s = 0; s < kBfBK / 16; ++s) {
             const int kk = 16 * s + 8 * half;
-            bf16x8 a[4], b[2];
 #pragma unroll
             for (int bm = 0; bm < 4; ++bm)
-                a[bm] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                                        As + (wm * 128 + bm * 32 + l32) * kBfLd + kk));
+                a[s][bm] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
+                                                           As + (wm * 128 + bm * 32 + l32) * kBfLd + kk));
 #pragma unroll
             for (int bn = 0; bn < 2; ++bn)
-                b[bn] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                                        Bs + (wn * 64 + bn * 32 + l32) * kBfLd + kk));
+                b[s][bn] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
+                                                           Bs + (wn * 64 + bn * 32 + l32) * kBfLd + kk));
+        }
+#pragma unroll
+        for (int s = 0; s < kBfBK / 16; ++s)
 #pragma unroll
             for (int bm = 0; bm < 4; ++bm)
 #pragma unroll
                 for (int bn = 0; bn < 2; ++bn)
-                    acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[bm], b[bn], acc[bm][bn], 0, 0, 0);
+                    acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s][bm], b[s][bn], acc[bm][bn], 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0); // step 0's reads
+#pragma unroll
+        for (int j = 0; j < 6; ++j) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // one step-1 read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // one step-0 MFMA
         }
+        __builtin_amdgcn_sched_group_barrier(0x008, 10, 0);
     };
 
     // K tiles of this workgroup: all of them, or split blockIdx.y's contiguous share
