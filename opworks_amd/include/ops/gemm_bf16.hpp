@@ -7,16 +7,18 @@
 // or already bf16.
 //
 // Kernel shape (gfx950):
-//  * workgroup tile 256 x 256, K tile 32, 512 threads = 8 waves in 2 x 4; each
-//    wave owns 128 x 64 = 4 x 2 v_mfma_f32_32x32x16_bf16 tiles (128
-//    accumulator registers);
+//  * workgroup tile 256 x 256, 512 threads = 8 waves in 2 x 4; each wave owns
+//    128 x 64 = 4 x 2 v_mfma_f32_32x32x16_bf16 tiles (128 accumulator
+//    registers);
+//  * K tile 64 for bf16 A (147 KB of LDS, one workgroup per CU), 32 for fp32
+//    A, whose raw staging registers are twice as wide;
 //  * an MFMA operand is 8 consecutive k of one row per lane, so both operands
-//    keep their k-contiguous global layout in LDS; rows are padded from 64 to
-//    80 bytes, which puts the 16-byte reads of 16 consecutive rows on disjoint
-//    bank groups;
+//    keep their k-contiguous global layout in LDS; rows are padded by 16 bytes,
+//    which puts the 16-byte reads of consecutive rows on disjoint bank groups;
 //  * LDS double buffered, next tile's global loads issued before the current
-//    tile's MFMAs, one barrier per K tile; same XCD-banded tile order as the
-//    fp32 kernel.
+//    tile's MFMAs, one barrier per K tile; inside a tile the next MFMA step's
+//    fragments are read while the current step's MFMAs run; same XCD-banded
+//    tile order as the fp32 kernel.
 
 #include <cstdint>
 
@@ -30,9 +32,9 @@ namespace opworks::detail {
 using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
 using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 
-constexpr int kBfBM = 256, kBfBN = 256, kBfBK = 32;
+constexpr int kBfBM = 256, kBfBN = 256;
+constexpr int kBfBK = 32; // K granularity of split-K planning (the smaller of the two K tiles)
 constexpr int kBfThreads = 512;
-constexpr int kBfLd = kBfBK + 8; // bf16 elements per padded LDS row (80 bytes)
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return static_cast<uint32_t>(float_to_bf16_rne(lo)) | (static_cast<uint32_t>(float_to_bf16_rne(hi)) << 16);
@@ -45,7 +47,13 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
                                                                     float *__restrict__ C, int M, int N, int K,
                                                                     Epi epi) {
     static_assert(std::is_same_v<TA, float> || std::is_same_v<TA, uint16_t>, "A is fp32 or bf16 bits");
-    constexpr int kStage = (kBfBM + kBfBN) * kBfLd; // uint16 elements per stage
+    constexpr bool kF32A = std::is_same_v<TA, float>;
+    // K tile 64 for bf16 A; 32 for fp32 A, whose raw staging registers are twice as wide.
+    constexpr int BK = kF32A ? 32 : 64;
+    constexpr int kLd = BK + 8;                        // bf16 elements per padded LDS row
+    constexpr int kCPR = BK / 8;                       // 16-byte chunks (8 k) per tile row
+    constexpr int kPer = kBfBM * kCPR / kBfThreads;    // chunks per thread per operand
+    constexpr int kStage = (kBfBM + kBfBN) * kLd;      // uint16 elements per stage
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kStage];
 
     const int tiles_m = (M + kBfBM - 1) / kBfBM, tiles_n = (N + kBfBN - 1) / kBfBN;
@@ -56,18 +64,17 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     const int wm = wave / 4, wn = wave % 4; // 2 x 4 waves
     const int l32 = lane % 32, half = lane / 32;
 
-    // Staging: each operand tile is 256 rows x 32 k = 1024 chunks of 8 k; 2 chunks per thread.
+    // Staging: each operand tile is 256 rows x BK k in chunks of 8 k, kPer chunks per thread.
     // The vector path loads unconditionally from clamped addresses into raw registers (fp32 A
     // is rounded to bf16 only when staged): a load under a branch makes the compiler wait for
     // every load in flight before the next one. Rows past M or N then hold copies of the last
     // row, which only feed outputs that are not stored; the K tail is zeroed when staged.
-    constexpr bool kF32A = std::is_same_v<TA, float>;
     using AStage = std::conditional_t<kF32A, f32x4, u32x4>;
     constexpr int kAParts = kF32A ? 2 : 1;
-    AStage ra[2][kAParts];
-    u32x4 rb[2];
-    auto chunk_row = [&](int i) { return (tid + kBfThreads * i) / 4; };
-    auto chunk_k = [&](int i) { return ((tid + kBfThreads * i) % 4) * 8; };
+    AStage ra[kPer][kAParts];
+    u32x4 rb[kPer];
+    auto chunk_row = [&](int i) { return (tid + kBfThreads * i) / kCPR; };
+    auto chunk_k = [&](int i) { return ((tid + kBfThreads * i) % kCPR) * 8; };
     auto load_chunk_bf16 = [&](const uint16_t *src, int row, int rows_total, int k) -> u32x4 {
         uint16_t e[8];
 #pragma unroll
@@ -77,9 +84,9 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
                      e[6] | (uint32_t(e[7]) << 16)};
     };
     auto global_load = [&](int kt) {
-        const int k0 = kt * kBfBK;
+        const int k0 = kt * BK;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kPer; ++i) {
             const int r = chunk_row(i), k = k0 + chunk_k(i);
             if constexpr (kVec) {
                 const int ar = m0 + r < M ? m0 + r : M - 1, br = n0 + r < N ? n0 + r : N - 1;
@@ -106,10 +113,10 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     };
     auto lds_store = [&](int buf, int kt, bool zero_tail) {
         uint16_t *As = lds + buf * kStage;
-        uint16_t *Bs = As + kBfBM * kBfLd;
-        const int k0 = kt * kBfBK;
+        uint16_t *Bs = As + kBfBM * kLd;
+        const int k0 = kt * BK;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kPer; ++i) {
             const int k = k0 + chunk_k(i);
             u32x4 av, bv = rb[i];
             if constexpr (kF32A)
@@ -124,7 +131,7 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
                     bv[j] = k < K ? bv[j] : 0u;
                 }
             }
-            const int off = chunk_row(i) * kBfLd + chunk_k(i);
+            const int off = chunk_row(i) * kLd + chunk_k(i);
             *reinterpret_cast<u32x4 *>(As + off) = av;
             *reinterpret_cast<u32x4 *>(Bs + off) = bv;
         }
@@ -137,49 +144,61 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
         for (int j = 0; j < 2; ++j)
             acc[i][j] = f32x16{};
 
-    // Both MFMA steps' fragments are read up front; the schedule below issues the first step's
-    // six reads, then one second-step read per first-step MFMA, so the second step's operands
-    // arrive while the first step's MFMAs run.
+    // One K tile: BK / 16 MFMA steps. The fragments are double buffered across steps: the next
+    // step's six reads are interleaved one per MFMA with the current step's first six MFMAs,
+    // so they arrive while the matrix core runs.
     auto compute = [&](int buf) {
         const uint16_t *As = lds + buf * kStage;
-        const uint16_t *Bs = As + kBfBM * kBfLd;
-        bf16x8 a[kBfBK / 16][4], b[kBfBK / 16][2];
-#pragma unroll
-        for (int s = 0; s < kBfBK / 16; ++s) {
+        const uint16_t *Bs = As + kBfBM * kLd;
+        constexpr int kSteps = BK / 16;
+        bf16x8 a[2][4], b[2][2];
+        auto read = [&](int s, bf16x8 (&fa)[4], bf16x8 (&fb)[2]) {
             const int kk = 16 * s + 8 * half;
 #pragma unroll
             for (int bm = 0; bm < 4; ++bm)
-                a[s][bm] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                                           As + (wm * 128 + bm * 32 + l32) * kBfLd + kk));
+                fa[bm] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
+                                                        As + (wm * 128 + bm * 32 + l32) * kLd + kk));
 #pragma unroll
             for (int bn = 0; bn < 2; ++bn)
-                b[s][bn] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                                           Bs + (wn * 64 + bn * 32 + l32) * kBfLd + kk));
-        }
+                fb[bn] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
+                                                        Bs + (wn * 64 + bn * 32 + l32) * kLd + kk));
+        };
+        read(0, a[0], b[0]);
 #pragma unroll
-        for (int s = 0; s < kBfBK / 16; ++s)
+        for (int s = 0; s < kSteps; ++s) {
+            if (s + 1 < kSteps)
+                read(s + 1, a[(s + 1) & 1], b[(s + 1) & 1]);
 #pragma unroll
             for (int bm = 0; bm < 4; ++bm)
 #pragma unroll
                 for (int bn = 0; bn < 2; ++bn)
-                    acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s][bm], b[s][bn], acc[bm][bn], 0, 0, 0);
+                    acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s & 1][bm], b[s & 1][bn], acc[bm][bn],
+                                                                          0, 0, 0);
+        }
         __builtin_amdgcn_sched_group_barrier(0x100, 6, 0); // step 0's reads
 #pragma unroll
-        for (int j = 0; j < 6; ++j) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // one step-1 read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // one step-0 MFMA
+        for (int s = 0; s < kSteps; ++s) {
+            if (s + 1 < kSteps) {
+#pragma unroll
+                for (int j = 0; j < 6; ++j) {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // one of step s + 1's reads
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // one of step s's MFMAs
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            } else {
+                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+            }
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 10, 0);
     };
 
     // K tiles of this workgroup: all of them, or split blockIdx.y's contiguous share
-    const int ktiles_all = (K + kBfBK - 1) / kBfBK;
+    const int ktiles_all = (K + BK - 1) / BK;
     const int per_split = (ktiles_all + gridDim.y - 1) / gridDim.y;
     const int kt_begin = blockIdx.y * per_split;
     const int kt_end = kt_begin + per_split < ktiles_all ? kt_begin + per_split : ktiles_all;
     // The vector path pipelines its full K tiles and runs a partial last tile (K not a multiple
     // of the K tile) after the loop, with the tail zeroed; the scalar path bounds every element.
-    const int kt_full = kVec ? (K / kBfBK < kt_end ? (K / kBfBK > kt_begin ? K / kBfBK : kt_begin) : kt_end) : kt_end;
+    const int kt_full = kVec ? (K / BK < kt_end ? (K / BK > kt_begin ? K / BK : kt_begin) : kt_end) : kt_end;
     if (kt_begin < kt_full) {
         global_load(kt_begin);
         lds_store(0, kt_begin, false);
