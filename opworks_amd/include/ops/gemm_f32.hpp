@@ -45,8 +45,9 @@ enum class BLayout { kn, nk };
 
 using f32x16 = float __attribute__((ext_vector_type(16)));
 
-template <int kBM, int kBN, int kWM, int kWN> struct GemmF32Shape {
-    static constexpr int BM = kBM, BN = kBN, BK = 16, WM = kWM, WN = kWN;
+template <int kBM, int kBN, int kWM, int kWN, int kBK = 16> struct GemmF32Shape {
+    static constexpr int BM = kBM, BN = kBN, BK = kBK, WM = kWM, WN = kWN;
+    static_assert(BK % 16 == 0, "a K tile is a whole number of 16-k MFMA groups");
     static constexpr int kThreads = WM * WN * kWaveSize;
     static constexpr int TM = BM / WM, TN = BN / WN;   // wave tile
     static constexpr int FM = TM / 16, FN = TN / 16;   // 16 x 16 MFMA tiles per wave
@@ -57,7 +58,7 @@ template <int kBM, int kBN, int kWM, int kWN> struct GemmF32Shape {
     static_assert(CA * kThreads * 4 == BM * BK && CB * kThreads * 4 == BN * BK, "tile / thread mismatch");
 };
 using GemmSmall = GemmF32Shape<128, 128, 2, 2>;
-using GemmBig = GemmF32Shape<256, 256, 4, 2>;
+using GemmBig = GemmF32Shape<256, 256, 4, 2>; // a K tile of 32 measured 132.4 against 133.5 TFLOP/s
 constexpr int kGemmBK = 16;
 constexpr int kNumXcd = 8;
 
@@ -204,32 +205,35 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
         for (int j = 0; j < FN; ++j)
             acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // One K tile = four MFMA steps; lane group g reads k = 4g .. 4g + 3.
+    // Each 16-k group of a K tile = four MFMA steps; lane group g reads k = 4g .. 4g + 3 of it.
     auto compute = [&](int buf) {
         const float *As = lds + buf * kStage;
         const float *Bs = As + kA;
-        const int kk = 4 * grp;
-        f32x4 a[FM], b[FN];
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
-            a[i] = *reinterpret_cast<const f32x4 *>(As + (wm * TM + i * 16 + l16) * LdK + kk);
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            if constexpr (kB == BLayout::kn) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    b[j][e] = Bs[(kk + e) * LdN + wn * TN + j * 16 + l16];
-            } else {
-                b[j] = *reinterpret_cast<const f32x4 *>(Bs + (wn * TN + j * 16 + l16) * LdK + kk);
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
+        for (int h = 0; h < BK / 16; ++h) {
+            const int kk = 16 * h + 4 * grp;
+            f32x4 a[FM], b[FN];
 #pragma unroll
             for (int i = 0; i < FM; ++i)
+                a[i] = *reinterpret_cast<const f32x4 *>(As + (wm * TM + i * 16 + l16) * LdK + kk);
 #pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < FN; ++j) {
+                if constexpr (kB == BLayout::kn) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        b[j][e] = Bs[(kk + e) * LdN + wn * TN + j * 16 + l16];
+                } else {
+                    b[j] = *reinterpret_cast<const f32x4 *>(Bs + (wn * TN + j * 16 + l16) * LdK + kk);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
+        }
     };
 
     // K tiles of this workgroup: all of them, or split blockIdx.y's contiguous share
