@@ -12,7 +12,7 @@ cannot serve them.
 `value` is the headline workload's throughput; every measured workload also
 appears under `components` with its own roofline. `cpu_baseline` times the CPU
 oracle (the restatement of the reference kernels) on a bounded sample on this
-host.
+host: the headline's at the top level, every other workload's in its component.
 """
 from __future__ import annotations
 
@@ -388,6 +388,10 @@ HEADLINE = "llama"
 
 
 # --------------------------------------------------------------- CPU baseline
+CPU_SAMPLES = ("map", "reduce", "softmax", "rmsnorm", "gemm", "gemm_bf16", "attention", "attention_decode", "scan",
+               "transpose", "gather", "llama")
+
+
 def cpu_baseline(name: str) -> dict:
     """Times the oracle on a bounded sample of the same workload on this host."""
     from tests import oracle as orc
@@ -438,6 +442,63 @@ def cpu_baseline(name: str) -> dict:
         dt = (time.perf_counter() - t0) / reps
         return {"value": round(8 * rows * cols / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
                 "sample": f"oracle orc_rms_norm_rows, 2048 of the 8192 rows, {reps} reps"}
+    def timed(fn, budget_s=3.0):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            if time.perf_counter() - t0 > budget_s:
+                return reps, (time.perf_counter() - t0) / reps
+
+    if name in ("gemm", "gemm_bf16"):
+        n, sample = 4096, np.arange(0, 4096, 64)
+        A = orc.fill_normal(n * n, SEED, 300, 0.0, 1.0 / 64, mt=True)
+        B = orc.fill_normal(n * n, SEED, 301, 0.0, 1.0 / 64, mt=True)
+        bias = orc.fill_uniform(n, SEED, 302, -0.1, 0.1)
+        if name == "gemm_bf16":  # the reference's CPU check of the bf16 path: fp32 math on rounded inputs
+            A, B = orc.round_bf16(A)[0], orc.round_bf16(B)[0]
+        reps, dt = timed(lambda: orc.mat_mul_rows(A, B, n, n, n, rows=sample, bias=bias, act="relu"))
+        return {"value": round(2.0 * len(sample) * n * n / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+                "kind": "port", "sample": f"oracle orc_mat_mul_rows (fp32, plus its float64 |a·b| bound), "
+                                          f"{len(sample)} of the 4096 rows of relu(A·B+bias), {reps} reps"}
+    if name == "attention":
+        T, qh, kvh, D = 2048, 32, 8, 64
+        q = orc.fill_normal(qh * T * D, SEED, 400, 0.0, 1.0, mt=True)
+        k = orc.fill_normal(kvh * T * D, SEED, 401, 0.0, 1.0, mt=True)
+        v = orc.fill_normal(kvh * T * D, SEED, 402, 0.0, 1.0, mt=True)
+        rows = np.arange(0, T, 128)
+        flop = 4.0 * qh * D * float(np.sum(rows + 1))  # unmasked QK^T + PV of the sampled causal rows
+        reps, dt = timed(lambda: orc.attention_explicit(q, k, v, T, T, qh, 4, D, T, rows=rows))
+        return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                "sample": f"oracle orc_attention_explicit, {len(rows)} of the 2048 causal query rows of "
+                          f"every head (unmasked flops), {reps} reps"}
+    if name == "attention_decode":
+        qh, kvh, D, L = 32, 8, 64, 2048
+        q = orc.fill_normal(qh * D, SEED, 410, 0.0, 1.0)
+        k = orc.fill_normal(kvh * L * D, SEED, 411, 0.0, 1.0, mt=True)
+        v = orc.fill_normal(kvh * L * D, SEED, 412, 0.0, 1.0, mt=True)
+        reps, dt = timed(lambda: orc.attention_decode(q, k, v, qh, 4, D, L, L))
+        return {"value": round((2 * kvh * L * D * 4 + 2 * qh * D * 4) / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+                "kind": "port", "sample": f"oracle orc_attention_decode, the full config (len 2048), {reps} reps"}
+    if name == "scan":
+        n = 1 << 24
+        x = orc.fill_uniform(n, SEED, 500, -1.0, 1.0, mt=True)
+        reps, dt = timed(lambda: orc.scan(x))
+        return {"value": round(8 * n / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"oracle orc_scan (inclusive sum, with its float64 |x| prefix) over n=2^24, {reps} reps"}
+    if name == "transpose":
+        r = c = 4096
+        x = orc.fill_uniform(r * c, SEED, 510, -1.0, 1.0, mt=True)
+        reps, dt = timed(lambda: orc.transpose(x, r, c))
+        return {"value": round(8 * r * c / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"oracle orc_transpose of 4096x4096 (a quarter of the 8192x8192 config), {reps} reps"}
+    if name == "gather":
+        n = 1 << 24
+        x = orc.fill_uniform(n, SEED, 520, -1.0, 1.0, mt=True)
+        idx = np.random.default_rng(SEED).permutation(n).astype(np.int32)
+        reps, dt = timed(lambda: orc.gather(x, idx))
+        return {"value": round(12 * n / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"oracle orc_gather through a random permutation of 2^24, {reps} reps"}
     if name == "llama":
         from opworks_amd.llama import LLAMA_3_2_1B
         cfg = dict(LLAMA_3_2_1B)
@@ -483,6 +544,12 @@ def main() -> int:
         results[name] = WORKLOADS[name](stream.handle, args.steps, args.warmup)
         print(f"[bench] {name}: {results[name]['value']:.1f} {results[name]['unit']} "
               f"({results[name]['ms']:.4f} ms/step)", file=sys.stderr, flush=True)
+    if not args.no_cpu:  # the oracle on this host beside every GPU figure (bounded samples)
+        for name in names:
+            if name != headline and name in CPU_SAMPLES:
+                results[name]["cpu_baseline"] = cpu_baseline(name)
+                print(f"[bench] {name} cpu: {results[name]['cpu_baseline']['value']} "
+                      f"{results[name]['cpu_baseline']['unit']}", file=sys.stderr, flush=True)
     head = results[headline]
     line = {
         "metric": METRIC,
