@@ -389,7 +389,7 @@ HEADLINE = "llama"
 
 # --------------------------------------------------------------- CPU baseline
 CPU_SAMPLES = ("map", "reduce", "softmax", "rmsnorm", "gemm", "gemm_bf16", "attention", "attention_decode", "scan",
-               "transpose", "gather", "llama")
+               "transpose", "gather", "llama", "llama_bf16")
 
 
 def cpu_baseline(name: str) -> dict:
@@ -499,9 +499,9 @@ def cpu_baseline(name: str) -> dict:
         reps, dt = timed(lambda: orc.gather(x, idx))
         return {"value": round(12 * n / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
                 "sample": f"oracle orc_gather through a random permutation of 2^24, {reps} reps"}
-    if name == "llama":
+    if name in ("llama", "llama_bf16"):
         from opworks_amd.llama import LLAMA_3_2_1B
-        cfg = dict(LLAMA_3_2_1B)
+        cfg = dict(LLAMA_3_2_1B, torch_dtype="bfloat16") if name == "llama_bf16" else dict(LLAMA_3_2_1B)
         t_build = time.perf_counter()
         model = orc.Llama(cfg, SEED, 0.02, "ones")  # the same seeded weights as the GPU model
         build_s = time.perf_counter() - t_build
@@ -517,8 +517,9 @@ def cpu_baseline(name: str) -> dict:
                 break
         dt = (time.perf_counter() - t0) / steps
         del model
+        kind = "bf16-weight" if name == "llama_bf16" else "fp32"
         return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-                "sample": f"oracle fp32 Llama forward (orc_llama_*), same seeded weights: 16-token prompt "
+                "sample": f"oracle {kind} Llama forward (orc_llama_*), same seeded weights: 16-token prompt "
                           f"(first 16 of the 512 ids), then {steps} greedy decode steps timed "
                           f"(~15 s; weight generation {build_s:.1f} s untimed)"}
     return {}
