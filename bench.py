@@ -195,6 +195,22 @@ def wl_rmsnorm(stream, steps, warmup):
             "kernel": "rms_norm_reg_kernel<1,8>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
 
 
+def wl_layernorm(stream, steps, warmup):
+    """ops::layer_norm (no configuration names it) at config 2c's shape: rows=8192, cols=2048,
+    eps=1e-5, gamma ~ U[0.5,1.5], beta ~ U[-0.1,0.1]; 4 rotating pairs (1 GiB)."""
+    rows, cols, sets = 8192, 2048, 4
+    xs, ys = _rotating(rows, cols, sets, lambda x, k: ow.fill_normal(x, SEED, 220 + k, 0.0, 1.0, stream=stream))
+    g, b = ow.DeviceBuffer.empty(cols), ow.DeviceBuffer.empty(cols)
+    ow.fill_uniform(g, SEED, 230, 0.5, 1.5, stream=stream)
+    ow.fill_uniform(b, SEED, 231, -0.1, 0.1, stream=stream)
+    ms = Timer(stream).run(lambda i: ow.ops.layer_norm(xs[i % sets], ys[i % sets], g, b, rows, cols, 1e-5,
+                                                       stream=stream), steps, warmup)
+    nbytes = 8 * rows * cols + 8 * cols
+    gbs = nbytes / ms / 1e6
+    return {"workload": "layer_norm_8192x2048", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
+            "kernel": "layer_norm_reg_kernel<1,8>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+
+
 def wl_gemm(stream, steps, warmup):
     """Config 3: C = relu(A @ B + bias), M = N = K = 4096 fp32, A, B ~ N(0, 1/64); 2*4096^3 flop."""
     n = 4096
@@ -373,7 +389,7 @@ def wl_gather(stream, steps, warmup):
             "bytes": nbytes, "kernel": "gather_kernel<true>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
 
 
-WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "gemm": wl_gemm, "gemm_bf16": wl_gemm_bf16, "attention": wl_attention,
+WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "layernorm": wl_layernorm, "gemm": wl_gemm, "gemm_bf16": wl_gemm_bf16, "attention": wl_attention,
              "attention_decode": wl_attention_decode, "scan": wl_scan, "transpose": wl_transpose,
              "gather": wl_gather, "llama": wl_llama,
              # the reference's published configurations (README.md:320-339, RTX 4080 SUPER, 128 new tokens)
@@ -388,7 +404,7 @@ HEADLINE = "llama"
 
 
 # --------------------------------------------------------------- CPU baseline
-CPU_SAMPLES = ("map", "reduce", "softmax", "rmsnorm", "gemm", "gemm_bf16", "attention", "attention_decode", "scan",
+CPU_SAMPLES = ("map", "reduce", "softmax", "rmsnorm", "layernorm", "gemm", "gemm_bf16", "attention", "attention_decode", "scan",
                "transpose", "gather", "llama", "llama_bf16")
 
 
@@ -450,6 +466,14 @@ def cpu_baseline(name: str) -> dict:
             if time.perf_counter() - t0 > budget_s:
                 return reps, (time.perf_counter() - t0) / reps
 
+    if name == "layernorm":
+        rows, cols = 2048, 2048
+        x = orc.fill_normal(rows * cols, SEED, 220, 0, 1, mt=True)
+        g = orc.fill_uniform(cols, SEED, 230, 0.5, 1.5)
+        b = orc.fill_uniform(cols, SEED, 231, -0.1, 0.1)
+        reps, dt = timed(lambda: orc.layer_norm_rows(x, g, b, rows, cols, 1e-5))
+        return {"value": round(8 * rows * cols / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": f"oracle orc_layer_norm_rows, 2048 of the 8192 rows, {reps} reps"}
     if name in ("gemm", "gemm_bf16"):
         n, sample = 4096, np.arange(0, 4096, 64)
         A = orc.fill_normal(n * n, SEED, 300, 0.0, 1.0 / 64, mt=True)

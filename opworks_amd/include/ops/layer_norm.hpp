@@ -13,17 +13,29 @@ template <int kW, int kV, bool kExact>
 __global__ __launch_bounds__(RowShape<kW>::kBlock) void layer_norm_reg_kernel(
     const float *__restrict__ in, float *__restrict__ out, const float *__restrict__ gamma,
     const float *__restrict__ beta, int rows, int cols, float eps) {
-    const RowPos p = row_position<kW>(rows);
+    RowPos p = row_position<kW>(rows);
+    p.active = __builtin_amdgcn_readfirstlane(p.active ? 1 : 0) != 0; // wave-uniform: one branch, loads batched
     const int n4 = cols / 4;
     const f32x4 *src = reinterpret_cast<const f32x4 *>(in + p.row * cols);
     f32x4 x[kV];
     float local = 0.f;
+    if constexpr (kExact) { // one wave-uniform test, then the row's loads as one batch
+        if (p.active) {
 #pragma unroll
-    for (int k = 0; k < kV; ++k) {
-        const int q = pack_index<kW>(p, k);
-        if (p.active && (kExact || q < n4)) {
-            x[k] = __builtin_nontemporal_load(src + q);
-            local += (x[k][0] + x[k][1]) + (x[k][2] + x[k][3]);
+            for (int k = 0; k < kV; ++k)
+                x[k] = __builtin_nontemporal_load(src + pack_index<kW>(p, k));
+#pragma unroll
+            for (int k = 0; k < kV; ++k)
+                local += (x[k][0] + x[k][1]) + (x[k][2] + x[k][3]);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kV; ++k) {
+            const int q = pack_index<kW>(p, k);
+            if (p.active && q < n4) {
+                x[k] = __builtin_nontemporal_load(src + q);
+                local += (x[k][0] + x[k][1]) + (x[k][2] + x[k][3]);
+            }
         }
     }
     const float mean = row_combine<kW>(wave::sum(local), p, wave::Add{}) / cols;
