@@ -89,9 +89,19 @@ int opw_mat_mul_f32(const float *A, const float *B, float *C, int M, int N, int 
  * executed as one fused kernel. */
 int opw_mat_mul_fused_f32(const float *A, const float *B, const float *bias, float *C, int M, int N, int K,
                           int b_transposed, int activation, void *stream);
+/* The same with a transposed A as well: op(A) is M x N, stored N x M (column-major) when a_transposed
+ * (MatmulBuilder::transpose_a, include/builders/matmul.cuh:19-20,35); read in place by the GEMM. */
+int opw_mat_mul_fused_ex_f32(const float *A, const float *B, const float *bias, float *C, int M, int N, int K,
+                             int a_transposed, int b_transposed, int activation, void *stream);
 /* Y[rows][out] = X[rows][in] @ W[out][in]^T (reference: ops::linear, include/ops/linear.cuh:130-153) */
 int opw_linear_f32(const float *X, const float *W, float *Y, int rows, int in_features, int out_features,
                    void *stream);
+
+/* Y[rows][out] = X[rows][in] @ W[out][in]^T with bf16 weights W (raw bits), fp32 X and Y: every weight is
+ * widened exactly and products accumulate in fp32 (reference: ops::linear<__nv_bfloat16>,
+ * include/ops/linear.cuh:99-153: gemv_bf16_kernel at rows == 1, the fp32 tiled kernel above). */
+int opw_linear_wbf16(const float *X, const uint16_t *W, float *Y, int rows, int in_features, int out_features,
+                     void *stream);
 
 /* ---- bf16 matrix-core path (reference: ops::linear_mma_bf16, include/ops/linear_mma.cuh:99-115) ----
  * Y[rows][out] = act(bf16(X)[rows][in] @ W[out][in]^T + bias), fp32 accumulation; W holds bf16 bit
@@ -121,6 +131,12 @@ int opw_attention_decode_workspace_size(int num_q_heads, int max_len, int head_d
 int opw_attention_decode_ws_f32(const float *q, const float *kcache, const float *vcache, float *out,
                                 int num_q_heads, int kv_rep, int head_dim, int len, int max_seq, float *workspace,
                                 int workspace_size, void *stream);
+/* ... in one launch, as the Llama decode step runs it: the last chunk workgroup of each kv head merges
+ * the head group's records. `counters` holds num_q_heads / kv_rep ints, zero before the call and zero
+ * again after it; calls sharing counters must not overlap. Same results as opw_attention_decode_ws_f32. */
+int opw_attention_decode_fused_f32(const float *q, const float *kcache, const float *vcache, float *out,
+                                   int num_q_heads, int kv_rep, int head_dim, int len, int max_seq, float *workspace,
+                                   int workspace_size, int *counters, void *stream);
 
 /* ---- decoder-block steps (reference: include/ops/add.cuh:18-25, swiglu.cuh:19-26,
  *      causal_scale.cuh:24-33, embedding.cuh:24-34, split_heads.cuh:39-66, rope.cuh:34-46,

@@ -70,6 +70,9 @@ _SIGNATURES = {
     "opw_mat_mul_fused_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                       c_void_p]),
     "opw_linear_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
+    "opw_mat_mul_fused_ex_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
+                                         c_int, c_void_p]),
+    "opw_linear_wbf16": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "opw_linear_bf16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
     "opw_linear_bf16_bf16": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
     "opw_convert_f32_to_bf16": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
@@ -78,6 +81,8 @@ _SIGNATURES = {
     "opw_attention_decode_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                          c_void_p]),
     "opw_attention_decode_workspace_size": (c_int, [c_int, c_int, c_int]),
+    "opw_attention_decode_fused_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
+                                               c_int, c_void_p, c_int, c_void_p, c_void_p]),
     "opw_attention_decode_ws_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                             c_void_p, c_int, c_void_p]),
     "opw_add_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
@@ -349,8 +354,18 @@ class _Ops:
         check(lib().opw_mat_mul_fused_f32(_p(A), _p(B), _p(bias), _p(C), M, N, K, int(b_transposed),
                                           self.ACTIVATIONS[activation], _stream(stream)))
 
+    def mat_mul_fused_ex(self, A: Ptr, B: Ptr, bias: Ptr, C: Ptr, M: int, N: int, K: int, a_transposed: bool,
+                         b_transposed: bool, activation: str = "none", stream=None) -> None:
+        check(lib().opw_mat_mul_fused_ex_f32(_p(A), _p(B), _p(bias), _p(C), M, N, K, int(a_transposed),
+                                             int(b_transposed), self.ACTIVATIONS[activation], _stream(stream)))
+
     def linear(self, X: Ptr, W: Ptr, Y: Ptr, rows: int, in_features: int, out_features: int, stream=None) -> None:
         check(lib().opw_linear_f32(_p(X), _p(W), _p(Y), rows, in_features, out_features, _stream(stream)))
+
+    # ops::linear<bf16>: fp32 X against bf16 weights (uint16 bits) widened exactly, fp32 accumulation.
+    def linear_wbf16(self, X: Ptr, W: Ptr, Y: Ptr, rows: int, in_features: int, out_features: int,
+                     stream=None) -> None:
+        check(lib().opw_linear_wbf16(_p(X), _p(W), _p(Y), rows, in_features, out_features, _stream(stream)))
 
     def linear_bf16(self, X: Ptr, W: Ptr, bias: Ptr, Y: Ptr, rows: int, in_features: int, out_features: int,
                     activation: str = "none", x_bf16: bool = False, stream=None) -> None:
@@ -375,6 +390,15 @@ class _Ops:
             check(lib().opw_attention_decode_ws_f32(_p(q), _p(k), _p(v), _p(out), num_q_heads, kv_rep, head_dim,
                                                     length, max_seq, _p(workspace), workspace_size,
                                                     _stream(stream)))
+
+    # One launch: the last chunk workgroup of each kv head merges; counters (int32, one per kv head)
+    # are zero before and after the call.
+    def attention_decode_fused(self, q: Ptr, k: Ptr, v: Ptr, out: Ptr, num_q_heads: int, kv_rep: int,
+                               head_dim: int, length: int, max_seq: int, workspace: Ptr, workspace_size: int,
+                               counters: Ptr, stream=None) -> None:
+        check(lib().opw_attention_decode_fused_f32(_p(q), _p(k), _p(v), _p(out), num_q_heads, kv_rep, head_dim,
+                                                   length, max_seq, _p(workspace), workspace_size, _p(counters),
+                                                   _stream(stream)))
 
     def attention_decode_workspace_size(self, num_q_heads: int, max_len: int, head_dim: int) -> int:
         return check(lib().opw_attention_decode_workspace_size(num_q_heads, max_len, head_dim))

@@ -3,7 +3,8 @@
 Outputs (all git-ignored, all shipped to the GPU box with the tree):
   opworks_amd/lib/libopworks_amd.so      HIP kernels + the extern "C" ABI
   opworks_amd/lib/adapters/*.so          one `solve` adapter per reference challenge
-  opworks_amd/lib/tests/*                hipcc-built C++ unit-test executables
+  opworks_amd/lib/tests/*                hipcc-built C++ unit-test executables and test-only
+                                         libraries (libprobe_*.so)
   oracle/liboracle.so                    the CPU checker (gcc), via oracle/Makefile
   oracle/_ref/*                          reference host code, when /root/reference exists
 
@@ -43,10 +44,12 @@ HIP_FLAGS = [
 
 LIB_SOURCES = sorted(CSRC.glob("*.hip"))
 ADAPTER_SOURCES = sorted((CSRC / "adapters").glob("*.hip"))
-# One executable per top-level .hip file or per subdirectory (all its .hip files).
-TEST_SOURCES = sorted((CSRC / "tests").glob("*.hip")) + sorted(
+# One executable per top-level .hip file or per subdirectory (all its .hip files);
+# a top-level probe_<name>.hip is a test-only shared library lib<probe_name>.so.
+TEST_SOURCES = sorted(p for p in (CSRC / "tests").glob("*.hip") if not p.name.startswith("probe_")) + sorted(
     d for d in (CSRC / "tests").glob("*") if d.is_dir() and any(d.glob("*.hip"))
 )
+PROBE_SOURCES = sorted((CSRC / "tests").glob("probe_*.hip"))
 
 
 def _run(cmd: list[str], cwd: Path | None = None) -> None:
@@ -99,8 +102,13 @@ def build_tests(jobs: int) -> list[Path]:
         _run([HIPCC, *HIP_FLAGS, "-o", str(exe), *map(str, files)])
         return exe
 
+    def probe(src: Path) -> Path:
+        so = out_dir / f"lib{src.stem}.so"
+        _run([HIPCC, *HIP_FLAGS, "-shared", "-o", str(so), str(src)])
+        return so
+
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        return list(ex.map(one, TEST_SOURCES))
+        return list(ex.map(one, TEST_SOURCES)) + list(ex.map(probe, PROBE_SOURCES))
 
 
 def build_oracle() -> None:

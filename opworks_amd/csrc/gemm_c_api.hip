@@ -30,10 +30,30 @@ int opw_mat_mul_fused_f32(const float *A, const float *B, const float *bias, flo
     });
 }
 
+int opw_mat_mul_fused_ex_f32(const float *A, const float *B, const float *bias, float *C, int M, int N, int K,
+                             int a_transposed, int b_transposed, int activation, void *stream) {
+    return guard([&] {
+        opworks::detail::require(activation >= 0 && activation <= 2, "activation must be 0 none, 1 relu, 2 gelu");
+        opworks::ops::mat_mul_fused(A, B, bias, C, M, N, K, a_transposed != 0, b_transposed != 0,
+                                    static_cast<opworks::ops::Activation>(activation),
+                                    static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
 int opw_linear_f32(const float *X, const float *W, float *Y, int rows, int in_features, int out_features,
                    void *stream) {
     return guard([&] {
         opworks::ops::linear(X, W, Y, rows, in_features, out_features, static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
+int opw_linear_wbf16(const float *X, const uint16_t *W, float *Y, int rows, int in_features, int out_features,
+                     void *stream) {
+    return guard([&] {
+        opworks::ops::linear(X, reinterpret_cast<const opworks::bf16 *>(W), Y, rows, in_features, out_features,
+                             static_cast<hipStream_t>(stream));
         return 0;
     });
 }

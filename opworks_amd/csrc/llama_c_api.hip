@@ -64,7 +64,7 @@ void *opw_llama_create_session(void *model, int max_seq_len, char *err, int err_
     return guard_ptr(
         [&]() -> void * {
             auto *m = static_cast<ModelHolder *>(model);
-            return new SessionHolder{m, m->model->create_session(max_seq_len)};
+            return new SessionHolder{m, m->model->new_session(max_seq_len)};
         },
         err, err_len);
 }
@@ -214,6 +214,9 @@ int opw_llama_generate_greedy(void *session, const int32_t *prompt, int n, int m
             if (!prompt || n <= 0 || max_new <= 0 || !out_tokens)
                 throw std::invalid_argument("generate needs a prompt, max_new > 0 and an output buffer");
             opworks::LlamaRuntime &m = *s->owner->model;
+            // checked before any work, so a rejected call leaves the session untouched
+            if (int64_t(n) + max_new - 1 > s->session->cache.max_seq_len)
+                throw std::invalid_argument("prompt plus max_new - 1 generated tokens exceed the session capacity");
             std::vector<int32_t> ids(prompt, prompt + n);
             using clock = std::chrono::steady_clock;
             const auto t0 = clock::now();
@@ -236,10 +239,14 @@ int opw_llama_profile_decode_step(void *session, int32_t prev_token, float *kern
     return guard(
         [&] {
             auto *s = as_session(session);
+            // one duration per decode stage of every layer plus the LM head, checked before any work
+            const int stages = 5 * s->owner->model->config().num_layers + 1;
+            if (!kernel_ms || capacity < stages)
+                throw std::invalid_argument("kernel_ms needs 5 * layers + 1 entries");
             int32_t next = -1;
             std::vector<float> ms = s->owner->model->profile_decode_step(*s->session, prev_token, &next);
-            if (!kernel_ms || capacity < static_cast<int>(ms.size()))
-                throw std::invalid_argument("kernel_ms needs 5 * layers + 1 entries");
+            if (static_cast<int>(ms.size()) != stages)
+                throw std::logic_error("profile_decode_step timed an unexpected number of stages");
             std::memcpy(kernel_ms, ms.data(), ms.size() * sizeof(float));
             return static_cast<int>(ms.size());
         },

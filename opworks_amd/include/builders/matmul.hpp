@@ -4,8 +4,9 @@
 // surface (interface: include/builders/matmul.cuh:7-57: transpose_a/b, bias,
 // activation, accessors, apply(fn)). run() is an addition: it launches the
 // fused MFMA kernel, output = act(a @ op(b) + bias), with bias and activation
-// applied in the kernel's epilogue. Shapes keep the reference's names: a is
-// m x n, b is n x k (k x n when transposed), the output m x k.
+// applied in the kernel's epilogue; a transposed a or b is read in place.
+// Shapes keep the reference's names: a is m x n (n x m when transposed), b
+// is n x k (k x n when transposed), the output m x k.
 
 #include <initializer_list>
 #include <utility>
@@ -47,13 +48,12 @@ class MatmulBuilder : public detail::CallbackBuilder<MatmulBuilder> {
     hipStream_t stream() const { return stream_; }
 
     void run() const {
-        detail::require(!flags_.ta, "MatmulBuilder::run: transpose_a is not supported by the fused kernel");
         detail::require(bias_.size() == 0 || bias_.size() >= k(), "matmul bias is shorter than the output width");
         const auto act = flags_.act == MatmulActivation::relu   ? ops::Activation::relu
                          : flags_.act == MatmulActivation::gelu ? ops::Activation::gelu
                                                                 : ops::Activation::none;
         ops::mat_mul_fused(lhs_.data(), rhs_.data(), bias_.size() ? bias_.data() : nullptr, out_.data(), m(), n(),
-                           k(), flags_.tb, act, stream_);
+                           k(), flags_.ta, flags_.tb, act, stream_);
     }
 
   private:

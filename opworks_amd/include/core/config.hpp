@@ -20,6 +20,22 @@
 #define OPWORKS_PACK_SIZE 4
 #endif
 
+// Tile knobs of the reference's SIMT GEMM (its include/core/config.cuh:27-37,
+// 61-63). They are accepted and checked for source compatibility, but the
+// MFMA GEMMs here take their tile shapes from the matrix-core layout
+// (ops/gemm_f32.hpp, ops/gemm_bf16.hpp), so these values select nothing.
+#ifndef OPWORKS_MATMUL_TILE
+#define OPWORKS_MATMUL_TILE 64
+#endif
+
+#ifndef OPWORKS_MATMUL_BLOCK
+#define OPWORKS_MATMUL_BLOCK 16
+#endif
+
+#ifndef OPWORKS_MATMUL_SUBTILE
+#define OPWORKS_MATMUL_SUBTILE 4
+#endif
+
 #ifndef OPWORKS_LAYERNORM_EPS
 #define OPWORKS_LAYERNORM_EPS 1e-5f
 #endif
@@ -42,6 +58,9 @@ constexpr int kThreads = OPWORKS_THREADS;    // default workgroup size for op la
 constexpr int kNumWaves = OPWORKS_NUM_WAVES; // grid cap: resident workgroups per CU times this
 constexpr int kPackSize = OPWORKS_PACK_SIZE; // floats per 16-byte pack in map/reduce kernels
 constexpr float kLayerNormEps = OPWORKS_LAYERNORM_EPS;
+constexpr int kMatmulTile = OPWORKS_MATMUL_TILE;   // reference SIMT GEMM output tile edge (inert here)
+constexpr int kMatmulBlock = OPWORKS_MATMUL_BLOCK; // reference SIMT GEMM K slice (inert here)
+constexpr int kMatmulSub = OPWORKS_MATMUL_SUBTILE; // reference SIMT GEMM per-lane sub-tile (inert here)
 
 // The reference's block_reduce contract requires whole multiples of 32 threads;
 // it is kept (a 32-lane tail wave is handled through LDS).
@@ -51,6 +70,9 @@ static_assert(kThreads > 0 && kThreads % kWaveSize == 0 && kThreads <= kMaxThrea
               "kThreads must be a positive multiple of the 64-lane wavefront and fit in a workgroup");
 static_assert(kNumWaves > 0, "kNumWaves must be positive");
 static_assert(kPackSize == 1 || kPackSize == 2 || kPackSize == 4, "kPackSize must be 1, 2 or 4");
+static_assert(kMatmulTile == kMatmulBlock * kMatmulSub, "kMatmulTile must equal kMatmulBlock * kMatmulSub");
+static_assert(kMatmulBlock > 0 && kMatmulSub > 0 && kMatmulBlock * kMatmulBlock <= kMaxThreadsPerBlock,
+              "matmul knobs must be positive and describe a workgroup of at most 1024 lanes");
 static_assert(kLayerNormEps > 0 && kLayerNormEps <= FLT_MAX, "layer norm epsilon must be finite and positive");
 
 } // namespace opworks

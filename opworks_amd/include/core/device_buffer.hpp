@@ -1,85 +1,47 @@
 #pragma once
 
-// Move-only owner of an fp32 device allocation (reference:
-// include/core/device_buffer.cuh:9-81). Host copies are blocking on the given
-// stream; empty buffers allocate nothing.
+// DeviceBuffer: the fp32 owner the operator API and the builders use. It is
+// TypedDeviceBuffer<float> with the reference's int-sized surface
+// (include/core/device_buffer.cuh:9-81): sizes are int (at most INT_MAX
+// elements), host transfers block on the given stream, to_host_scalar needs
+// exactly one element, and view() lends a DeviceSpan only from an lvalue
+// owner, so a span can never outlive a temporary.
 
 #include <limits>
 #include <vector>
 
 #include "device_span.hpp"
+#include "typed_device_buffer.hpp"
 
 namespace opworks {
 
 class DeviceBuffer {
   public:
     DeviceBuffer() = default;
-    explicit DeviceBuffer(int n) : n_(n) {
-        detail::validate_size(n);
-        if (n != 0)
-            OPWORKS_HIP_CHECK(hipMalloc(reinterpret_cast<void **>(&ptr_), sizeof(float) * static_cast<size_t>(n_)));
-    }
-    ~DeviceBuffer() {
-        if (ptr_)
-            (void)hipFree(ptr_);
-    }
+    explicit DeviceBuffer(int n) : store_((detail::validate_size(n), n)) {}
 
-    DeviceBuffer(const DeviceBuffer &) = delete;
-    DeviceBuffer &operator=(const DeviceBuffer &) = delete;
-    DeviceBuffer(DeviceBuffer &&o) noexcept : ptr_(o.ptr_), n_(o.n_) {
-        o.ptr_ = nullptr;
-        o.n_ = 0;
-    }
-    DeviceBuffer &operator=(DeviceBuffer &&o) noexcept {
-        if (this != &o) {
-            if (ptr_)
-                (void)hipFree(ptr_);
-            ptr_ = o.ptr_;
-            n_ = o.n_;
-            o.ptr_ = nullptr;
-            o.n_ = 0;
-        }
-        return *this;
-    }
-
-    static DeviceBuffer from_host(const std::vector<float> &h, hipStream_t stream = nullptr) {
-        detail::require(h.size() <= static_cast<size_t>(std::numeric_limits<int>::max()),
+    static DeviceBuffer from_host(const std::vector<float> &host, hipStream_t stream = nullptr) {
+        detail::require(host.size() <= static_cast<size_t>(std::numeric_limits<int>::max()),
                         "buffer exceeds the supported INT_MAX elements");
-        DeviceBuffer buf(static_cast<int>(h.size()));
-        if (!h.empty()) {
-            OPWORKS_HIP_CHECK(
-                hipMemcpyAsync(buf.ptr_, h.data(), sizeof(float) * h.size(), hipMemcpyHostToDevice, stream));
-            synchronize(stream);
-        }
-        return buf;
+        return DeviceBuffer(TypedDeviceBuffer<float>::from_host(host, stream));
     }
 
-    std::vector<float> to_host(hipStream_t stream = nullptr) const {
-        std::vector<float> h(static_cast<size_t>(n_));
-        if (n_ != 0) {
-            OPWORKS_HIP_CHECK(hipMemcpyAsync(h.data(), ptr_, sizeof(float) * h.size(), hipMemcpyDeviceToHost, stream));
-            synchronize(stream);
-        }
-        return h;
-    }
+    std::vector<float> to_host(hipStream_t stream = nullptr) const { return store_.to_host(stream); }
+    float to_host_scalar(hipStream_t stream = nullptr) const { return store_.to_host_scalar(stream); }
 
-    float to_host_scalar(hipStream_t stream = nullptr) const {
-        detail::require(n_ == 1, "scalar copy requires exactly one element");
-        return to_host(stream)[0];
-    }
-
-    DeviceSpan<float> view() & { return {ptr_, n_}; }
-    DeviceSpan<const float> view() const & { return {ptr_, n_}; }
+    DeviceSpan<float> view() & { return {data(), size()}; }
+    DeviceSpan<const float> view() const & { return {data(), size()}; }
     DeviceSpan<float> view() && = delete;
     DeviceSpan<const float> view() const && = delete;
 
-    float *data() { return ptr_; }
-    const float *data() const { return ptr_; }
-    int size() const { return n_; }
+    float *data() { return store_.data(); }
+    const float *data() const { return store_.data(); }
+    int size() const { return static_cast<int>(store_.size()); }
 
   private:
-    float *ptr_ = nullptr;
-    int n_ = 0;
+    explicit DeviceBuffer(TypedDeviceBuffer<float> &&store) : store_(std::move(store)) {}
+
+    TypedDeviceBuffer<float> store_;
 };
 
 } // namespace opworks

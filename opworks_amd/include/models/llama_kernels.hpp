@@ -28,6 +28,7 @@
 #include "../core/bf16.hpp"
 #include "../core/hip_utils.hpp"
 #include "../core/wave.hpp"
+#include "../core/weight_pack.hpp"
 #include "../ops/argmax.hpp"
 #include "../ops/attention.hpp"
 #include "../ops/elementwise.hpp"
@@ -48,44 +49,12 @@ constexpr int kRows = 4;       // rows per LM-head wave; rows per workgroup of t
 constexpr int kBlock = 256;    // threads per GEMV workgroup
 constexpr int kWavesPerBlock = kBlock / kWaveSize;
 
-// Weights are streamed in 16-byte packs: 4 fp32 or 8 bf16 values; bf16 is
-// widened exactly (bits << 16) and every product is accumulated in fp32.
-using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
-template <typename WT> struct WPack;
-template <> struct WPack<float> {
-    static constexpr int kElems = 4;
-    using type = f32x4;
-    __device__ static float at(const f32x4 &p, int j) { return p[j]; }
-};
-template <> struct WPack<bf16> {
-    static constexpr int kElems = 8;
-    using type = u32x4;
-    __device__ static float at(const u32x4 &p, int j) {
-        const uint32_t w = p[j >> 1];
-        return __builtin_bit_cast(float, (j & 1) ? (w & 0xffff0000u) : (w << 16));
-    }
-};
-template <typename WT> __device__ __forceinline__ typename WPack<WT>::type load_wpack(const WT *row, int pack) {
-    return __builtin_nontemporal_load(reinterpret_cast<const typename WPack<WT>::type *>(row) + pack);
-}
-template <typename WT> __device__ __forceinline__ float widen(WT v) {
-    if constexpr (std::is_same_v<WT, bf16>)
-        return bf16_to_float(v.bits);
-    else
-        return v;
-}
-// acc += sum_j w[j] * x[j] over one pack (x: the pack's kElems inputs)
-template <typename WT>
-__device__ __forceinline__ float dot_wpack(const typename WPack<WT>::type &w, const f32x4 (&x)[WPack<WT>::kElems / 4],
-                                           float acc) {
-    constexpr int E = WPack<WT>::kElems;
-#pragma unroll
-    for (int q = 0; q < E / 4; ++q)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            acc = fmaf(WPack<WT>::at(w, 4 * q + j), x[q][j], acc);
-    return acc;
-}
+// Weights are streamed in 16-byte packs (core/weight_pack.hpp).
+using detail::dot_wpack;
+using detail::load_wpack;
+using detail::u32x4;
+using detail::widen;
+using detail::WPack;
 
 // GEMV of a 4-wave workgroup: each wave owns kR rows of a [*, H] matrix,
 // H = 256 * kV. The input vector is staged once per workgroup: its loads are

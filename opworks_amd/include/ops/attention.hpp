@@ -630,33 +630,34 @@ inline int attention_decode_workspace_size(int num_q_heads, int max_len, int hea
     return detail::attention_decode_workspace_floats(num_q_heads, max_len, head_dim);
 }
 
-// Single-query GQA attention over the first len cache entries, workspace form
-// (no allocation; graph-capturable). If len_ptr is non-null the length is
-// *len_ptr + len_bias, read on the device, and max_len bounds it.
-inline void attention_decode_ws(const float *q, const float *kcache, const float *vcache, float *out,
-                                int num_q_heads, int kv_rep, int head_dim, int len, int max_seq, float *workspace,
-                                int workspace_size, const int *len_ptr = nullptr, int len_bias = 0,
-                                int max_len = 0, hipStream_t stream = nullptr) {
-    detail::require(num_q_heads > 0 && kv_rep > 0 && head_dim > 0 && num_q_heads % kv_rep == 0,
-                    "attention_decode requires positive head shape");
-    detail::require(kv_rep <= detail::kAttnMaxRep, "attention_decode supports at most 16 q heads per kv head");
-    detail::require(head_dim <= 64, "attention_decode supports head_dim <= 64");
+} // namespace opworks::ops
+
+namespace opworks::detail {
+
+inline void attention_decode_enqueue(const float *q, const float *kcache, const float *vcache, float *out,
+                                     int num_q_heads, int kv_rep, int head_dim, int len, int max_seq,
+                                     float *workspace, int workspace_size, const int *len_ptr, int len_bias,
+                                     int max_len, int *counters, hipStream_t stream) {
+    require(num_q_heads > 0 && kv_rep > 0 && head_dim > 0 && num_q_heads % kv_rep == 0,
+            "attention_decode requires positive head shape");
+    require(kv_rep <= kAttnMaxRep, "attention_decode supports at most 16 q heads per kv head");
+    require(head_dim <= 64, "attention_decode supports head_dim <= 64");
     const int bound = len_ptr ? max_len : len;
-    detail::require(bound > 0 && bound <= max_seq, "attention_decode length outside the cache capacity");
-    detail::require(bound <= detail::kAttnDecodeMaxLen, "attention_decode length exceeds 8192");
-    detail::require(q && kcache && vcache && out && workspace, "attention_decode requires non-null pointers");
-    const int max_chunks = (bound + detail::kAttnChunk - 1) / detail::kAttnChunk;
-    detail::require(workspace_size >= num_q_heads * max_chunks * (head_dim + 2), "attention_decode workspace is too small");
-    detail::require(head_dim % 4 == 0, "attention_decode needs head_dim to be a multiple of 4");
-    detail::require(detail::aligned16(q) && detail::aligned16(kcache) && detail::aligned16(vcache),
-                    "attention_decode needs 16-byte aligned q and caches");
-    detail::DecodeAttnArgs a{};
+    require(bound > 0 && bound <= max_seq, "attention_decode length outside the cache capacity");
+    require(bound <= kAttnDecodeMaxLen, "attention_decode length exceeds 8192");
+    require(q && kcache && vcache && out && workspace, "attention_decode requires non-null pointers");
+    const int max_chunks = (bound + kAttnChunk - 1) / kAttnChunk;
+    require(workspace_size >= num_q_heads * max_chunks * (head_dim + 2), "attention_decode workspace is too small");
+    require(head_dim % 4 == 0, "attention_decode needs head_dim to be a multiple of 4");
+    require(aligned16(q) && aligned16(kcache) && aligned16(vcache), "attention_decode needs 16-byte aligned q and caches");
+    DecodeAttnArgs a{};
     a.q = q;
     a.kcache = kcache;
     a.vcache = vcache;
     a.out = out;
     a.partial = workspace;
     a.len_ptr = len_ptr;
+    a.counters = counters;
     a.len = len;
     a.len_bias = len_bias;
     a.kv_rep = kv_rep;
@@ -664,7 +665,34 @@ inline void attention_decode_ws(const float *q, const float *kcache, const float
     a.cap = max_seq;
     a.max_chunks = max_chunks;
     a.scale = 1.f / std::sqrt(static_cast<float>(head_dim));
-    detail::attention_decode_launch(a, num_q_heads / kv_rep, stream);
+    attention_decode_launch(a, num_q_heads / kv_rep, stream);
+}
+
+} // namespace opworks::detail
+
+namespace opworks::ops {
+
+// Single-query GQA attention over the first len cache entries, workspace form
+// (no allocation; graph-capturable). If len_ptr is non-null the length is
+// *len_ptr + len_bias, read on the device, and max_len bounds it.
+inline void attention_decode_ws(const float *q, const float *kcache, const float *vcache, float *out,
+                                int num_q_heads, int kv_rep, int head_dim, int len, int max_seq, float *workspace,
+                                int workspace_size, const int *len_ptr = nullptr, int len_bias = 0,
+                                int max_len = 0, hipStream_t stream = nullptr) {
+    detail::attention_decode_enqueue(q, kcache, vcache, out, num_q_heads, kv_rep, head_dim, len, max_seq, workspace,
+                                     workspace_size, len_ptr, len_bias, max_len, nullptr, stream);
+}
+
+// The same in one launch: the last chunk workgroup of each kv head to finish
+// merges that head group's records. `counters` holds num_q_heads / kv_rep
+// ints that are zero before the call and are zero again when it completes;
+// calls that share counters must not overlap.
+inline void attention_decode_fused(const float *q, const float *kcache, const float *vcache, float *out,
+                                   int num_q_heads, int kv_rep, int head_dim, int len, int max_seq, float *workspace,
+                                   int workspace_size, int *counters, hipStream_t stream = nullptr) {
+    detail::require(counters != nullptr, "attention_decode_fused needs its arrival counters");
+    detail::attention_decode_enqueue(q, kcache, vcache, out, num_q_heads, kv_rep, head_dim, len, max_seq, workspace,
+                                     workspace_size, nullptr, 0, 0, counters, stream);
 }
 
 // Reference signature (include/ops/attention_decode.cuh:99-109): scratch comes

@@ -17,10 +17,10 @@
 #include <cstdint>
 
 #include "../core/hip_utils.hpp"
+#include "../core/weight_pack.hpp"
 
 namespace opworks::detail {
 
-using f32x4 = float __attribute__((ext_vector_type(4)));
 
 constexpr int64_t kMaxGrid = 1ll << 30; // workgroups; far above what INT_MAX elements need
 

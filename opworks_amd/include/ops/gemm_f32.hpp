@@ -2,6 +2,9 @@
 
 // fp32 GEMM on the CDNA4 matrix cores: C[m][n] = epi(sum_k A[m][k] * B(k, n) + bias[n]).
 //
+// A comes in two layouts: ALayout::mk — A[m][k], k contiguous (the usual
+// row-major operand) — and ALayout::km — A[k][m], m contiguous (a transposed
+// operand, MatmulBuilder::transpose_a), staged like the kn-layout B.
 // B comes in two layouts:
 //  * BLayout::kn — B[k][n], n contiguous: ops::mat_mul (reference
 //    include/ops/matmul.cuh:11-91, where the reduction dim is called N);
@@ -42,6 +45,7 @@
 namespace opworks::detail {
 
 enum class BLayout { kn, nk };
+enum class ALayout { mk, km };
 
 using f32x16 = float __attribute__((ext_vector_type(16)));
 
@@ -53,6 +57,7 @@ template <int kBM, int kBN, int kWM, int kWN, int kBK = 16> struct GemmF32Shape 
     static constexpr int FM = TM / 16, FN = TN / 16;   // 16 x 16 MFMA tiles per wave
     static constexpr int LdK = BK + 4;                 // padded row of a k-contiguous tile
     static constexpr int LdN = BN + 4;                 // padded row of the kn-layout B tile
+    static constexpr int LdM = BM + 4;                 // padded row of the km-layout A tile
     static constexpr int CA = BM * BK / 4 / kThreads;  // 16-byte A chunks per thread per K tile
     static constexpr int CB = BN * BK / 4 / kThreads;  // 16-byte B chunks per thread per K tile
     static_assert(CA * kThreads * 4 == BM * BK && CB * kThreads * 4 == BN * BK, "tile / thread mismatch");
@@ -98,7 +103,7 @@ __device__ __forceinline__ void gemm_tile_of(int bid, int tiles_m, int tiles_n, 
 // fp32 (bits << 16) while staged, so the products are fp32 x fp32 on the
 // matrix core (the reference's rows 2..15 path for bf16 weights).
 template <typename Shape, BLayout kB, bool kVec, typename Epi, GemmStore kStore = GemmStore::store,
-          typename TB = float>
+          typename TB = float, ALayout kAL = ALayout::mk>
 __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const float *__restrict__ A,
                                                                         const TB *__restrict__ B,
                                                                         const float *__restrict__ bias,
@@ -106,8 +111,8 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
                                                                         Epi epi) {
     constexpr int BM = Shape::BM, BN = Shape::BN, BK = Shape::BK, T_ = Shape::kThreads;
     constexpr int TM = Shape::TM, TN = Shape::TN, FM = Shape::FM, FN = Shape::FN;
-    constexpr int LdK = Shape::LdK, LdN = Shape::LdN, CA = Shape::CA, CB = Shape::CB;
-    constexpr int kA = BM * LdK;                                    // floats of the A stage
+    constexpr int LdK = Shape::LdK, LdN = Shape::LdN, LdM = Shape::LdM, CA = Shape::CA, CB = Shape::CB;
+    constexpr int kA = kAL == ALayout::mk ? BM * LdK : BK * LdM;    // floats of the A stage
     constexpr int kStage = kA + (kB == BLayout::kn ? BK * LdN : BN * LdK);
     __shared__ __attribute__((aligned(16))) float lds[2 * kStage];
 
@@ -172,9 +177,28 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
             }
         }
     };
+    auto load_a_km = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < CA; ++i) {
+            const int idx = tid + T_ * i;
+            const int r = idx / (BM / 4), c = (idx % (BM / 4)) * 4;
+            const int gk = k0 + r, gm = m0 + c;
+            if constexpr (kVec) {
+                ra[i] = (gk < K && gm < M) ? *reinterpret_cast<const f32x4 *>(A + int64_t(gk) * M + gm)
+                                           : f32x4{0.f, 0.f, 0.f, 0.f};
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    ra[i][j] = (gk < K && gm + j < M) ? A[int64_t(gk) * M + gm + j] : 0.f;
+            }
+        }
+    };
     auto global_load = [&](int kt) {
         const int k0 = kt * BK;
-        load_rows_k(A, m0, M, k0, ra);
+        if constexpr (kAL == ALayout::mk)
+            load_rows_k(A, m0, M, k0, ra);
+        else
+            load_a_km(k0);
         if constexpr (kB == BLayout::kn)
             load_b_kn(k0);
         else
@@ -186,7 +210,10 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
 #pragma unroll
         for (int i = 0; i < CA; ++i) {
             const int idx = tid + T_ * i;
-            *reinterpret_cast<f32x4 *>(As + (idx / (BK / 4)) * LdK + (idx % (BK / 4)) * 4) = ra[i];
+            if constexpr (kAL == ALayout::mk)
+                *reinterpret_cast<f32x4 *>(As + (idx / (BK / 4)) * LdK + (idx % (BK / 4)) * 4) = ra[i];
+            else
+                *reinterpret_cast<f32x4 *>(As + (idx / (BM / 4)) * LdM + (idx % (BM / 4)) * 4) = ra[i];
         }
 #pragma unroll
         for (int i = 0; i < CB; ++i) {
@@ -214,8 +241,15 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
             const int kk = 16 * h + 4 * grp;
             f32x4 a[FM], b[FN];
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
-                a[i] = *reinterpret_cast<const f32x4 *>(As + (wm * TM + i * 16 + l16) * LdK + kk);
+            for (int i = 0; i < FM; ++i) {
+                if constexpr (kAL == ALayout::mk) {
+                    a[i] = *reinterpret_cast<const f32x4 *>(As + (wm * TM + i * 16 + l16) * LdK + kk);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        a[i][e] = As[(kk + e) * LdM + wm * TM + i * 16 + l16];
+                }
+            }
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 if constexpr (kB == BLayout::kn) {
@@ -328,35 +362,40 @@ inline int splitk_factor(int tiles, int ktiles, int target) {
     return s;
 }
 
-inline bool gemm_vec_ok(const void *a, const void *b, int K, int N, BLayout layout) {
+// 16-byte loads need aligned operands and 4-element runs along each contiguous dimension.
+inline bool gemm_vec_ok(const void *a, const void *b, int M, int K, int N, ALayout a_layout, BLayout b_layout) {
     const bool aligned = aligned16(a) && aligned16(b);
-    return aligned && K % 4 == 0 && (layout == BLayout::nk || N % 4 == 0);
+    const bool a_runs = a_layout == ALayout::mk ? K % 4 == 0 : M % 4 == 0;
+    const bool b_runs = b_layout == BLayout::nk ? K % 4 == 0 : N % 4 == 0;
+    return aligned && a_runs && b_runs;
 }
 
-template <typename Shape, BLayout kB, typename Epi, GemmStore kStore, typename TB = float>
+template <typename Shape, BLayout kB, typename Epi, GemmStore kStore, typename TB = float,
+          ALayout kAL = ALayout::mk>
 void gemm_f32_launch_shape(const float *A, const TB *B, const float *bias, float *C, int M, int N, int K, Epi epi,
                            hipStream_t stream, int splits) {
     const int tiles = static_cast<int>(blocks_for64(M, Shape::BM) * blocks_for64(N, Shape::BN));
     const dim3 grid(tiles, splits);
-    if (gemm_vec_ok(A, B, K, N, kB))
-        launch_async(stream, gemm_f32_mfma_kernel<Shape, kB, true, Epi, kStore, TB>, grid, Shape::kThreads, A, B, bias,
-                     C, M, N, K, epi);
-    else
-        launch_async(stream, gemm_f32_mfma_kernel<Shape, kB, false, Epi, kStore, TB>, grid, Shape::kThreads, A, B,
+    if (gemm_vec_ok(A, B, M, K, N, kAL, kB))
+        launch_async(stream, gemm_f32_mfma_kernel<Shape, kB, true, Epi, kStore, TB, kAL>, grid, Shape::kThreads, A, B,
                      bias, C, M, N, K, epi);
+    else
+        launch_async(stream, gemm_f32_mfma_kernel<Shape, kB, false, Epi, kStore, TB, kAL>, grid, Shape::kThreads, A,
+                     B, bias, C, M, N, K, epi);
 }
 
 // Enqueues C[M][N] = epi(A[M][K] B + bias) (written per kStore). K == 0 writes epi(bias or 0).
 // GemmBig when K is not split and its tiles alone cover every CU, else GemmSmall.
-template <BLayout kB, typename Epi, GemmStore kStore = GemmStore::store, typename TB = float>
+template <BLayout kB, typename Epi, GemmStore kStore = GemmStore::store, typename TB = float,
+          ALayout kAL = ALayout::mk>
 void gemm_f32_launch(const float *A, const TB *B, const float *bias, float *C, int M, int N, int K, Epi epi,
                      hipStream_t stream, int splits = 1) {
     require(kStore != GemmStore::swiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
     const int64_t big_tiles = blocks_for64(M, GemmBig::BM) * blocks_for64(N, GemmBig::BN);
     if (splits == 1 && big_tiles >= 256)
-        gemm_f32_launch_shape<GemmBig, kB, Epi, kStore, TB>(A, B, bias, C, M, N, K, epi, stream, splits);
+        gemm_f32_launch_shape<GemmBig, kB, Epi, kStore, TB, kAL>(A, B, bias, C, M, N, K, epi, stream, splits);
     else
-        gemm_f32_launch_shape<GemmSmall, kB, Epi, kStore, TB>(A, B, bias, C, M, N, K, epi, stream, splits);
+        gemm_f32_launch_shape<GemmSmall, kB, Epi, kStore, TB, kAL>(A, B, bias, C, M, N, K, epi, stream, splits);
 }
 
 // Floats of split-K workspace any launch planned by splitk_factor(tiles, ., 512) needs.

@@ -12,16 +12,10 @@
 #include <limits>
 
 #include "../core/bf16.hpp"
+#include "../core/weight_pack.hpp"
 #include "elementwise.hpp"
 
 namespace opworks::detail {
-
-template <typename WT> __device__ __forceinline__ float widen(WT v) {
-    if constexpr (std::is_same_v<WT, bf16>)
-        return bf16_to_float(v.bits);
-    else
-        return v;
-}
 
 // vocab bounds the ids; an id outside [0, vocab) produces a NaN row instead
 // of reading outside the table.

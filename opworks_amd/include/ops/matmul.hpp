@@ -44,31 +44,55 @@ struct GeluEpilogue {
 };
 
 namespace detail_act {
-template <detail::BLayout kB>
+template <detail::BLayout kB, detail::ALayout kA>
 inline void gemm_act(const float *A, const float *B, const float *bias, float *C, int M, int N, int K,
                      Activation act, hipStream_t stream) {
+    using detail::GemmStore;
     switch (act) {
-    case Activation::none: detail::gemm_f32_launch<kB>(A, B, bias, C, M, N, K, PassThrough{}, stream); break;
-    case Activation::relu: detail::gemm_f32_launch<kB>(A, B, bias, C, M, N, K, ReluEpilogue{}, stream); break;
-    case Activation::gelu: detail::gemm_f32_launch<kB>(A, B, bias, C, M, N, K, GeluEpilogue{}, stream); break;
+    case Activation::none:
+        detail::gemm_f32_launch<kB, PassThrough, GemmStore::store, float, kA>(A, B, bias, C, M, N, K, PassThrough{},
+                                                                             stream);
+        break;
+    case Activation::relu:
+        detail::gemm_f32_launch<kB, ReluEpilogue, GemmStore::store, float, kA>(A, B, bias, C, M, N, K, ReluEpilogue{},
+                                                                              stream);
+        break;
+    case Activation::gelu:
+        detail::gemm_f32_launch<kB, GeluEpilogue, GemmStore::store, float, kA>(A, B, bias, C, M, N, K, GeluEpilogue{},
+                                                                              stream);
+        break;
     default: throw std::invalid_argument("unknown activation");
     }
 }
 } // namespace detail_act
 
-// C(M x K) = act(A(M x N) @ B + bias[K]); B is (N x K), or (K x N) when b_transposed.
+// C(M x K) = act(op(A) @ op(B) + bias[K]) with the reference's names: op(A) is
+// M x N, stored (N x M) when a_transposed; op(B) is N x K, stored (K x N) when
+// b_transposed. A transposed A is read by the GEMM in place (no copy).
 inline void mat_mul_fused(const float *A, const float *B, const float *bias, float *C, int M, int N, int K,
-                          bool b_transposed, Activation act, hipStream_t stream = nullptr) {
+                          bool a_transposed, bool b_transposed, Activation act, hipStream_t stream = nullptr) {
     detail::validate_matrix(M, N);
     detail::validate_matrix(N, K);
     detail::validate_matrix(M, K);
     if (M == 0 || K == 0)
         return;
     detail::require(C && (N == 0 || (A && B)), "matmul requires non-null pointers for nonempty tensors");
-    if (b_transposed)
-        detail_act::gemm_act<detail::BLayout::nk>(A, B, bias, C, M, K, N, act, stream);
+    using detail::ALayout;
+    using detail::BLayout;
+    if (a_transposed && b_transposed)
+        detail_act::gemm_act<BLayout::nk, ALayout::km>(A, B, bias, C, M, K, N, act, stream);
+    else if (a_transposed)
+        detail_act::gemm_act<BLayout::kn, ALayout::km>(A, B, bias, C, M, K, N, act, stream);
+    else if (b_transposed)
+        detail_act::gemm_act<BLayout::nk, ALayout::mk>(A, B, bias, C, M, K, N, act, stream);
     else
-        detail_act::gemm_act<detail::BLayout::kn>(A, B, bias, C, M, K, N, act, stream);
+        detail_act::gemm_act<BLayout::kn, ALayout::mk>(A, B, bias, C, M, K, N, act, stream);
+}
+
+// C(M x K) = act(A(M x N) @ B + bias[K]); B is (N x K), or (K x N) when b_transposed.
+inline void mat_mul_fused(const float *A, const float *B, const float *bias, float *C, int M, int N, int K,
+                          bool b_transposed, Activation act, hipStream_t stream = nullptr) {
+    mat_mul_fused(A, B, bias, C, M, N, K, false, b_transposed, act, stream);
 }
 
 } // namespace opworks::ops

@@ -131,6 +131,49 @@ class PackReader {
             throw std::runtime_error(path_ + ": failed reading tensor " + name);
     }
 
+    // Host-vector readers (interface of the reference's PackReader,
+    // include/runtime/pack_reader.cuh:109-160), all built on read_into.
+
+    // One tensor's bytes as stored.
+    std::vector<uint8_t> read_raw(const std::string &name) const {
+        std::vector<uint8_t> out(static_cast<size_t>(meta(name).numel) * elem_size_);
+        read_into(name, out.data(), out.size());
+        return out;
+    }
+
+    // A tensor of a float32 pack.
+    std::vector<float> read(const std::string &name) const {
+        if (dtype_ != "float32")
+            throw std::runtime_error(path_ + ": read() requires a float32 pack; use read_raw for " + dtype_);
+        std::vector<float> out(static_cast<size_t>(meta(name).numel));
+        read_into(name, out.data(), out.size() * sizeof(float));
+        return out;
+    }
+
+    // A tensor of a bfloat16 pack, each value widened exactly to fp32.
+    std::vector<float> read_bf16_as_float(const std::string &name) const {
+        if (dtype_ != "bfloat16")
+            throw std::runtime_error(path_ + ": read_bf16_as_float requires a bfloat16 pack");
+        std::vector<uint16_t> bits(static_cast<size_t>(meta(name).numel));
+        read_into(name, bits.data(), bits.size() * sizeof(uint16_t));
+        std::vector<float> out(bits.size());
+        for (size_t i = 0; i < bits.size(); ++i) {
+            const uint32_t word = static_cast<uint32_t>(bits[i]) << 16;
+            std::memcpy(&out[i], &word, sizeof(word));
+        }
+        return out;
+    }
+
+    // int32 values stored bit for bit in a float32 tensor (how fixture packs
+    // carry token ids; model packs hold no such tensor).
+    std::vector<int32_t> read_int32(const std::string &name) const {
+        if (dtype_ != "float32")
+            throw std::runtime_error(path_ + ": read_int32 requires a float32 pack");
+        std::vector<int32_t> out(static_cast<size_t>(meta(name).numel));
+        read_into(name, out.data(), out.size() * sizeof(int32_t));
+        return out;
+    }
+
   private:
     std::string path_, dtype_;
     size_t elem_size_ = 4;

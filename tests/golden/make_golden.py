@@ -64,6 +64,7 @@ def make_kats():
     hb = [float(i % 5 - 2) for i in range(35)]
     mm = [[2 * sum(ha[r * 5 + k] * hb[k * 7 + c] for k in range(5)) for c in range(7)] for r in range(3)]
     den = sum(math.exp(j - 4) for j in range(5))
+    bias = [-3.0, -2.0, -1.0, 0.0, 1.0, 2.0, 3.0]
     return {
         "source": "reference tests/unit/framework.cu",
         "add": {"a": [1, 2, 3], "b": [4, 5, 6], "out": [5, 7, 9], "line": "framework.cu:73-75"},
@@ -78,6 +79,13 @@ def make_kats():
                            "line": "framework.cu:196-199"},
         "mat_mul_3x5x7_scale2": {"a": ha, "b": hb, "M": 3, "N": 5, "K": 7, "out": [v for row in mm for v in row],
                                  "line": "framework.cu:201-218"},
+        "mat_mul_zero_inner": {"M": 3, "N": 0, "K": 7, "out": 0.0, "line": "framework.cu:219-221"},
+        "elementwise_boundaries": {"n": [1, 2, 3, 4, 5, 31, 32, 33, 255, 256, 257, 1025], "offsets": [0, 1],
+                                   "value": "i - 10", "add_same": 2.0, "scale_in_place": 3.0,
+                                   "line": "framework.cu:109-129"},
+        "builder_relu_bias": {"a": ha, "b": hb, "M": 3, "N": 5, "K": 7, "bias": bias,
+                              "out": [max(mm[r][c] / 2 + bias[c], 0.0) for r in range(3) for c in range(7)],
+                              "line": "addition: MatmulBuilder.run() on the framework.cu:201-218 operands"},
         "tolerance": {"rule": "|a - e| <= 1e-5 * (1 + |e|)", "line": "framework.cu:45-48"},
     }
 

@@ -34,6 +34,23 @@ def run_prefill(ow, orc, T, S, qh, kv_rep, D, cap, rows=None, data=None):
     if rows is not None:
         got = got[:, rows]
     check(got, ref, bound)
+    return got, bound
+
+
+def attention_f64(q, k, v, T, qh, kv_rep, D, rows):
+    """Causal GQA attention in float64 for the given query rows (T queries over T keys, scale 1/sqrt(D))."""
+    kvh = qh // kv_rep
+    q = q.reshape(qh, T, D).astype(np.float64)
+    k = k.reshape(kvh, T, D).astype(np.float64)
+    v = v.reshape(kvh, T, D).astype(np.float64)
+    out = np.empty((qh, len(rows), D))
+    for h in range(qh):
+        kh, vh = k[h // kv_rep], v[h // kv_rep]
+        for i, r in enumerate(rows):
+            s = kh[:r + 1] @ q[h, r] / np.sqrt(D)
+            p = np.exp(s - s.max())
+            out[h, i] = p @ vh[:r + 1] / p.sum()
+    return out
 
 
 @pytest.mark.parametrize("T,S,qh,kv_rep,D,cap", [
@@ -92,7 +109,14 @@ def test_config4_prefill_full_size_sampled(ow, orc):
     k = orc.fill_normal(kvh * T * D, SEED, 401, 0.0, 1.0, mt=True)
     v = orc.fill_normal(kvh * T * D, SEED, 402, 0.0, 1.0, mt=True)
     rows = np.concatenate([np.arange(0, 40), np.arange(T - 40, T), np.arange(40, T - 40, 97)]).astype(np.int32)
-    run_prefill(ow, orc, T, T, qh, qh // kvh, D, T, rows=rows, data=(q, k, v))
+    got, bound = run_prefill(ow, orc, T, T, qh, qh // kvh, D, T, rows=rows, data=(q, k, v))
+    # fp32 arithmetic, not a reduced-precision path: against float64 attention on the same inputs, every
+    # element within 2e-6 of its PV magnitude sum_key p |v| and NRMSE <= 2e-6. Scores rounded to
+    # tf32-class precision move p by ~1e-4 relative, bf16 by ~1e-3.
+    exact = attention_f64(q, k, v, T, qh, qh // kvh, D, rows)
+    check(got, exact, bound, tol=2e-6)
+    err = got.astype(np.float64) - exact
+    assert float(np.sqrt(np.mean(err ** 2)) / np.sqrt(np.mean(exact ** 2))) <= 2e-6
 
 
 @pytest.mark.parametrize("qh,kv_rep,D", [(8, 1, 32), (16, 16, 64), (6, 3, 48), (8, 8, 16), (12, 2, 64)])
@@ -133,3 +157,33 @@ def test_decode_matches_oracle(ow, orc, length, cap, use_ws):
     ref = orc.attention_decode(q, k, v, qh, kv_rep, D, length, cap)
     _, bound = orc.attention_explicit(q, k, v, 1, length, qh, kv_rep, D, cap)
     check(got, ref, bound[:, 0])
+
+
+@pytest.mark.parametrize("kv_rep", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("length", [1, 63, 64, 65, 1024, 8192])
+def test_decode_fused_merge_matches_two_kernels(ow, orc, kv_rep, length):
+    """The one-launch form (the last chunk workgroup of each kv head merges the head group's records,
+    read back with agent-coherent loads after an agent-scope counter) against the two-kernel form
+    (partials, then the combine kernel): the same merge arithmetic, so bit-identical outputs; both
+    against the oracle; counters back at zero afterwards, and a second call on the same counters
+    agrees again."""
+    qh, D, cap = 2 * kv_rep, 64, 8192
+    kvh = qh // kv_rep
+    q = orc.fill_normal(qh * D, SEED, 30 + kv_rep, 0.0, 1.0)
+    k = orc.fill_normal(kvh * cap * D, SEED, 31, 0.0, 1.0)
+    v = orc.fill_normal(kvh * cap * D, SEED, 32, 0.0, 1.0)
+    dq, dk, dv = upload(ow, q), upload(ow, k), upload(ow, v)
+    ws_n = ow.ops.attention_decode_workspace_size(qh, length, D)
+    ws = ow.DeviceBuffer.empty(ws_n)
+    counters = ow.DeviceBuffer.from_host(np.zeros(kvh, np.int32))
+    two = ow.DeviceBuffer.empty(qh * D)
+    ow.ops.attention_decode(dq, dk, dv, two, qh, kv_rep, D, length, cap, workspace=ws)
+    ref_bits = two.to_host().view(np.uint32).copy()
+    for _ in range(2):
+        fused = ow.DeviceBuffer.empty(qh * D)
+        ow.ops.attention_decode_fused(dq, dk, dv, fused, qh, kv_rep, D, length, cap, ws, ws_n, counters)
+        assert np.array_equal(fused.to_host().view(np.uint32), ref_bits)
+        assert np.array_equal(counters.to_host(), np.zeros(kvh, np.int32))
+    ref = orc.attention_decode(q, k, v, qh, kv_rep, D, length, cap)
+    _, bound = orc.attention_explicit(q, k, v, 1, length, qh, kv_rep, D, cap)
+    check(two.to_host().reshape(qh, D), ref, bound[:, 0])

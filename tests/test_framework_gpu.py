@@ -21,10 +21,14 @@ ADAPTERS = ROOT / "opworks_amd" / "lib" / "adapters"
 
 
 def test_framework_executable():
+    """The C++ operator API self-test, driven by the reference unit test's known answers
+    (tests/golden/framework_kats.json)."""
     exe = ROOT / "opworks_amd" / "lib" / "tests" / "framework"
     assert exe.exists(), "build the C++ tests first (python -m opworks_amd.build tests)"
-    print("[framework] running", exe, flush=True)
-    proc = subprocess.run([str(exe)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=90)
+    kats = ROOT / "tests" / "golden" / "framework_kats.json"
+    print("[framework] running", exe, kats, flush=True)
+    proc = subprocess.run([str(exe), str(kats)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                          timeout=90)
     print(proc.stdout)
     assert proc.returncode == 0, proc.stdout
     assert proc.stdout.startswith("PASS"), proc.stdout

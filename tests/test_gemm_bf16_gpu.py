@@ -88,3 +88,27 @@ def test_config3_bf16_full_size_sampled(ow, orc):
     ref, absdot = orc.mat_mul_rows(Ar, Wr, n, n, n, rows=rows, bias=bias, b_transposed=True, act="relu")
     got = Y.to_host().reshape(n, n)[rows]
     assert float((np.abs(got - ref) / (1e-4 * absdot + 1e-6)).max()) <= 1.0
+
+
+@pytest.mark.parametrize("rows,in_f,out_f", [(1, 2048, 2048), (1, 8192, 2048), (1, 2048, 513), (1, 100, 37),
+                                             (2, 2048, 512), (15, 2048, 3072), (16, 2048, 2048), (16, 100, 64),
+                                             (7, 4104, 33)])
+def test_linear_bf16_weights_keep_fp32_inputs(ow, orc, rows, in_f, out_f):
+    """ops::linear<bf16> (reference include/ops/linear.cuh:99-153): fp32 X against bf16 weights widened
+    exactly, fp32 accumulation, at every row count (the GEMV at rows == 1, the fp32 GEMM with a widened
+    B operand above). Bars: against the oracle on the widened weights, K-scaled 1e-4; against the float64
+    product of the fp32 inputs and the widened weights, 1e-6 * sum|x w| per element, which a path that
+    rounds X to bf16 (typically 3e-5 to 1e-4 of sum|x w| at these widths) cannot meet. in % 8 != 0 takes the scalar GEMV."""
+    X = orc.fill_normal(rows * in_f, SEED, 11, 0.0, 1.0)
+    W = orc.fill_normal(out_f * in_f, SEED, 12, 0.0, 0.02)
+    Wr, Wb = orc.round_bf16(W)
+    dX, dW = upload(ow, X), upload(ow, Wb, np.uint16)
+    Y = ow.DeviceBuffer.empty(rows * out_f)
+    ow.ops.linear_wbf16(dX, dW, Y, rows, in_f, out_f)
+    got = Y.to_host().reshape(rows, out_f).astype(np.float64)
+    ref, absdot = orc.mat_mul_rows(X, Wr, rows, in_f, out_f, b_transposed=True)
+    assert float(np.max(np.abs(got - ref) / (1e-4 * absdot + 1e-6))) <= 1.0
+    exact = X.reshape(rows, in_f).astype(np.float64) @ Wr.reshape(out_f, in_f).astype(np.float64).T
+    assert float(np.max(np.abs(got - exact) / (1e-6 * absdot + 1e-12))) <= 1.0
+    if rows == 1:  # the reference's GEMV (fp32 x, widened bf16 row) agrees too
+        assert float(np.max(np.abs(got[0] - orc.gemv(X, Wr, in_f, out_f)) / (1e-4 * absdot[0] + 1e-6))) <= 1.0

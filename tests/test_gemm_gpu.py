@@ -55,6 +55,26 @@ def test_fused_matmul_matches_oracle(ow, orc, M, N, K, b_t, act):
     check_kscaled(C.to_host().reshape(M, K), ref, absdot)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (3, 5, 7), (127, 33, 129), (130, 4, 260), (257, 1000, 515),
+                                   (2048, 64, 1024), (4096, 96, 4096), (6, 9, 11)])
+@pytest.mark.parametrize("b_t", [False, True])
+@pytest.mark.parametrize("act", ["none", "relu"])
+def test_fused_matmul_transposed_a(ow, orc, M, N, K, b_t, act):
+    """MatmulBuilder::transpose_a (reference include/builders/matmul.cuh:19-20,35): op(A) = A^T with A stored
+    N x M; the GEMM stages it in place. The oracle gets the transposed copy. M % 4 != 0 takes the scalar
+    staging path; 4096 x 4096 outputs take the 256 x 256 tiles."""
+    At = orc.fill_normal(N * M, SEED, 21, 0.0, 1.0)  # stored N x M
+    B = orc.fill_normal(N * K, SEED, 22, 0.0, 1.0)
+    bias = orc.fill_uniform(K, SEED, 23, -0.1, 0.1)
+    C = ow.DeviceBuffer.empty(M * K)
+    ow.ops.mat_mul_fused_ex(upload(ow, At), upload(ow, B), upload(ow, bias), C, M, N, K, True, b_t, activation=act)
+    A = np.ascontiguousarray(At.reshape(N, M).T).ravel()
+    rows = None if M <= 512 else np.arange(0, M, 61)
+    ref, absdot = orc.mat_mul_rows(A, B, M, N, K, rows=rows, bias=bias, b_transposed=b_t, act=act)
+    got = C.to_host().reshape(M, K)
+    check_kscaled(got if rows is None else got[rows], ref, absdot)
+
+
 @pytest.mark.parametrize("M,N,K", [(4100, 40, 4000), (4100, 37, 3999), (4096, 64, 4096)])
 @pytest.mark.parametrize("b_t", [False, True])
 def test_big_tile_path_every_element(ow, orc, M, N, K, b_t):
@@ -116,3 +136,11 @@ def test_config3_full_size_sampled(ow, orc):
     ref, absdot = orc.mat_mul_rows(A, B, M, N, K, rows=rows, bias=bias, act="relu")
     got = dC.to_host().reshape(M, K)[rows]
     check_kscaled(got, ref, absdot)
+    # fp32 arithmetic, not a reduced-precision path: against the float64 product, every element within
+    # 1e-6 * (sum_k |a b| + |bias|) and NRMSE <= 5e-6. fp32 accumulation over K = 4096 sits near 1e-7 of
+    # that sum; tf32-class inputs (10-bit mantissas) near 1e-5, bf16 inputs near 1e-4.
+    exact = np.maximum(A.reshape(M, N)[rows].astype(np.float64) @ B.reshape(N, K).astype(np.float64)
+                       + bias.astype(np.float64), 0.0)
+    check_kscaled(got, exact, absdot, tol=1e-6, floor=1e-12)
+    err = got.astype(np.float64) - exact
+    assert float(np.sqrt(np.mean(err ** 2)) / np.sqrt(np.mean(exact ** 2))) <= 5e-6

@@ -3,8 +3,9 @@ include/models/llama.cuh:190-199, 290-291; runtime/weights.cuh:16-94) against
 the oracle's bf16 model on the same seeded weights.
 
 Bar (north_star, bf16 path): final logits within NRMSE 1e-2 of the oracle at
-every step; in practice they agree to ~1e-4 (the GPU rounds prefill
-projection inputs to bf16 from 2 rows, the reference from 16). Greedy ids are
+every step; in practice they agree to ~1e-4 (prefill projection inputs are
+rounded to bf16 from 16 rows, as in the reference; shorter prompts keep fp32
+inputs against the widened weights). Greedy ids are
 compared like the fp32 path, with a near-tie margin of 1e-2 (the bf16 bar)."""
 import numpy as np
 import pytest

@@ -242,6 +242,29 @@ def test_ffi_edge_cases(tiny, ow):
     assert "null session" in lib().opw_llama_last_error().decode()
 
 
+def test_rejected_calls_leave_the_session_untouched(tiny, ow):
+    """Capacity and buffer checks of the added entry points run before any work: a rejected
+    generate_greedy leaves the session fresh, a rejected profile_decode_step leaves its length."""
+    import ctypes
+    from ctypes import POINTER, c_float, c_int32
+    from opworks_amd import lib
+    gpu, cpu = tiny
+    s = gpu.session(8)
+    with pytest.raises(ow.OpworksError, match="capacity"):
+        s.generate_greedy([1, 2, 3], 7)  # 3 + 7 - 1 > 8
+    ids = [1, 2, 3]
+    tok = s.prefill(ids)  # still fresh: prefill is accepted
+    cpu.reset(8)
+    assert tok == cpu.prefill(ids)[0]
+    small = np.zeros(3, np.float32)
+    err = ctypes.create_string_buffer(256)
+    rc = lib().opw_llama_profile_decode_step(s.handle, tok, small.ctypes.data_as(POINTER(c_float)), small.size,
+                                             err, 256)
+    assert rc == -1 and b"entries" in err.value
+    nxt = s.decode_step(tok)  # the rejected call did not advance the session
+    assert nxt == cpu.decode(tok)[0]
+
+
 def test_pack_load_matches_random_init(tiny, tmp_path, ow):
     from opworks_amd.llama import LlamaModel
     gpu, cpu = tiny
