@@ -72,6 +72,12 @@ int opw_reduction_workspace_size(int n);
 /* op: 0 = sum, 1 = max, 2 = product. workspace == NULL selects the
  * stream-ordered-allocation convenience overload. */
 int opw_reduce_f32(const float *in, float *out, int n, int op, float *workspace, int workspace_size, void *stream);
+/* The same reduction, allocating nothing: no counterpart in the reference. For callers that cannot
+ * allocate device memory (HIP graph capture, serving loops, harnesses that forbid hipMalloc). The
+ * partials live in a static 256 KiB device array of this library (one copy per GPU, kept until the
+ * process ends), so n <= 2^29 (536870912); larger n is rejected before any launch. All calls on one
+ * GPU share that array: calls that overlap on a GPU race. Results equal opw_reduce_f32's bit for bit. */
+int opw_reduce_f32_noalloc(const float *in, float *out, int n, int op, void *stream);
 
 /* ---- rows (reference: include/ops/softmax.cuh:36-43, layer_norm.cuh:38-47, rms_norm.cuh:31-40) ---- */
 int opw_softmax_f32(const float *in, float *out, int rows, int cols, void *stream);

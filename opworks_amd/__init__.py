@@ -62,6 +62,7 @@ _SIGNATURES = {
     "opw_map_scale_f32": (c_int, [c_void_p, c_void_p, c_int, c_float, c_void_p]),
     "opw_map_relu_f32": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
     "opw_reduction_workspace_size": (c_int, [c_int]),
+    "opw_reduce_f32_noalloc": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "opw_reduce_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_void_p]),
     "opw_softmax_f32": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "opw_layer_norm_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),
