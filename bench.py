@@ -38,7 +38,13 @@ METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
 
 
 def cpu_threads() -> int:
-    return max(1, min(16, os.cpu_count() or 1))
+    """Threads the CPU baseline uses: every CPU this process may run on, at most 16 (the GPU pool's CPU
+    share per GPU, whatever nproc reports there)."""
+    try:
+        available = len(os.sched_getaffinity(0))
+    except AttributeError:
+        available = os.cpu_count() or 1
+    return max(1, min(16, available))
 
 
 class Timer:
@@ -117,17 +123,19 @@ def roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) 
             "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "llama_decode_traffic.md"
+TRAFFIC_FILES = (ROOT / "profiles" / "llama_decode_traffic.md", ROOT / "profiles" / "stream_ops_traffic.md")
 
 
 def profiled_traffic(stage: str):
-    """HBM bytes per launch of a decode stage's kernel, as measured by the committed rocprofv3 --pmc
-    FETCH_SIZE / WRITE_SIZE passes (scaled by the copy-kernel calibration in that file), or None."""
-    if not TRAFFIC_FILE.exists():
-        return None
-    for line in TRAFFIC_FILE.read_text().splitlines():
-        if line.startswith(f"traffic_bytes_per_launch {stage}:"):
-            return int(line.split(":", 1)[1].strip())
+    """HBM bytes per launch of a kernel (a decode stage, or a streaming op's workload name), as measured by
+    the committed rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes (scaled by the copy-kernel calibration in
+    those files), or None."""
+    for path in TRAFFIC_FILES:
+        if not path.exists():
+            continue
+        for line in path.read_text().splitlines():
+            if line.startswith(f"traffic_bytes_per_launch {stage}:"):
+                return int(line.split(":", 1)[1].strip())
     return None
 
 
@@ -142,7 +150,8 @@ def wl_map(stream, steps, warmup):
     nbytes = 12 * n
     gbs = nbytes / ms / 1e6
     return {"workload": "map_scale_add_n2^28", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
-            "kernel": "map_pack_kernel", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+            "kernel": "map_pack_kernel",
+            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("map"))}
 
 
 def wl_reduce(stream, steps, warmup):
@@ -156,7 +165,8 @@ def wl_reduce(stream, steps, warmup):
     nbytes = 4 * n
     gbs = nbytes / ms / 1e6
     return {"workload": "reduce_sum_n2^28", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
-            "kernel": "reduce_partial_kernel+reduce_final_kernel", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+            "kernel": "reduce_partial_kernel+reduce_final_kernel",
+            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("reduce"))}
 
 
 def _rotating(rows, cols, sets, fill):
@@ -178,7 +188,8 @@ def wl_softmax(stream, steps, warmup):
     nbytes = 8 * rows * cols
     gbs = nbytes / ms / 1e6
     return {"workload": "softmax_4096x1024", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
-            "kernel": "softmax_rows_reg_kernel<1,4>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+            "kernel": "softmax_rows_reg_kernel<1,4>",
+            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("softmax"))}
 
 
 def wl_rmsnorm(stream, steps, warmup):
@@ -192,7 +203,8 @@ def wl_rmsnorm(stream, steps, warmup):
     nbytes = 8 * rows * cols + 4 * cols
     gbs = nbytes / ms / 1e6
     return {"workload": "rms_norm_8192x2048", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
-            "kernel": "rms_norm_reg_kernel<1,8>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+            "kernel": "rms_norm_reg_kernel<1,8>",
+            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("rmsnorm"))}
 
 
 def wl_layernorm(stream, steps, warmup):
@@ -208,7 +220,8 @@ def wl_layernorm(stream, steps, warmup):
     nbytes = 8 * rows * cols + 8 * cols
     gbs = nbytes / ms / 1e6
     return {"workload": "layer_norm_8192x2048", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
-            "kernel": "layer_norm_reg_kernel<1,8>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+            "kernel": "layer_norm_reg_kernel<1,8>",
+            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("layernorm"))}
 
 
 def wl_gemm(stream, steps, warmup):
@@ -310,6 +323,24 @@ def wl_llama(stream, steps, warmup, bf16=False, prompt_len=512, new_tokens=256, 
     dec = sorted(r[1] for r in runs)[len(runs) // 2]
     pre = sorted(r[0] for r in runs)[len(runs) // 2]
     tok_s = (new_tokens - 1) / (dec / 1e3)
+    # The reference's own method (scripts/llama/benchmark.py:53-68): reset, prefill, then one
+    # opw_llama_decode_step call per token from the host (a round trip and a synchronize each);
+    # median of the per-run decode rates. The ids must equal the chained generation's.
+    loop_rates = []
+    for i in range(2 + min(steps, 5)):
+        sess.reset()
+        tok = sess.prefill(prompt)
+        ids = [tok]
+        t0 = time.perf_counter()
+        for _ in range(new_tokens - 1):
+            tok = sess.decode_step(tok)
+            ids.append(tok)
+        t1 = time.perf_counter()
+        if ids != [int(t) for t in runs[-1][2]]:
+            raise RuntimeError("per-token decode_step loop and chained generation produced different ids")
+        if i >= 2:
+            loop_rates.append((new_tokens - 1) / (t1 - t0))
+    loop_tok_s = sorted(loop_rates)[len(loop_rates) // 2]
     # Each decode stage launched back to back over the 16 layers (HIP events on the session stream):
     # kernel time without launch gaps, comparable with rocprofv3's per-kernel average.
     H, I, V, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"], cfg["num_hidden_layers"]
@@ -335,6 +366,9 @@ def wl_llama(stream, steps, warmup, bf16=False, prompt_len=512, new_tokens=256, 
            "roofline": roofline(gu_gbs, HBM_PEAK_GBS, "GB/s", "hbm",
                                 traffic=None if bf16 else profiled_traffic("gate_up")),
            "decode_step_roofline": roofline(step_gbs, HBM_PEAK_GBS, "GB/s", "hbm"),
+           "decode_step_loop_tok_s": round(loop_tok_s, 2),
+           "decode_step_loop_method": "reference scripts/llama/benchmark.py:53-68: one opw_llama_decode_step "
+                                      "call per token from the host, median of the runs",
            "weight_bytes_per_token": weight_bytes, "kernels": breakdown,
            "first_tokens": [int(t) for t in runs[-1][2][:8]]}
     if published:  # the reference's own figure for this exact configuration (other hardware)
@@ -408,72 +442,63 @@ CPU_SAMPLES = ("map", "reduce", "softmax", "rmsnorm", "layernorm", "gemm", "gemm
                "transpose", "gather", "llama", "llama_bf16")
 
 
-def cpu_baseline(name: str) -> dict:
-    """Times the oracle on a bounded sample of the same workload on this host."""
+def host_cpu() -> dict:
+    """The host the CPU baseline runs on: model name, what the OS reports, what this run may use."""
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    return {"model": model, "nproc": os.cpu_count(), "affinity": affinity, "threads_used": cpu_threads(),
+            "thread_cap": "16 threads: the GPU pool's CPU share per GPU, whatever nproc reports"}
+
+
+def _rate(fn, budget_s: float, max_reps: int = 1 << 30):
+    """Repeats fn for about budget_s of wall time; returns (reps, seconds per call)."""
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        if time.perf_counter() - t0 > budget_s or reps >= max_reps:
+            return reps, (time.perf_counter() - t0) / reps
+
+
+def _cpu_work(name: str):
+    """(fn, units per call, unit, sample description, budget s) for the oracle on a bounded sample of a workload."""
     from tests import oracle as orc
 
-    threads = cpu_threads()
-    orc.set_threads(threads)
     if name == "map":
         n = 1 << 26
         a = orc.fill_uniform(n, SEED, 0, -1, 1, mt=True)
         b = orc.fill_uniform(n, SEED, 1, -1, 1, mt=True)
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            orc.map_scale_add(a, b, 2.5, mt=True)
-            reps += 1
-            if time.perf_counter() - t0 > 10.0 or reps >= 200:
-                break
-        dt = (time.perf_counter() - t0) / reps
-        return {"value": round(12 * n / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-                "sample": f"oracle orc_map_scale_add_mt over n=2^26 (768 MiB), {reps} reps, ~10 s"}
+        return (lambda: orc.map_scale_add(a, b, 2.5, mt=True), 12 * n / 1e9, "GB/s",
+                "oracle orc_map_scale_add over n=2^26 (768 MiB)", 5.0)
     if name == "reduce":
         n = 1 << 24
         x = orc.fill_uniform(n, SEED, 2, -1, 1, mt=True)
-        reps, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < 3.0:
-            orc.reduce(x, "sum")
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        return {"value": round(4 * n / dt / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"oracle orc_reduce (reference order, single thread) over n=2^24, {reps} reps"}
+        return (lambda: orc.reduce(x, "sum"), 4 * n / 1e9, "GB/s",
+                "oracle orc_reduce (the reference's block order; blocks split across threads) over n=2^24", 3.0)
     if name == "softmax":
         rows, cols = 1024, 1024
         x = orc.fill_normal(rows * cols, SEED, 100, 0, 4, mt=True)
-        reps, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < 3.0:
-            orc.softmax_rows(x, rows, cols)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        return {"value": round(8 * rows * cols / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-                "sample": f"oracle orc_softmax_rows, 1024 of the 4096 rows, {reps} reps"}
-    if name == "rmsnorm":
+        return (lambda: orc.softmax_rows(x, rows, cols), 8 * rows * cols / 1e9, "GB/s",
+                "oracle orc_softmax_rows, 1024 of the 4096 rows", 3.0)
+    if name in ("rmsnorm", "layernorm"):
         rows, cols = 2048, 2048
         x = orc.fill_normal(rows * cols, SEED, 200, 0, 1, mt=True)
-        w = orc.fill_uniform(cols, SEED, 210, 0.5, 1.5)
-        reps, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < 3.0:
-            orc.rms_norm_rows(x, w, rows, cols, 1e-5)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        return {"value": round(8 * rows * cols / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-                "sample": f"oracle orc_rms_norm_rows, 2048 of the 8192 rows, {reps} reps"}
-    def timed(fn, budget_s=3.0):
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            fn()
-            reps += 1
-            if time.perf_counter() - t0 > budget_s:
-                return reps, (time.perf_counter() - t0) / reps
-
-    if name == "layernorm":
-        rows, cols = 2048, 2048
-        x = orc.fill_normal(rows * cols, SEED, 220, 0, 1, mt=True)
-        g = orc.fill_uniform(cols, SEED, 230, 0.5, 1.5)
-        b = orc.fill_uniform(cols, SEED, 231, -0.1, 0.1)
-        reps, dt = timed(lambda: orc.layer_norm_rows(x, g, b, rows, cols, 1e-5))
-        return {"value": round(8 * rows * cols / dt / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-                "sample": f"oracle orc_layer_norm_rows, 2048 of the 8192 rows, {reps} reps"}
+        g = orc.fill_uniform(cols, SEED, 210, 0.5, 1.5)
+        bt = orc.fill_uniform(cols, SEED, 231, -0.1, 0.1)
+        fn = ((lambda: orc.rms_norm_rows(x, g, rows, cols, 1e-5)) if name == "rmsnorm"
+              else (lambda: orc.layer_norm_rows(x, g, bt, rows, cols, 1e-5)))
+        return (fn, 8 * rows * cols / 1e9, "GB/s", f"oracle orc_{'rms' if name == 'rmsnorm' else 'layer'}_norm_rows, "
+                "2048 of the 8192 rows", 3.0)
     if name in ("gemm", "gemm_bf16"):
         n, sample = 4096, np.arange(0, 4096, 64)
         A = orc.fill_normal(n * n, SEED, 300, 0.0, 1.0 / 64, mt=True)
@@ -481,10 +506,10 @@ def cpu_baseline(name: str) -> dict:
         bias = orc.fill_uniform(n, SEED, 302, -0.1, 0.1)
         if name == "gemm_bf16":  # the reference's CPU check of the bf16 path: fp32 math on rounded inputs
             A, B = orc.round_bf16(A)[0], orc.round_bf16(B)[0]
-        reps, dt = timed(lambda: orc.mat_mul_rows(A, B, n, n, n, rows=sample, bias=bias, act="relu"))
-        return {"value": round(2.0 * len(sample) * n * n / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-                "kind": "port", "sample": f"oracle orc_mat_mul_rows (fp32, plus its float64 |a·b| bound), "
-                                          f"{len(sample)} of the 4096 rows of relu(A·B+bias), {reps} reps"}
+        return (lambda: orc.mat_mul_rows(A, B, n, n, n, rows=sample, bias=bias, act="relu"),
+                2.0 * len(sample) * n * n / 1e12, "TFLOP/s",
+                f"oracle orc_mat_mul_rows (fp32, plus its float64 |a·b| bound), {len(sample)} of the 4096 rows of "
+                "relu(A·B+bias)", 3.0)
     if name == "attention":
         T, qh, kvh, D = 2048, 32, 8, 64
         q = orc.fill_normal(qh * T * D, SEED, 400, 0.0, 1.0, mt=True)
@@ -492,61 +517,91 @@ def cpu_baseline(name: str) -> dict:
         v = orc.fill_normal(kvh * T * D, SEED, 402, 0.0, 1.0, mt=True)
         rows = np.arange(0, T, 128)
         flop = 4.0 * qh * D * float(np.sum(rows + 1))  # unmasked QK^T + PV of the sampled causal rows
-        reps, dt = timed(lambda: orc.attention_explicit(q, k, v, T, T, qh, 4, D, T, rows=rows))
-        return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-                "sample": f"oracle orc_attention_explicit, {len(rows)} of the 2048 causal query rows of "
-                          f"every head (unmasked flops), {reps} reps"}
+        return (lambda: orc.attention_explicit(q, k, v, T, T, qh, 4, D, T, rows=rows), flop / 1e12, "TFLOP/s",
+                f"oracle orc_attention_explicit, {len(rows)} of the 2048 causal query rows of every head "
+                "(unmasked flops)", 3.0)
     if name == "attention_decode":
         qh, kvh, D, L = 32, 8, 64, 2048
         q = orc.fill_normal(qh * D, SEED, 410, 0.0, 1.0)
         k = orc.fill_normal(kvh * L * D, SEED, 411, 0.0, 1.0, mt=True)
         v = orc.fill_normal(kvh * L * D, SEED, 412, 0.0, 1.0, mt=True)
-        reps, dt = timed(lambda: orc.attention_decode(q, k, v, qh, 4, D, L, L))
-        return {"value": round((2 * kvh * L * D * 4 + 2 * qh * D * 4) / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
-                "kind": "port", "sample": f"oracle orc_attention_decode, the full config (len 2048), {reps} reps"}
+        return (lambda: orc.attention_decode(q, k, v, qh, 4, D, L, L), (2 * kvh * L * D * 4 + 2 * qh * D * 4) / 1e9,
+                "GB/s", "oracle orc_attention_decode (q heads split across threads), the full config (len 2048)", 3.0)
     if name == "scan":
         n = 1 << 24
         x = orc.fill_uniform(n, SEED, 500, -1.0, 1.0, mt=True)
-        reps, dt = timed(lambda: orc.scan(x))
-        return {"value": round(8 * n / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"oracle orc_scan (inclusive sum, with its float64 |x| prefix) over n=2^24, {reps} reps"}
+        return (lambda: orc.scan(x), 8 * n / 1e9, "GB/s",
+                "oracle orc_scan (inclusive sum in index order, with its float64 |x| prefix: sequential by "
+                "definition, so one thread at any count) over n=2^24", 3.0)
     if name == "transpose":
         r = c = 4096
         x = orc.fill_uniform(r * c, SEED, 510, -1.0, 1.0, mt=True)
-        reps, dt = timed(lambda: orc.transpose(x, r, c))
-        return {"value": round(8 * r * c / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"oracle orc_transpose of 4096x4096 (a quarter of the 8192x8192 config), {reps} reps"}
+        return (lambda: orc.transpose(x, r, c), 8 * r * c / 1e9, "GB/s",
+                "oracle orc_transpose of 4096x4096 (a quarter of the 8192x8192 config)", 3.0)
     if name == "gather":
         n = 1 << 24
         x = orc.fill_uniform(n, SEED, 520, -1.0, 1.0, mt=True)
         idx = np.random.default_rng(SEED).permutation(n).astype(np.int32)
-        reps, dt = timed(lambda: orc.gather(x, idx))
-        return {"value": round(12 * n / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"oracle orc_gather through a random permutation of 2^24, {reps} reps"}
-    if name in ("llama", "llama_bf16"):
-        from opworks_amd.llama import LLAMA_3_2_1B
-        cfg = dict(LLAMA_3_2_1B, torch_dtype="bfloat16") if name == "llama_bf16" else dict(LLAMA_3_2_1B)
-        t_build = time.perf_counter()
-        model = orc.Llama(cfg, SEED, 0.02, "ones")  # the same seeded weights as the GPU model
-        build_s = time.perf_counter() - t_build
-        rng = np.random.default_rng(SEED)
-        prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], 512)][:16]
+        return (lambda: orc.gather(x, idx), 12 * n / 1e9, "GB/s",
+                "oracle orc_gather through a random permutation of 2^24", 3.0)
+    return None
+
+
+def _cpu_llama(name: str, threads: int) -> dict:
+    """The oracle's Llama forward on the same seeded weights: all-threads and single-thread greedy decode."""
+    from tests import oracle as orc
+    from opworks_amd.llama import LLAMA_3_2_1B
+    cfg = dict(LLAMA_3_2_1B, torch_dtype="bfloat16") if name == "llama_bf16" else dict(LLAMA_3_2_1B)
+    orc.set_threads(threads)
+    t_build = time.perf_counter()
+    model = orc.Llama(cfg, SEED, 0.02, "ones")
+    build_s = time.perf_counter() - t_build
+    prompt = [int(v) for v in np.random.default_rng(SEED).integers(0, cfg["vocab_size"], 512)]
+    out = {}
+    for label, nthreads, plen, budget, cap in (("all", threads, 16, 15.0, 64), ("one", 1, 2, 8.0, 16)):
+        orc.set_threads(nthreads)
         model.reset(1024)
-        tok, _ = model.prefill(prompt)
+        tok, _ = model.prefill(prompt[:plen])
         steps, t0 = 0, time.perf_counter()
         while True:
             tok, _ = model.decode(tok)
             steps += 1
-            if time.perf_counter() - t0 > 15.0 or steps >= 64:
+            if time.perf_counter() - t0 > budget or steps >= cap:
                 break
-        dt = (time.perf_counter() - t0) / steps
-        del model
-        kind = "bf16-weight" if name == "llama_bf16" else "fp32"
-        return {"value": round(1.0 / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-                "sample": f"oracle {kind} Llama forward (orc_llama_*), same seeded weights: 16-token prompt "
-                          f"(first 16 of the 512 ids), then {steps} greedy decode steps timed "
-                          f"(~15 s; weight generation {build_s:.1f} s untimed)"}
-    return {}
+        out[label] = (round(steps / (time.perf_counter() - t0), 3), steps, plen)
+    del model
+    orc.set_threads(threads)
+    kind = "bf16-weight" if name == "llama_bf16" else "fp32"
+    return {"value": out["all"][0], "unit": "tok/s", "cores": threads, "kind": "port",
+            "single_thread": {"value": out["one"][0], "cores": 1},
+            "sample": f"oracle {kind} Llama forward (orc_llama_*), same seeded weights; all threads: "
+                      f"{out['all'][2]}-token prompt then {out['all'][1]} greedy decode steps timed (~15 s); one "
+                      f"thread: {out['one'][2]}-token prompt then {out['one'][1]} steps (~8 s); weight generation "
+                      f"{build_s:.1f} s untimed",
+            "host": host_cpu()}
+
+
+def cpu_baseline(name: str) -> dict:
+    """Times the oracle on a bounded sample of the same workload on this host, with every thread this
+    run may use and with one thread."""
+    from tests import oracle as orc
+
+    threads = cpu_threads()
+    if name in ("llama", "llama_bf16"):
+        return _cpu_llama(name, threads)
+    orc.set_threads(threads)
+    work = _cpu_work(name)
+    if work is None:
+        return {}
+    fn, units, unit, sample, budget = work
+    reps, dt = _rate(fn, budget)
+    orc.set_threads(1)
+    reps1, dt1 = _rate(fn, budget / 2)
+    orc.set_threads(threads)
+    digits = 6 if unit == "TFLOP/s" else 3
+    return {"value": round(units / dt, digits), "unit": unit, "cores": threads, "kind": "port",
+            "single_thread": {"value": round(units / dt1, digits), "cores": 1},
+            "sample": f"{sample}; {reps} reps on {threads} threads, {reps1} on one", "host": host_cpu()}
 
 
 def main() -> int:
@@ -591,6 +646,8 @@ def main() -> int:
         "data": "synthetic (counter-based seeded generator, seed 1234, resident in HBM)",
         "config": {"workload": head["workload"], "device": ow.device_name()},
         "roofline": head["roofline"],
+        # the whole decode step against the weight-streaming bound (weights + KV cache bytes per token)
+        "decode_step_roofline": head.get("decode_step_roofline"),
         "cpu_baseline": None if args.no_cpu else cpu_baseline(headline),
         "components": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                        for k, v in results.items()},

@@ -113,7 +113,7 @@ struct LlamaSession : detail::SessionHandles {
     static WorkspaceSizes workspace_sizes(const ModelConfig &cfg, int max_seq_len) {
         WorkspaceSizes ws;
         ws.attn_chunks = static_cast<int>(detail::blocks_for64(max_seq_len, detail::kAttnChunk));
-        ws.lm_records = static_cast<int>(detail::blocks_for64(cfg.vocab_size, llama::kRows * llama::kWavesPerBlock));
+        ws.lm_records = static_cast<int>(detail::blocks_for64(cfg.vocab_size, llama::kLmRows * llama::kWavesPerBlock));
         ws.splitk_floats = std::max(detail::kSplitKWorkspaceF32, detail::kSplitKWorkspaceBf16);
         ws.state_ints = sizeof(llama::StepState) / sizeof(int32_t);
         return ws;

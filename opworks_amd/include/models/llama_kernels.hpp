@@ -45,7 +45,8 @@ struct StepState {
     int32_t chain; // nonzero: the argmax kernel also records `next` in gen[pos] and advances to it
 };
 
-constexpr int kRows = 4;       // rows per LM-head wave; rows per workgroup of the other GEMVs
+constexpr int kRows = 4;       // rows per workgroup of the o_proj / down GEMVs
+constexpr int kLmRows = 1;     // rows per LM-head wave
 constexpr int kBlock = 256;    // threads per GEMV workgroup
 constexpr int kWavesPerBlock = kBlock / kWaveSize;
 
@@ -397,18 +398,18 @@ __global__ __launch_bounds__(kBlock) void lm_head_kernel(LmHeadArgs<WT> a) {
     __shared__ float sv[kWavesPerBlock];
     __shared__ int si[kWavesPerBlock];
     const int lane = threadIdx.x % kWaveSize, wave = threadIdx.x / kWaveSize;
-    const int r0 = (blockIdx.x * kWavesPerBlock + wave) * kRows;
-    int row[kRows];
+    const int r0 = (blockIdx.x * kWavesPerBlock + wave) * kLmRows;
+    int row[kLmRows];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r)
+    for (int r = 0; r < kLmRows; ++r)
         row[r] = r0 + r < a.vocab ? r0 + r : 0;
-    float y[kRows];
-    block_gemv<kV, kRows, WT>(a.hidden_row, a.gamma, a.eps, a.embed, row, r0 < a.vocab, nullptr, y);
+    float y[kLmRows];
+    block_gemv<kV, kLmRows, WT>(a.hidden_row, a.gamma, a.eps, a.embed, row, r0 < a.vocab, nullptr, y);
     float bv = kNegInf;
     int bi = 0x7fffffff;
     if (r0 < a.vocab) {
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) {
+        for (int r = 0; r < kLmRows; ++r) {
             if (r0 + r < a.vocab) {
                 if (lane == 0)
                     a.logits[r0 + r] = y[r];

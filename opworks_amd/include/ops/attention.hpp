@@ -447,7 +447,7 @@ __device__ __forceinline__ void decode_combine_head(const DecodeAttnArgs &a, int
         }
     }
     if (lane < D)
-        a.out[int64_t(h) * D + lane] = L > 0.f ? acc / L : 0.f;
+        record_store<kCoherent>(a.out + int64_t(h) * D + lane, L > 0.f ? acc / L : 0.f);
 }
 
 __device__ __forceinline__ int decode_len(const DecodeAttnArgs &a) {
@@ -456,14 +456,16 @@ __device__ __forceinline__ int decode_len(const DecodeAttnArgs &a) {
     return len < a.max_chunks * kAttnChunk ? len : a.max_chunks * kAttnChunk;
 }
 
+// One (kv head, chunk) workgroup of the decode attention. Returns true in the
+// workgroup that merged its kv head's records (fused form only; the merged
+// outputs were written with agent-coherent stores and have completed).
 template <int kWaves>
-__global__ __launch_bounds__(kWaves *kWaveSize) void attention_decode_partial_kernel(DecodeAttnArgs a) {
+__device__ __forceinline__ bool decode_attention_chunk(const DecodeAttnArgs &a, int kvh, int chunk) {
     constexpr int C = kAttnChunk;
     const int len = decode_len(a);
     const int nchunks = (len + C - 1) / C;
-    const int kvh = blockIdx.x, chunk = blockIdx.y;
     if (chunk >= nchunks)
-        return;
+        return false;
     const int k0 = chunk * C;
     const int n = len - k0 < C ? len - k0 : C;
     const int D = a.D;
@@ -549,7 +551,7 @@ __global__ __launch_bounds__(kWaves *kWaveSize) void attention_decode_partial_ke
         }
     }
     if (!a.counters)
-        return;
+        return false;
     // Fused merge: count in once this workgroup's records are complete; the last one merges.
     __shared__ int last;
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); // the record stores have completed
@@ -559,11 +561,19 @@ __global__ __launch_bounds__(kWaves *kWaveSize) void attention_decode_partial_ke
                nchunks - 1;
     __syncthreads();
     if (!last)
-        return;
+        return false;
     if (head_ok)
         decode_combine_head<true>(a, h, nchunks, lane);
     if (threadIdx.x == 0)
         __hip_atomic_store(a.counters + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); // the merged outputs have completed
+    __syncthreads();
+    return true;
+}
+
+template <int kWaves>
+__global__ __launch_bounds__(kWaves *kWaveSize) void attention_decode_partial_kernel(DecodeAttnArgs a) {
+    decode_attention_chunk<kWaves>(a, blockIdx.x, blockIdx.y);
 }
 
 // grid kvh, block kv_rep waves; wave w merges q head kvh * kv_rep + w.

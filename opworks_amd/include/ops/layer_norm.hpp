@@ -11,7 +11,10 @@ namespace opworks::detail {
 
 // Rows of up to 8 packs per lane are held to 64 registers, so 8 waves fit per SIMD: at 8192
 // rows of 2048 (one wave each) the whole grid is then resident at once; at 67 registers the
-// last 1024 rows waited for a second round (26.5 against ~22 us).
+// last 1024 rows waited for a second round (26.5 against ~22 us). One-wave rows stage gamma
+// and beta in LDS once per workgroup, so the output loop does not hold every gamma/beta pack
+// in registers at once (which had spilled 5 registers to scratch at that limit, +16% HBM
+// traffic), and the workgroup's rows share one read of them.
 template <int kW, int kV, bool kExact>
 __global__ __launch_bounds__(RowShape<kW>::kBlock) __attribute__((amdgpu_waves_per_eu(kV <= 8 ? 8 : 1)))
 void layer_norm_reg_kernel(
@@ -30,6 +33,16 @@ void layer_norm_reg_kernel(
             local += (x[k][0] + x[k][1]) + (x[k][2] + x[k][3]);
         }
     }
+    const f32x4 *g4 = reinterpret_cast<const f32x4 *>(gamma);
+    const f32x4 *b4 = reinterpret_cast<const f32x4 *>(beta);
+    constexpr bool kStaged = kW == 1;
+    __shared__ f32x4 gs[kStaged ? kV * kWaveSize : 1], bs[kStaged ? kV * kWaveSize : 1];
+    if constexpr (kStaged) {
+        for (int i = threadIdx.x; i < n4; i += RowShape<kW>::kBlock) {
+            gs[i] = g4[i];
+            bs[i] = b4[i];
+        }
+    }
     const float mean = row_combine<kW>(wave::sum(local), p, wave::Add{}) / cols;
     local = 0.f;
 #pragma unroll
@@ -44,20 +57,22 @@ void layer_norm_reg_kernel(
         }
     }
     const float rstd = rsqrtf(row_combine<kW>(wave::sum(local), p, wave::Add{}) / cols + eps);
-    const f32x4 *g4 = reinterpret_cast<const f32x4 *>(gamma);
-    const f32x4 *b4 = reinterpret_cast<const f32x4 *>(beta);
+    if constexpr (kStaged)
+        __syncthreads();
     f32x4 *dst = reinterpret_cast<f32x4 *>(out + p.row * cols);
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
         const int q = pack_index<kW>(p, k);
         if (p.active && (kExact || q < n4)) {
-            const f32x4 g = g4[q], b = b4[q];
+            const f32x4 g = kStaged ? gs[q] : g4[q], b = kStaged ? bs[q] : b4[q];
             f32x4 r;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 r[j] = fmaf((x[k][j] - mean) * rstd, g[j], b[j]);
             __builtin_nontemporal_store(r, dst + q);
         }
+        if constexpr (!kStaged)
+            __builtin_amdgcn_sched_barrier(0); // keep each pack's gamma/beta loads beside their use
     }
 }
 

@@ -181,6 +181,17 @@ static float partial_block(const float *in, int64_t n, int block, int grid, int 
     return orc_block_reduce(acc, REF_THREADS, op);
 }
 
+struct reduce_ctx {
+    const float *in;
+    float *partial;
+    int n, blocks, op;
+};
+static void reduce_blocks_range(void *p, int64_t b0, int64_t b1) {
+    struct reduce_ctx *c = (struct reduce_ctx *)p;
+    for (int64_t b = b0; b < b1; ++b)
+        c->partial[b] = partial_block(c->in, c->n, (int)b, c->blocks, c->op);
+}
+
 /* ops::reduce (include/ops/reduction.cuh:34-54): blocks = min(ceil(n/256), 1024);
  * one block writes the result directly; otherwise partials, then
  * reduce_final_kernel (:19-27) with one block of 256 threads. */
@@ -191,8 +202,8 @@ float orc_reduce(const float *in, int n, int op) {
     if (blocks > REF_MAX_PARTIALS)
         blocks = REF_MAX_PARTIALS;
     float *partial = (float *)malloc(sizeof(float) * blocks);
-    for (int b = 0; b < blocks; ++b)
-        partial[b] = partial_block(in, n, b, blocks, op);
+    struct reduce_ctx c = {in, partial, n, blocks, op};
+    parallel_for(blocks, reduce_blocks_range, &c); /* blocks are independent: any thread count, same partials */
     const float r = partial_block(partial, blocks, 0, 1, op);
     free(partial);
     return r;
@@ -510,17 +521,24 @@ void orc_attention_explicit(const float *q, const float *k, const float *v, floa
  * fmaf(e_j * inv, v_j[d], acc[d]) over keys j = t, t+256, ..., then a 32-lane
  * shuffle tree per d and a serial sum over the 8 warps. scale = rsqrtf(D),
  * restated as 1/sqrtf(D) (exact for D = 64). */
-void orc_attention_decode(const float *q, const float *k, const float *v, float *out, int qh, int kv_rep, int D,
-                          int len, int max_seq) {
+struct decode_ctx {
+    const float *q, *k, *v;
+    float *out;
+    int kv_rep, D, len, max_seq;
+};
+/* Heads are independent: q heads [h0, h1) with their own scratch. */
+static void decode_heads_range(void *p, int64_t h0, int64_t h1) {
+    const struct decode_ctx *c = (const struct decode_ctx *)p;
+    const int D = c->D, len = c->len, max_seq = c->max_seq;
     float *scores = (float *)malloc(sizeof(float) * (size_t)len);
     float *acc = (float *)malloc(sizeof(float) * REF_THREADS * (size_t)D);
     float part[REF_THREADS];
     const float scale = 1.0f / sqrtf((float)D);
-    for (int h = 0; h < qh; ++h) {
-        const int kvh = h / kv_rep;
-        const float *kh = k + (int64_t)kvh * max_seq * D;
-        const float *vh = v + (int64_t)kvh * max_seq * D;
-        const float *qv = q + (int64_t)h * D;
+    for (int h = (int)h0; h < (int)h1; ++h) {
+        const int kvh = h / c->kv_rep;
+        const float *kh = c->k + (int64_t)kvh * max_seq * D;
+        const float *vh = c->v + (int64_t)kvh * max_seq * D;
+        const float *qv = c->q + (int64_t)h * D;
         for (int j = 0; j < len; ++j) {
             float dot = 0.f;
             for (int d = 0; d < D; ++d)
@@ -562,11 +580,17 @@ void orc_attention_decode(const float *q, const float *k, const float *v, float 
                     lanes[l] = acc[(int64_t)(w * REF_WARP + l) * D + d];
                 total += warp_tree(lanes, 0);
             }
-            out[(int64_t)h * D + d] = total;
+            c->out[(int64_t)h * D + d] = total;
         }
     }
     free(scores);
     free(acc);
+}
+
+void orc_attention_decode(const float *q, const float *k, const float *v, float *out, int qh, int kv_rep, int D,
+                          int len, int max_seq) {
+    struct decode_ctx c = {q, k, v, out, kv_rep, D, len, max_seq};
+    parallel_for(qh, decode_heads_range, &c);
 }
 
 /* ------------------------------------------------------------ llama forward */
@@ -912,15 +936,36 @@ void orc_scan(const float *in, float *out, double *abs_prefix, int64_t n, int op
     }
 }
 
+struct transpose_ctx {
+    const float *in;
+    float *out;
+    int rows, cols;
+};
+static void transpose_range(void *p, int64_t r0, int64_t r1) {
+    const struct transpose_ctx *t = (const struct transpose_ctx *)p;
+    for (int64_t r = r0; r < r1; ++r)
+        for (int c = 0; c < t->cols; ++c)
+            t->out[(int64_t)c * t->rows + r] = t->in[r * t->cols + c];
+}
 void orc_transpose(const float *in, float *out, int rows, int cols) {
-    for (int r = 0; r < rows; ++r)
-        for (int c = 0; c < cols; ++c)
-            out[(int64_t)c * rows + r] = in[(int64_t)r * cols + c];
+    struct transpose_ctx t = {in, out, rows, cols};
+    parallel_for(rows, transpose_range, &t);
 }
 
+struct gather_ctx {
+    const float *in;
+    int64_t in_size;
+    const int *idx;
+    float *out;
+};
+static void gather_range(void *p, int64_t i0, int64_t i1) {
+    const struct gather_ctx *g = (const struct gather_ctx *)p;
+    for (int64_t i = i0; i < i1; ++i)
+        g->out[i] = (g->idx[i] >= 0 && g->idx[i] < g->in_size) ? g->in[g->idx[i]] : NAN;
+}
 void orc_gather(const float *in, int64_t in_size, const int *idx, float *out, int64_t count) {
-    for (int64_t i = 0; i < count; ++i)
-        out[i] = (idx[i] >= 0 && idx[i] < in_size) ? in[idx[i]] : NAN;
+    struct gather_ctx g = {in, in_size, idx, out};
+    parallel_for(count, gather_range, &g);
 }
 
 void orc_scatter(const float *in, const int *idx, float *out, int64_t out_size, int64_t count) {

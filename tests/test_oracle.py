@@ -328,3 +328,23 @@ def test_gather_scatter_oracle(orc):
     assert gb[0] == x[0] and gb[2] == x[999] and np.isnan(gb[[1, 3, 4]]).all()
     sb = orc.scatter(np.array([5, 6, 7], np.float32), np.array([1, -3, 1], np.int32), np.zeros(4, np.float32))
     assert np.array_equal(sb, np.array([0, 7, 0, 0], np.float32))  # in-order: the last duplicate wins
+
+
+def test_threaded_oracle_functions_match_single_thread(orc):
+    """reduce (independent partial blocks), decode attention (independent heads), transpose and gather
+    split their work across threads for the CPU baseline; the results must not depend on the count."""
+    x = orc.fill_normal(300_001, 91, 0, 0.0, 1.0)
+    q = orc.fill_normal(8 * 64, 91, 1, 0.0, 1.0)
+    k = orc.fill_normal(2 * 700 * 64, 91, 2, 0.0, 1.0)
+    v = orc.fill_normal(2 * 700 * 64, 91, 3, 0.0, 1.0)
+    idx = np.random.default_rng(91).permutation(x.size).astype(np.int32)
+    results = []
+    for threads in (1, 5):
+        orc.set_threads(threads)
+        results.append((np.float32(orc.reduce(x, "sum")).view(np.uint32),
+                        orc.attention_decode(q, k, v, 8, 4, 64, 650, 700).view(np.uint32),
+                        orc.transpose(x[:299 * 1003], 299, 1003).view(np.uint32),
+                        orc.gather(x, idx).view(np.uint32)))
+    orc.set_threads(1)
+    for a, b in zip(*results):
+        assert np.array_equal(a, b)
