@@ -291,13 +291,21 @@ def wl_attention_decode(stream, steps, warmup):
         ow.fill_normal(v, SEED, 412 + 2 * i, 0.0, 1.0, stream=stream)
         ks.append(k)
         vs.append(v)
-    ws = ow.DeviceBuffer.empty(ow.ops.attention_decode_workspace_size(qh, L, D))
-    ms = Timer(stream).run(lambda i: ow.ops.attention_decode(q, ks[i % sets], vs[i % sets], out, qh, 4, D, L, L,
-                                                             workspace=ws, stream=stream), steps, warmup)
+    ws_n = ow.ops.attention_decode_workspace_size(qh, L, D)
+    ws = ow.DeviceBuffer.empty(ws_n)
+    counters = ow.DeviceBuffer.from_host(np.zeros(ow.ops.attention_decode_counters_size(qh, 4), np.int32))
+    # the single-launch form (the last chunk workgroup of each kv head merges), as the decode step runs it
+    ms = Timer(stream).run(lambda i: ow.ops.attention_decode_fused(q, ks[i % sets], vs[i % sets], out, qh, 4, D, L,
+                                                                   L, ws, ws_n, counters, stream=stream),
+                           steps, warmup)
+    # the two-launch workspace form (partial kernel, then the combine kernel)
+    ms_two = Timer(stream).run(lambda i: ow.ops.attention_decode(q, ks[i % sets], vs[i % sets], out, qh, 4, D, L,
+                                                                 L, workspace=ws, stream=stream), steps, warmup)
     nbytes = 2 * kvh * L * D * 4 + 2 * qh * D * 4
     gbs = nbytes / ms / 1e6
     return {"workload": "attention_decode_32q8kv_d64_len2048", "unit": "GB/s", "value": gbs, "ms": ms,
-            "bytes": nbytes, "kernel": "attention_decode_partial_kernel+combine",
+            "bytes": nbytes, "kernel": "attention_decode_partial_kernel (fused merge)",
+            "two_launch_ms": ms_two, "two_launch_kernels": "attention_decode_partial_kernel+combine",
             "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
 
 

@@ -138,11 +138,14 @@ int opw_attention_decode_ws_f32(const float *q, const float *kcache, const float
                                 int num_q_heads, int kv_rep, int head_dim, int len, int max_seq, float *workspace,
                                 int workspace_size, void *stream);
 /* ... in one launch, as the Llama decode step runs it: the last chunk workgroup of each kv head merges
- * the head group's records. `counters` holds num_q_heads / kv_rep ints, zero before the call and zero
- * again after it; calls sharing counters must not overlap. Same results as opw_attention_decode_ws_f32. */
+ * the head group's records. `counters` holds counters_size >= opw_attention_decode_counters_size() ints
+ * (one 256-byte line per kv head), zero before the call and zero again after it; calls sharing counters
+ * must not overlap. Same results as opw_attention_decode_ws_f32. No reference counterpart: the
+ * reference's decode attention is one workgroup per q head with no cross-workgroup merge. */
+int opw_attention_decode_counters_size(int num_q_heads, int kv_rep);
 int opw_attention_decode_fused_f32(const float *q, const float *kcache, const float *vcache, float *out,
                                    int num_q_heads, int kv_rep, int head_dim, int len, int max_seq, float *workspace,
-                                   int workspace_size, int *counters, void *stream);
+                                   int workspace_size, int *counters, int counters_size, void *stream);
 
 /* ---- decoder-block steps (reference: include/ops/add.cuh:18-25, swiglu.cuh:19-26,
  *      causal_scale.cuh:24-33, embedding.cuh:24-34, split_heads.cuh:39-66, rope.cuh:34-46,

@@ -82,8 +82,9 @@ _SIGNATURES = {
     "opw_attention_decode_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                          c_void_p]),
     "opw_attention_decode_workspace_size": (c_int, [c_int, c_int, c_int]),
+    "opw_attention_decode_counters_size": (c_int, [c_int, c_int]),
     "opw_attention_decode_fused_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
-                                               c_int, c_void_p, c_int, c_void_p, c_void_p]),
+                                               c_int, c_void_p, c_int, c_void_p, c_int, c_void_p]),
     "opw_attention_decode_ws_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                             c_void_p, c_int, c_void_p]),
     "opw_add_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
@@ -392,14 +393,19 @@ class _Ops:
                                                     length, max_seq, _p(workspace), workspace_size,
                                                     _stream(stream)))
 
-    # One launch: the last chunk workgroup of each kv head merges; counters (int32, one per kv head)
-    # are zero before and after the call.
+    # One launch: the last chunk workgroup of each kv head merges; counters (int32,
+    # attention_decode_counters_size of them) are zero before and after the call.
     def attention_decode_fused(self, q: Ptr, k: Ptr, v: Ptr, out: Ptr, num_q_heads: int, kv_rep: int,
                                head_dim: int, length: int, max_seq: int, workspace: Ptr, workspace_size: int,
-                               counters: Ptr, stream=None) -> None:
+                               counters: Ptr, counters_size: int = 0, stream=None) -> None:
+        if isinstance(counters, DeviceView) and counters_size == 0:
+            counters_size = counters.n
         check(lib().opw_attention_decode_fused_f32(_p(q), _p(k), _p(v), _p(out), num_q_heads, kv_rep, head_dim,
                                                    length, max_seq, _p(workspace), workspace_size, _p(counters),
-                                                   _stream(stream)))
+                                                   counters_size, _stream(stream)))
+
+    def attention_decode_counters_size(self, num_q_heads: int, kv_rep: int) -> int:
+        return check(lib().opw_attention_decode_counters_size(num_q_heads, kv_rep))
 
     def attention_decode_workspace_size(self, num_q_heads: int, max_len: int, head_dim: int) -> int:
         return check(lib().opw_attention_decode_workspace_size(num_q_heads, max_len, head_dim))

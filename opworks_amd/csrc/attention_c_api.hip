@@ -45,10 +45,16 @@ int opw_attention_decode_ws_f32(const float *q, const float *kcache, const float
     });
 }
 
+int opw_attention_decode_counters_size(int num_q_heads, int kv_rep) {
+    return guard([&] { return opworks::ops::attention_decode_counters_size(num_q_heads, kv_rep); });
+}
+
 int opw_attention_decode_fused_f32(const float *q, const float *kcache, const float *vcache, float *out,
                                    int num_q_heads, int kv_rep, int head_dim, int len, int max_seq, float *workspace,
-                                   int workspace_size, int *counters, void *stream) {
+                                   int workspace_size, int *counters, int counters_size, void *stream) {
     return guard([&] {
+        opworks::detail::require(counters_size >= opworks::ops::attention_decode_counters_size(num_q_heads, kv_rep),
+                                 "attention_decode_fused: counters are too small");
         opworks::ops::attention_decode_fused(q, kcache, vcache, out, num_q_heads, kv_rep, head_dim, len, max_seq,
                                              workspace, workspace_size, counters, static_cast<hipStream_t>(stream));
         return 0;

@@ -116,6 +116,7 @@ struct LlamaSession : detail::SessionHandles {
         ws.lm_records = static_cast<int>(detail::blocks_for64(cfg.vocab_size, llama::kLmRows * llama::kWavesPerBlock));
         ws.splitk_floats = std::max(detail::kSplitKWorkspaceF32, detail::kSplitKWorkspaceBf16);
         ws.state_ints = sizeof(llama::StepState) / sizeof(int32_t);
+        ws.attn_counter_ints = cfg.num_kv_heads * detail::kAttnCounterStride;
         return ws;
     }
 

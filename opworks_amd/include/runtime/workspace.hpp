@@ -23,6 +23,7 @@ struct WorkspaceSizes {
     int lm_records = 0;        // LM-head workgroups (one argmax record each)
     int64_t splitk_floats = 0; // split-K partial tiles of the prefill GEMMs
     int state_ints = 0;        // device step state
+    int attn_counter_ints = 0; // decode attention arrival counters (one cache line per kv head)
 };
 
 struct Workspace {
@@ -42,7 +43,7 @@ struct Workspace {
     TypedDeviceBuffer<float> step_attn;     // [qh D] attention output
     TypedDeviceBuffer<float> step_act;      // [I] silu(gate) * up
     TypedDeviceBuffer<float> attn_partial;  // [qh][chunks][D + 2] chunk records
-    TypedDeviceBuffer<int32_t> attn_counters; // [kvh] arrivals, zero between launches
+    TypedDeviceBuffer<int32_t> attn_counters; // per-kv-head arrivals, zero between launches
     TypedDeviceBuffer<float> logits;        // [V] last row's logits
     TypedDeviceBuffer<float> lm_best_val;   // [records]
     TypedDeviceBuffer<int32_t> lm_best_idx; // [records]
@@ -69,7 +70,7 @@ struct Workspace {
         step_attn = TypedDeviceBuffer<float>(qw);
         step_act = TypedDeviceBuffer<float>(I);
         attn_partial = TypedDeviceBuffer<float>(int64_t(cfg.num_q_heads) * s.attn_chunks * (D + 2));
-        attn_counters = TypedDeviceBuffer<int32_t>(cfg.num_kv_heads);
+        attn_counters = TypedDeviceBuffer<int32_t>(s.attn_counter_ints);
         logits = TypedDeviceBuffer<float>(cfg.vocab_size);
         lm_best_val = TypedDeviceBuffer<float>(s.lm_records);
         lm_best_idx = TypedDeviceBuffer<int32_t>(s.lm_records);

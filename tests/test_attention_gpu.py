@@ -175,7 +175,9 @@ def test_decode_fused_merge_matches_two_kernels(ow, orc, kv_rep, length):
     dq, dk, dv = upload(ow, q), upload(ow, k), upload(ow, v)
     ws_n = ow.ops.attention_decode_workspace_size(qh, length, D)
     ws = ow.DeviceBuffer.empty(ws_n)
-    counters = ow.DeviceBuffer.from_host(np.zeros(kvh, np.int32))
+    n_counters = ow.ops.attention_decode_counters_size(qh, kv_rep)
+    assert n_counters >= kvh
+    counters = ow.DeviceBuffer.from_host(np.zeros(n_counters, np.int32))
     two = ow.DeviceBuffer.empty(qh * D)
     ow.ops.attention_decode(dq, dk, dv, two, qh, kv_rep, D, length, cap, workspace=ws)
     ref_bits = two.to_host().view(np.uint32).copy()
@@ -183,7 +185,7 @@ def test_decode_fused_merge_matches_two_kernels(ow, orc, kv_rep, length):
         fused = ow.DeviceBuffer.empty(qh * D)
         ow.ops.attention_decode_fused(dq, dk, dv, fused, qh, kv_rep, D, length, cap, ws, ws_n, counters)
         assert np.array_equal(fused.to_host().view(np.uint32), ref_bits)
-        assert np.array_equal(counters.to_host(), np.zeros(kvh, np.int32))
+        assert np.array_equal(counters.to_host(), np.zeros(n_counters, np.int32))
     ref = orc.attention_decode(q, k, v, qh, kv_rep, D, length, cap)
     _, bound = orc.attention_explicit(q, k, v, 1, length, qh, kv_rep, D, cap)
     check(two.to_host().reshape(qh, D), ref, bound[:, 0])
