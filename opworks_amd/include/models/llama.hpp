@@ -162,6 +162,7 @@ class LlamaRuntime {
 // include/models/llama.cuh:78-291; LlamaModel = fp32, LlamaModelBF16 = bf16).
 template <typename WT> class LlamaModelT final : public LlamaRuntime {
     static constexpr bool kBf16 = std::is_same_v<WT, bf16>;
+    static constexpr int kRowScale = llama::kRowScale<WT>;
 
   public:
     using Session = LlamaSession;
@@ -505,7 +506,8 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         }
         if (stage_on(3)) {
             tick();
-            launch_async(st, llama::swiglu_gemv_kernel<kV, WT>, detail::blocks_for64(2 * I, llama::kWavesPerBlock),
+            launch_async(st, llama::swiglu_gemv_kernel<kV, WT>,
+                         detail::blocks_for64(2 * I, llama::kWavesPerBlock * kRowScale),
                          llama::kBlock, s.workspace.step_hidden.data(), lw.post_norm.data(), cfg_.rms_norm_eps, lw.gate_up_proj.data(),
                          s.workspace.step_act.data(), I);
         }
@@ -541,9 +543,11 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         la.eps = cfg_.rms_norm_eps;
         la.vocab = cfg_.vocab_size;
         tick();
-        launch_async(s.stream, llama::lm_head_kernel<kV, WT>, s.workspace.sizes.lm_records, llama::kBlock, la);
+        const int records = static_cast<int>(
+            detail::blocks_for64(cfg_.vocab_size, llama::kLmRows * kRowScale * llama::kWavesPerBlock));
+        launch_async(s.stream, llama::lm_head_kernel<kV, WT>, records, llama::kBlock, la);
         launch_async(s.stream, llama::argmax_records_kernel, 1, 1024, s.workspace.lm_best_val.data(), s.workspace.lm_best_idx.data(),
-                     s.workspace.sizes.lm_records, s.state(), s.workspace.gen.data());
+                     records, s.state(), s.workspace.gen.data());
     }
 
     // Calls f(IntTag<H / 256>, IntTag<I / 1024>); bf16 rows need whole 8-weight

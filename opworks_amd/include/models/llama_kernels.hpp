@@ -45,8 +45,8 @@ struct StepState {
     int32_t chain; // nonzero: the argmax kernel also records `next` in gen[pos] and advances to it
 };
 
-constexpr int kRows = 4;       // rows per workgroup of the o_proj / down GEMVs
-constexpr int kLmRows = 1;     // rows per LM-head wave
+constexpr int kRows = 4;       // rows per workgroup of the o_proj / down GEMVs (fp32 weights)
+constexpr int kLmRows = 1;     // rows per LM-head wave (fp32 weights): sizes the argmax records
 constexpr int kBlock = 256;    // threads per GEMV workgroup
 constexpr int kWavesPerBlock = kBlock / kWaveSize;
 
@@ -56,6 +56,15 @@ using detail::load_wpack;
 using detail::u32x4;
 using detail::widen;
 using detail::WPack;
+
+// Rows per wave of the two long GEMVs (gate/up, LM head) relative to fp32: a bf16 row is half
+// the bytes of an fp32 row, so with bf16 weights a wave takes two rows and streams as many
+// bytes as an fp32 wave, and the per-workgroup costs (staging and normalising the input
+// vector, the reductions, the stores) are spread over twice the bytes (bf16 LM head 88.4 ->
+// 80.5 us, gate/up 12.8 -> 12.4 us). The short matrices (qkv, o_proj, down: 2048-3072 rows)
+// keep one row's share per wave: halving their workgroup count leaves CUs idle (qkv 5.26 ->
+// 5.37 us, o_proj 3.90 -> 4.00 us when doubled).
+template <typename WT> constexpr int kRowScale = std::is_same_v<WT, bf16> ? 2 : 1;
 
 // GEMV of a 4-wave workgroup: each wave owns kR rows of a [*, H] matrix,
 // H = 256 * kV. The input vector is staged once per workgroup: its loads are
@@ -152,14 +161,14 @@ __device__ __forceinline__ void block_gemv(const float *__restrict__ x, const fl
 // sums go through LDS, combined in the fixed order (w0 + w1) + (w2 + w3).
 // Serves short matrices (o_proj), where it measured faster than one row per
 // wave.
-template <int kV, typename WT = float>
+template <int kV, int kR, typename WT = float>
 __device__ __forceinline__ void block_gemv_split(const float *__restrict__ x, const WT *__restrict__ W,
-                                                 const int (&row)[kRows], float (&y)[kRows]) {
+                                                 const int (&row)[kR], float (&y)[kR]) {
     constexpr int H = 256 * kV;
     constexpr int E = WPack<WT>::kElems;
     constexpr int kX = H / (kBlock * E); // weight packs per thread
     static_assert(kX * kBlock * E == H, "the split GEMV needs H to be a multiple of 256 weight packs");
-    __shared__ float part[kWavesPerBlock][kRows];
+    __shared__ float part[kWavesPerBlock][kR];
     const int tid = threadIdx.x, lane = tid % kWaveSize, wave = tid / kWaveSize;
     const f32x4 *x4 = reinterpret_cast<const f32x4 *>(x);
     f32x4 xv[kX][E / 4];
@@ -168,15 +177,15 @@ __device__ __forceinline__ void block_gemv_split(const float *__restrict__ x, co
 #pragma unroll
         for (int q = 0; q < E / 4; ++q)
             xv[i][q] = x4[(E / 4) * (tid + kBlock * i) + q];
-    typename WPack<WT>::type w[kRows][kX];
+    typename WPack<WT>::type w[kR][kX];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r)
+    for (int r = 0; r < kR; ++r)
 #pragma unroll
         for (int i = 0; i < kX; ++i)
             w[r][i] = load_wpack(W + int64_t(row[r]) * H, tid + kBlock * i);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
+    for (int r = 0; r < kR; ++r) {
         float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < kX; ++i)
@@ -187,7 +196,7 @@ __device__ __forceinline__ void block_gemv_split(const float *__restrict__ x, co
     }
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < kRows; ++r)
+    for (int r = 0; r < kR; ++r)
         y[r] = (part[0][r] + part[1][r]) + (part[2][r] + part[3][r]);
 }
 
@@ -274,18 +283,19 @@ template <int kV, typename WT>
 __global__ __launch_bounds__(kBlock) void gemv_residual_kernel(const WT *__restrict__ W,
                                                                const float *__restrict__ x, float *__restrict__ hidden,
                                                                int out) {
-    if constexpr (kV % WPack<WT>::kElems == 0) { // 4 rows per workgroup, columns split across the waves
-        const int r0 = blockIdx.x * kRows;
-        int row[kRows];
+    if constexpr (kV % WPack<WT>::kElems == 0) { // kRows rows per workgroup, columns split across the waves
+        constexpr int kR = kRows;
+        const int r0 = blockIdx.x * kR;
+        int row[kR];
 #pragma unroll
-        for (int r = 0; r < kRows; ++r)
+        for (int r = 0; r < kR; ++r)
             row[r] = r0 + r < out ? r0 + r : r0;
-        float y[kRows];
-        block_gemv_split<kV, WT>(x, W, row, y);
-        if (threadIdx.x < kRows && r0 + threadIdx.x < out) {
+        float y[kR];
+        block_gemv_split<kV, kR, WT>(x, W, row, y);
+        if (threadIdx.x < kR && r0 + threadIdx.x < out) {
             float v = y[0];
 #pragma unroll
-            for (int r = 1; r < kRows; ++r)
+            for (int r = 1; r < kR; ++r)
                 v = threadIdx.x == r ? y[r] : v;
             hidden[r0 + threadIdx.x] += v;
         }
@@ -301,14 +311,25 @@ __global__ __launch_bounds__(kBlock) void gemv_residual_kernel(const WT *__restr
 }
 
 // ---- 4. act = silu(gate) * up, interleaved [gate_i; up_i] rows ----------------
-// Workgroup b computes pairs 2b and 2b + 1, one row per wave (rows 4b .. 4b+3).
+// fp32: workgroup b computes pairs 2b and 2b + 1, one row per wave (rows 4b .. 4b+3).
+// bf16 (two rows per wave): wave w of workgroup b computes both rows of pair 4b + w.
 template <int kV, typename WT>
 __global__ __launch_bounds__(kBlock) void swiglu_gemv_kernel(const float *__restrict__ hidden,
                                                              const float *__restrict__ gamma, float eps,
                                                              const WT *__restrict__ wgu, float *__restrict__ act,
                                                              int inter) {
-    __shared__ float res[kWavesPerBlock];
     const int wave = threadIdx.x / kWaveSize;
+    if constexpr (kRowScale<WT> == 2) {
+        const int i = blockIdx.x * kWavesPerBlock + wave;
+        const bool active = i < inter;
+        const int row[2] = {active ? 2 * i : 0, active ? 2 * i + 1 : 1};
+        float y[2];
+        block_gemv<kV, 2, WT>(hidden, gamma, eps, wgu, row, active, nullptr, y);
+        if (active && threadIdx.x % kWaveSize == 0)
+            act[i] = y[0] / (1.f + expf(-y[0])) * y[1];
+        return;
+    }
+    __shared__ float res[kWavesPerBlock];
     const int r = blockIdx.x * kWavesPerBlock + wave;
     const bool active = r < 2 * inter;
     const int row[1] = {active ? r : 0};
@@ -333,10 +354,11 @@ __global__ __launch_bounds__(kBlock) void down_residual_kernel(const WT *__restr
     constexpr int Kw = I / kWavesPerBlock; // columns per wave
     constexpr int E = WPack<WT>::kElems;
     constexpr int kP = Kw / (kWaveSize * E); // weight packs per lane per row
+    constexpr int kR = kRows;
     static_assert(kP * kWaveSize * E == Kw, "intermediate size must split into 64-lane weight packs");
-    __shared__ float part[kWavesPerBlock][kRows];
+    __shared__ float part[kWavesPerBlock][kR];
     const int lane = threadIdx.x % kWaveSize, wave = threadIdx.x / kWaveSize;
-    const int r0 = blockIdx.x * kRows;
+    const int r0 = blockIdx.x * kR;
     const int c0 = wave * Kw;
     f32x4 xv[kP][E / 4];
     const f32x4 *a4 = reinterpret_cast<const f32x4 *>(act + c0);
@@ -345,9 +367,9 @@ __global__ __launch_bounds__(kBlock) void down_residual_kernel(const WT *__restr
 #pragma unroll
         for (int q = 0; q < E / 4; ++q)
             xv[u][q] = a4[(E / 4) * (lane + kWaveSize * u) + q];
-    typename WPack<WT>::type wv[kRows][kP];
+    typename WPack<WT>::type wv[kR][kP];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
+    for (int r = 0; r < kR; ++r) {
         const int row = r0 + r < out ? r0 + r : r0;
 #pragma unroll
         for (int u = 0; u < kP; ++u)
@@ -355,7 +377,7 @@ __global__ __launch_bounds__(kBlock) void down_residual_kernel(const WT *__restr
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
+    for (int r = 0; r < kR; ++r) {
         float acc = 0.f;
 #pragma unroll
         for (int u = 0; u < kP; ++u)
@@ -365,7 +387,7 @@ __global__ __launch_bounds__(kBlock) void down_residual_kernel(const WT *__restr
             part[wave][r] = acc;
     }
     __syncthreads();
-    if (threadIdx.x < kRows && r0 + threadIdx.x < out) {
+    if (threadIdx.x < kR && r0 + threadIdx.x < out) {
         float t = 0.f;
 #pragma unroll
         for (int k = 0; k < kWavesPerBlock; ++k)
@@ -398,18 +420,19 @@ __global__ __launch_bounds__(kBlock) void lm_head_kernel(LmHeadArgs<WT> a) {
     __shared__ float sv[kWavesPerBlock];
     __shared__ int si[kWavesPerBlock];
     const int lane = threadIdx.x % kWaveSize, wave = threadIdx.x / kWaveSize;
-    const int r0 = (blockIdx.x * kWavesPerBlock + wave) * kLmRows;
-    int row[kLmRows];
+    constexpr int kLR = kLmRows * kRowScale<WT>;
+    const int r0 = (blockIdx.x * kWavesPerBlock + wave) * kLR;
+    int row[kLR];
 #pragma unroll
-    for (int r = 0; r < kLmRows; ++r)
+    for (int r = 0; r < kLR; ++r)
         row[r] = r0 + r < a.vocab ? r0 + r : 0;
-    float y[kLmRows];
-    block_gemv<kV, kLmRows, WT>(a.hidden_row, a.gamma, a.eps, a.embed, row, r0 < a.vocab, nullptr, y);
+    float y[kLR];
+    block_gemv<kV, kLR, WT>(a.hidden_row, a.gamma, a.eps, a.embed, row, r0 < a.vocab, nullptr, y);
     float bv = kNegInf;
     int bi = 0x7fffffff;
     if (r0 < a.vocab) {
 #pragma unroll
-        for (int r = 0; r < kLmRows; ++r) {
+        for (int r = 0; r < kLR; ++r) {
             if (r0 + r < a.vocab) {
                 if (lane == 0)
                     a.logits[r0 + r] = y[r];
