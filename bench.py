@@ -589,6 +589,9 @@ def _cpu_llama(name: str, threads: int) -> dict:
             "host": host_cpu()}
 
 
+SERIAL_ORACLE = ("scan",)  # oracle functions that do not split over threads
+
+
 def cpu_baseline(name: str) -> dict:
     """Times the oracle on a bounded sample of the same workload on this host, with every thread this
     run may use and with one thread."""
@@ -602,11 +605,15 @@ def cpu_baseline(name: str) -> dict:
     if work is None:
         return {}
     fn, units, unit, sample, budget = work
+    digits = 6 if unit == "TFLOP/s" else 3
+    if name in SERIAL_ORACLE:  # one thread whatever set_threads says: report it as such
+        reps, dt = _rate(fn, budget)
+        return {"value": round(units / dt, digits), "unit": unit, "cores": 1, "kind": "port",
+                "sample": f"{sample}; {reps} reps, single-threaded oracle function", "host": host_cpu()}
     reps, dt = _rate(fn, budget)
     orc.set_threads(1)
     reps1, dt1 = _rate(fn, budget / 2)
     orc.set_threads(threads)
-    digits = 6 if unit == "TFLOP/s" else 3
     return {"value": round(units / dt, digits), "unit": unit, "cores": threads, "kind": "port",
             "single_thread": {"value": round(units / dt1, digits), "cores": 1},
             "sample": f"{sample}; {reps} reps on {threads} threads, {reps1} on one", "host": host_cpu()}
