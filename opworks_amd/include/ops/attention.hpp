@@ -461,9 +461,198 @@ __device__ __forceinline__ int decode_len(const DecodeAttnArgs &a) {
     return len < a.max_chunks * kAttnChunk ? len : a.max_chunks * kAttnChunk;
 }
 
-// One (kv head, chunk) workgroup of the decode attention. Returns true in the
-// workgroup that merged its kv head's records (fused form only; the merged
-// outputs were written with agent-coherent stores and have completed).
+// Fused form, after a chunk workgroup has issued its records: count in once they are
+// complete; the last workgroup of the kv head merges the head group's records into the
+// output, then resets the counter. Returns true in that workgroup (its merged outputs,
+// written with agent-coherent stores, have completed).
+__device__ __forceinline__ bool decode_count_in_and_merge(const DecodeAttnArgs &a, int kvh, int nchunks, int h,
+                                                          bool head_ok, int lane) {
+    __shared__ int last;
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); // the record stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(a.counters + kvh * kAttnCounterStride, 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == nchunks - 1;
+    __syncthreads();
+    if (!last)
+        return false;
+    if (head_ok)
+        decode_combine_head<true>(a, h, nchunks, lane);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(a.counters + kvh * kAttnCounterStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); // the merged outputs have completed
+    __syncthreads();
+    return true;
+}
+
+// A chunk's record (m, l, acc[D]) of q head h: agent-coherent stores in the fused form.
+__device__ __forceinline__ float *decode_record(const DecodeAttnArgs &a, int h, int chunk) {
+    return a.partial + (int64_t(h) * a.max_chunks + chunk) * (a.D + 2);
+}
+
+// Register-blocked (kv head, chunk) workgroup for kWaves <= 8 waves (kv_rep <= 8 q heads).
+// Thread t holds key slots i < kPer = 16 / kWaves: key t/16 + (kWaves * 4) * i, head-dim
+// pack dq = t % 16 of it (the row padded to 16 packs; packs >= D/4 and keys >= n are zero),
+// loaded straight from HBM into registers with the q packs of every head of the group, so
+// K and V never pass through LDS and no wave re-reads the chunk:
+//  * scores: the thread's kPer x kWaves partial dot products (always 16) are summed over
+//    the 16 lanes of its row by a DPP reduce-scatter (row_ror 8, row_half_mirror, quad_perm
+//    ^2, ^1: each step keeps half the values and adds the partner lane's other half), after
+//    which lane dq of the row holds value dq, i.e. head dq % kWaves of slot dq / kWaves;
+//  * softmax: wave h reads head h's 64 scores from LDS (lane = key);
+//  * P V: each thread accumulates its slots' V packs for every head (kWaves packs of 4),
+//    reduce-scatters them over the wave's four rows with v_permlane32_swap then
+//    v_permlane16_swap, and the waves' partial outputs are summed through LDS.
+// About 10 KB of LDS traffic per workgroup, against the 128 KB of the one-head-per-wave
+// form. Same record layout and merge as decode_attention_chunk.
+template <int kWaves>
+__device__ __forceinline__ bool decode_attention_chunk_rb(const DecodeAttnArgs &a, int kvh, int chunk) {
+    static_assert(kWaves >= 1 && kWaves <= 8 && (kWaves & (kWaves - 1)) == 0, "1, 2, 4 or 8 waves");
+    constexpr int C = kAttnChunk;
+    constexpr int T = kWaves * kWaveSize;
+    constexpr int kRowStep = T / 16;          // keys between a thread's slots
+    constexpr int kPer = 16 / kWaves;         // key slots per thread
+    constexpr int kOut = 4 * kWaves;          // P V values per thread: kWaves heads x 4 dims
+    constexpr int kOStride = kOut + 4;        // floats per dq column of a wave's partial outputs (kOut used)
+    static_assert(kPer * kWaves == 16, "16 partial scores per thread");
+    const int len = decode_len(a);
+    const int nchunks = (len + C - 1) / C;
+    if (chunk >= nchunks)
+        return false;
+    const int k0 = chunk * C;
+    const int n = len - k0 < C ? len - k0 : C;
+    const int D = a.D, P = D / 4, rep = a.kv_rep;
+    const int t = threadIdx.x, wave = t / kWaveSize, lane = t % kWaveSize;
+    const int dq = t % 16, row = t / 16, row4 = lane / 16;
+    const bool dq_ok = dq < P;
+    const f32x4 *kh = reinterpret_cast<const f32x4 *>(a.kcache + (int64_t(kvh) * a.cap + k0) * D);
+    const f32x4 *vh = reinterpret_cast<const f32x4 *>(a.vcache + (int64_t(kvh) * a.cap + k0) * D);
+    const f32x4 *q4 = reinterpret_cast<const f32x4 *>(a.q + int64_t(kvh) * rep * D);
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    f32x4 kv[kPer], vv[kPer], qv[kWaves];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int key = row + kRowStep * i;
+        const bool ok = dq_ok && key < n;
+        kv[i] = ok ? kh[key * P + dq] : zero;
+        vv[i] = ok ? vh[key * P + dq] : zero;
+    }
+#pragma unroll
+    for (int h = 0; h < kWaves; ++h)
+        qv[h] = dq_ok && h < rep ? q4[h * P + dq] : zero;
+    __shared__ float Ss[kWaves][C];                        // scaled scores, [head][key]
+    __shared__ __attribute__((aligned(16))) float Ps[C][kWaves]; // probabilities, [key][head]
+    __shared__ __attribute__((aligned(16))) float Os[kWaves][16 * kOStride]; // per-wave P V partials
+    // scores: 16 partial dot products, then the row reduce-scatter
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+#pragma unroll
+        for (int h = 0; h < kWaves; ++h) {
+            const f32x4 x = kv[i] * qv[h];
+            v[i * kWaves + h] = (x[0] + x[1]) + (x[2] + x[3]);
+        }
+    {
+        const bool b3 = dq & 8, b2 = dq & 4, b1 = dq & 2, b0 = dq & 1;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float keep = b3 ? v[k + 8] : v[k], send = b3 ? v[k] : v[k + 8];
+            v[k] = keep + wave::dpp<0x128>(send, send); // row_ror:8, lane ^ 8
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float keep = b2 ? v[k + 4] : v[k], send = b2 ? v[k] : v[k + 4];
+            v[k] = keep + wave::dpp<wave::kRowHalfMirror>(send, send); // lane 7 - p in each half row
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const float keep = b1 ? v[k + 2] : v[k], send = b1 ? v[k] : v[k + 2];
+            v[k] = keep + wave::dpp<wave::kQuadSwap2>(send, send);
+        }
+        const float keep = b0 ? v[1] : v[0], send = b0 ? v[0] : v[1];
+        v[0] = keep + wave::dpp<wave::kQuadSwap1>(send, send);
+    }
+    {
+        const int h = dq % kWaves, key = row + kRowStep * (dq / kWaves);
+        if (h < rep)
+            Ss[h][key] = key < n ? v[0] * a.scale : kNegInf;
+    }
+    __syncthreads();
+    // softmax of head `wave` over the chunk's keys (lane = key)
+    const bool head_ok = wave < rep;
+    const int h = kvh * rep + (head_ok ? wave : 0);
+    float m = 0.f, l = 0.f;
+    if (head_ok) {
+        const float sc = Ss[wave][lane];
+        m = wave::max(sc);
+        const float pr = lane < n ? expf(sc - m) : 0.f;
+        l = wave::sum(pr);
+        Ps[lane][wave] = pr;
+    }
+    __syncthreads();
+    // P V: this thread's slots for every head of the group
+    float o[kOut];
+#pragma unroll
+    for (int k = 0; k < kOut; ++k)
+        o[k] = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int key = row + kRowStep * i;
+#pragma unroll
+        for (int hh = 0; hh < kWaves; ++hh) {
+            const float pr = Ps[key][hh];
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                o[4 * hh + c] = fmaf(pr, vv[i][c], o[4 * hh + c]);
+        }
+    }
+    // reduce-scatter over the wave's four rows: rows 0-1 keep values [0, 2kW), rows 2-3 the
+    // rest (permlane32_swap), then even rows the first kW of their half (permlane16_swap);
+    // row r4 ends with values [r4 * kW, (r4 + 1) * kW), each summed over the four rows
+#pragma unroll
+    for (int k = 0; k < 2 * kWaves; ++k) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(o[k]), __float_as_uint(o[k + 2 * kWaves]),
+                                                         false, false);
+        o[k] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) {
+        const auto sw =
+            __builtin_amdgcn_permlane16_swap(__float_as_uint(o[k]), __float_as_uint(o[k + kWaves]), false, false);
+        o[k] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k)
+        Os[wave][dq * kOStride + row4 * kWaves + k] = o[k];
+    __syncthreads();
+    if (head_ok && lane < D) { // wave = head, lane = head-dim element d: value 4 * head + d % 4 of column d / 4
+        const int j = 4 * wave + lane % 4, col = lane / 4;
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+            acc += Os[w][col * kOStride + j];
+        float *rec = decode_record(a, h, chunk);
+        if (a.counters) {
+            if (lane == 0) {
+                record_store<true>(rec, m);
+                record_store<true>(rec + 1, l);
+            }
+            record_store<true>(rec + 2 + lane, acc);
+        } else {
+            if (lane == 0) {
+                rec[0] = m;
+                rec[1] = l;
+            }
+            rec[2 + lane] = acc;
+        }
+    }
+    return a.counters && decode_count_in_and_merge(a, kvh, nchunks, h, head_ok, lane);
+}
+
+// One (kv head, chunk) workgroup of the decode attention with one wave per q head, for
+// groups of more than 8 q heads. Returns true in the workgroup that merged its kv head's
+// records (fused form only; the merged outputs were written with agent-coherent stores and
+// have completed).
 template <int kWaves>
 __device__ __forceinline__ bool decode_attention_chunk(const DecodeAttnArgs &a, int kvh, int chunk) {
     constexpr int C = kAttnChunk;
@@ -555,31 +744,15 @@ __device__ __forceinline__ bool decode_attention_chunk(const DecodeAttnArgs &a, 
             }
         }
     }
-    if (!a.counters)
-        return false;
-    // Fused merge: count in once this workgroup's records are complete; the last one merges.
-    __shared__ int last;
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); // the record stores have completed
-    __syncthreads();
-    if (threadIdx.x == 0)
-        last = __hip_atomic_fetch_add(a.counters + kvh * kAttnCounterStride, 1, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT) ==
-               nchunks - 1;
-    __syncthreads();
-    if (!last)
-        return false;
-    if (head_ok)
-        decode_combine_head<true>(a, h, nchunks, lane);
-    if (threadIdx.x == 0)
-        __hip_atomic_store(a.counters + kvh * kAttnCounterStride, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); // the merged outputs have completed
-    __syncthreads();
-    return true;
+    return a.counters && decode_count_in_and_merge(a, kvh, nchunks, h, head_ok, lane);
 }
 
 template <int kWaves>
 __global__ __launch_bounds__(kWaves *kWaveSize) void attention_decode_partial_kernel(DecodeAttnArgs a) {
-    decode_attention_chunk<kWaves>(a, blockIdx.x, blockIdx.y);
+    if constexpr (kWaves <= 8)
+        decode_attention_chunk_rb<kWaves>(a, blockIdx.x, blockIdx.y);
+    else
+        decode_attention_chunk<kWaves>(a, blockIdx.x, blockIdx.y);
 }
 
 // grid kvh, block kv_rep waves; wave w merges q head kvh * kv_rep + w. Workgroup k runs on the
