@@ -219,19 +219,20 @@ template <typename WT> struct QkvArgs {
     int qh, kvh, D, cap;
 };
 
+// Rotary pair p (0 or 1) of the group: elements (j + p, j + p + D/2) of the head slot, with
+// (lo, hi) = (lo c - hi s, hi c + lo s) for q and k. Each of the group's two pairs is stored by
+// its own thread, so the two sincosf calls (large arguments: pos up to 8191) run side by side
+// at the end of the kernel rather than four trigonometric calls one after another.
 template <typename WT>
-__device__ __forceinline__ void qkv_store(const QkvArgs<WT> &a, int slot, int j, int pos, const float (&y_in)[4]) {
-    const int half = a.D / 2;
-    float y[4] = {y_in[0], y_in[1], y_in[2], y_in[3]};
-    if (slot < a.qh + a.kvh) { // rotate q and k: (lo, hi) = (a c - b s, b c + a s)
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const float freq = static_cast<float>(pos) * a.inv_freq[j + p];
-            const float c = cosf(freq), s = sinf(freq);
-            const float lo = y[p], hi = y[p + 2];
-            y[p] = lo * c - hi * s;
-            y[p + 2] = hi * c + lo * s;
-        }
+__device__ __forceinline__ void qkv_store_pair(const QkvArgs<WT> &a, int slot, int j, int pos, int p, float lo,
+                                               float hi) {
+    if (slot < a.qh + a.kvh) {
+        const float freq = static_cast<float>(pos) * a.inv_freq[j + p];
+        float s, c;
+        sincosf(freq, &s, &c);
+        const float rlo = lo * c - hi * s, rhi = hi * c + lo * s;
+        lo = rlo;
+        hi = rhi;
     }
     float *dst;
     if (slot < a.qh)
@@ -240,10 +241,8 @@ __device__ __forceinline__ void qkv_store(const QkvArgs<WT> &a, int slot, int j,
         dst = a.kcache + (int64_t(slot - a.qh) * a.cap + pos) * a.D;
     else
         dst = a.vcache + (int64_t(slot - a.qh - a.kvh) * a.cap + pos) * a.D;
-    dst[j] = y[0];
-    dst[j + 1] = y[1];
-    dst[j + half] = y[2];
-    dst[j + 1 + half] = y[3];
+    dst[j + p] = lo;
+    dst[j + p + a.D / 2] = hi;
 }
 
 // One workgroup per 4-row group (grid = (qh + 2 kvh) * D / 4), one row per
@@ -269,8 +268,8 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(QkvArgs<WT> a) {
     if (lane == 0)
         res[wave] = y[0];
     __syncthreads();
-    if (threadIdx.x == 0)
-        qkv_store(a, slot, j, pos, {res[0], res[1], res[2], res[3]});
+    if (threadIdx.x < 2) // wave w holds row j + (w & 1) + (w >> 1) * D/2: pair p is (res[p], res[p + 2])
+        qkv_store_pair(a, slot, j, pos, threadIdx.x, res[threadIdx.x], res[threadIdx.x + 2]);
 }
 
 // ---- 2. decode attention: split-KV partials + combine ---------------------
@@ -286,27 +285,32 @@ __global__ __launch_bounds__(kBlock) void gemv_residual_kernel(const WT *__restr
     if constexpr (kV % WPack<WT>::kElems == 0) { // kRows rows per workgroup, columns split across the waves
         constexpr int kR = kRows;
         const int r0 = blockIdx.x * kR;
+        const bool owner = threadIdx.x < kR && r0 + threadIdx.x < out;
+        // the residual is read at the start, so its load is not a round trip in the tail
+        const float resid = owner ? hidden[r0 + threadIdx.x] : 0.f;
         int row[kR];
 #pragma unroll
         for (int r = 0; r < kR; ++r)
             row[r] = r0 + r < out ? r0 + r : r0;
         float y[kR];
         block_gemv_split<kV, kR, WT>(x, W, row, y);
-        if (threadIdx.x < kR && r0 + threadIdx.x < out) {
+        if (owner) {
             float v = y[0];
 #pragma unroll
             for (int r = 1; r < kR; ++r)
                 v = threadIdx.x == r ? y[r] : v;
-            hidden[r0 + threadIdx.x] += v;
+            hidden[r0 + threadIdx.x] = resid + v;
         }
     } else { // one row per wave
         const int r = blockIdx.x * kWavesPerBlock + threadIdx.x / kWaveSize;
         const bool active = r < out;
+        const bool owner = active && threadIdx.x % kWaveSize == 0;
+        const float resid = owner ? hidden[r] : 0.f;
         const int row[1] = {active ? r : 0};
         float y[1];
         block_gemv<kV, 1, WT>(x, nullptr, 0.f, W, row, active, nullptr, y);
-        if (active && threadIdx.x % kWaveSize == 0)
-            hidden[r] += y[0];
+        if (owner)
+            hidden[r] = resid + y[0];
     }
 }
 
@@ -360,6 +364,8 @@ __global__ __launch_bounds__(kBlock) void down_residual_kernel(const WT *__restr
     const int lane = threadIdx.x % kWaveSize, wave = threadIdx.x / kWaveSize;
     const int r0 = blockIdx.x * kR;
     const int c0 = wave * Kw;
+    const bool owner = threadIdx.x < kR && r0 + threadIdx.x < out;
+    const float resid = owner ? hidden[r0 + threadIdx.x] : 0.f; // read first: no round trip in the tail
     f32x4 xv[kP][E / 4];
     const f32x4 *a4 = reinterpret_cast<const f32x4 *>(act + c0);
 #pragma unroll
@@ -387,12 +393,12 @@ __global__ __launch_bounds__(kBlock) void down_residual_kernel(const WT *__restr
             part[wave][r] = acc;
     }
     __syncthreads();
-    if (threadIdx.x < kR && r0 + threadIdx.x < out) {
+    if (owner) {
         float t = 0.f;
 #pragma unroll
         for (int k = 0; k < kWavesPerBlock; ++k)
             t += part[k][threadIdx.x];
-        hidden[r0 + threadIdx.x] += t;
+        hidden[r0 + threadIdx.x] = resid + t;
     }
 }
 
@@ -542,7 +548,8 @@ __global__ __launch_bounds__(256) static void rope_split_kernel(const float *__r
         float lo = src[j], hi = src[j + half];
         if (slot < qh + kvh) {
             const float freq = static_cast<float>(pos) * inv_freq[j];
-            const float c = cosf(freq), s = sinf(freq);
+            float s, c;
+            sincosf(freq, &s, &c); // as the decode step's qkv_store_pair, so both fill the cache alike
             const float a = lo, b = hi;
             lo = a * c - b * s;
             hi = b * c + a * s;
