@@ -318,3 +318,56 @@ def test_config5_llama_3_2_1b_greedy(ow):
     got, want, worst = greedy_compare(gpu, cpu, ids, 256, 1024)
     print(f"config5: {len(got)} tokens compared, worst logits nrmse {worst:.2e}")
     assert got == want
+
+
+def test_lm_head_argmax_ties_and_nan(tiny, tmp_path, ow):
+    """The LM head's argmax rules at model level (reference: include/ops/argmax.cuh:8-14), through its
+    per-workgroup records and their merge. Embedding rows 38, 39 and 301 are set to the same vector, which
+    gives the largest logit of the last prompt position: 38 and 39 share an LM-head workgroup, 301 lies in
+    another. Equal maxima must go to the lowest index (38). Rows 2 and 300 (300 in 301's workgroup) are
+    NaN, whose logits must never win. A table of NaN rows only yields 0x7fffffff."""
+    from opworks_amd.llama import LlamaModel
+    from tests.packs import pack_from_oracle, write_pack
+    import json
+    import struct
+    _, cpu = tiny
+    H, V = TINY["hidden_size"], TINY["vocab_size"]
+    crafted = {2, 38, 39, 300, 301}
+    ids = [t for t in prompt(40, V, 4242) if t not in crafted][:12]
+    cpu.reset(64)
+    _, _, caps = cpu.prefill(ids, capture=True)
+    h = caps[-1][-1].astype(np.float64)  # last position's hidden state after the last layer
+    gamma = cpu.weight(1, 0, H).astype(np.float64)
+    nh = h / np.sqrt(np.mean(h * h) + TINY["rms_norm_eps"]) * gamma
+    row = (nh * (10.0 / np.dot(nh, nh))).astype(np.float32)  # logit ~10, far above the N(0, 0.02) rows
+
+    base = tmp_path / "base.opwpack"
+    pack_from_oracle(str(base), cpu, TINY)
+    raw = base.read_bytes()
+    mlen = struct.unpack("<Q", raw[8:16])[0]
+    manifest = json.loads(raw[16:16 + mlen])
+    blob = raw[16 + mlen:]
+    tensors = {}
+    for name, meta in manifest["tensors"].items():
+        n = int(np.prod(meta["shape"]))
+        tensors[name] = np.frombuffer(blob, np.float32, n, meta["offset"]).reshape(meta["shape"]).copy()
+    extra = {k: v for k, v in manifest.items() if k not in ("format_version", "dtype", "tensors", "aliases")}
+
+    emb = tensors["model.embed_tokens.weight"]
+    for r in (38, 39, 301):
+        emb[r] = row
+    emb[2] = np.nan
+    emb[300] = np.nan
+    path = tmp_path / "ties.opwpack"
+    write_pack(str(path), tensors, aliases=manifest.get("aliases"), extra=extra)
+    s = LlamaModel.load(str(path)).session(64)
+    tok = s.prefill(ids)
+    logits = s.last_logits()
+    assert logits[38] == logits[39] == logits[301] and logits[38] > 5.0
+    assert np.isnan(logits[2]) and np.isnan(logits[300])
+    assert tok == 38
+    assert 0 <= s.decode_step(tok) < V
+    emb[:] = np.nan
+    write_pack(str(path), tensors, aliases=manifest.get("aliases"), extra=extra)
+    s = LlamaModel.load(str(path)).session(64)
+    assert s.prefill(ids) == 0x7FFFFFFF
