@@ -116,6 +116,7 @@ struct LlamaSession : detail::SessionHandles {
         ws.lm_records = static_cast<int>(detail::blocks_for64(cfg.vocab_size, llama::kLmRows * llama::kWavesPerBlock));
         ws.splitk_floats = std::max(detail::kSplitKWorkspaceF32, detail::kSplitKWorkspaceBf16);
         ws.state_ints = sizeof(llama::StepState) / sizeof(int32_t);
+        ws.argmax_groups = llama::kArgmaxGroups;
         ws.attn_counter_ints = cfg.num_kv_heads * detail::kAttnCounterStride;
         return ws;
     }
@@ -125,6 +126,7 @@ struct LlamaSession : detail::SessionHandles {
         OPWORKS_HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         OPWORKS_HIP_CHECK(hipMemsetAsync(workspace.state.data(), 0, workspace.state.bytes(), stream));
         OPWORKS_HIP_CHECK(hipMemsetAsync(workspace.attn_counters.data(), 0, workspace.attn_counters.bytes(), stream));
+        OPWORKS_HIP_CHECK(hipMemsetAsync(workspace.lm_counter.data(), 0, workspace.lm_counter.bytes(), stream));
         OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&h_state), sizeof(llama::StepState)));
         *h_state = llama::StepState{0, 0, -1, 0};
         synchronize(stream);
@@ -546,8 +548,9 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         const int records = static_cast<int>(
             detail::blocks_for64(cfg_.vocab_size, llama::kLmRows * kRowScale * llama::kWavesPerBlock));
         launch_async(s.stream, llama::lm_head_kernel<kV, WT>, records, llama::kBlock, la);
-        launch_async(s.stream, llama::argmax_records_kernel, 1, 1024, s.workspace.lm_best_val.data(), s.workspace.lm_best_idx.data(),
-                     records, s.state(), s.workspace.gen.data());
+        launch_async(s.stream, llama::argmax_records_kernel, llama::kArgmaxGroups, 256, s.workspace.lm_best_val.data(),
+                     s.workspace.lm_best_idx.data(), records, s.workspace.lm_part_val.data(), s.workspace.lm_part_idx.data(),
+                     s.workspace.lm_counter.data(), s.state(), s.workspace.gen.data());
     }
 
     // Calls f(IntTag<H / 256>, IntTag<I / 1024>); bf16 rows need whole 8-weight

@@ -459,24 +459,37 @@ __global__ __launch_bounds__(kBlock) void lm_head_kernel(LmHeadArgs<WT> a) {
     }
 }
 
-// One workgroup of 1024 threads reduces the per-workgroup records.
-__global__ __launch_bounds__(1024) static void argmax_records_kernel(const float *__restrict__ best_val,
-                                                                     const int *__restrict__ best_idx, int count,
-                                                                     StepState *state, int *gen) {
-    __shared__ float sv[16];
-    __shared__ int si[16];
+// kArgmaxGroups workgroups of 256 lanes reduce the LM head's per-workgroup
+// records: workgroup g takes records [g * per, (g + 1) * per) down to one
+// (value, index) partial and publishes it with agent-coherent stores; once
+// they have completed it counts itself in on `counter`, and the last to arrive
+// merges the partials (agent-coherent loads), resets the counter and advances
+// the step state. This is the protocol of the fused decode-attention merge.
+// The merge is order-independent (largest value, then lowest index), so the
+// result does not depend on which workgroup arrives last. (One 1024-lane
+// workgroup over the 32064 records of the fp32 LM head took 8.1 us.)
+constexpr int kArgmaxGroups = 64;
+__global__ __launch_bounds__(256) static void argmax_records_kernel(const float *__restrict__ best_val,
+                                                                    const int *__restrict__ best_idx, int count,
+                                                                    float *part_val, int *part_idx, int *counter,
+                                                                    StepState *state, int *gen) {
+    __shared__ float sv[256 / kWaveSize];
+    __shared__ int si[256 / kWaveSize];
+    __shared__ int last;
     const int lane = threadIdx.x % kWaveSize, wave = threadIdx.x / kWaveSize;
+    const int per = (count + kArgmaxGroups - 1) / kArgmaxGroups;
+    const int b0 = blockIdx.x * per, b1 = b0 + per < count ? b0 + per : count;
     float bv = kNegInf;
     int bi = 0x7fffffff;
-    constexpr int kBatch = 8;
-    for (int base = threadIdx.x; base < count; base += kBatch * 1024) {
+    constexpr int kBatch = 4;
+    for (int base = b0 + threadIdx.x; base < b1; base += kBatch * 256) {
         float v[kBatch];
         int ix[kBatch];
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
-            const int b = base + u * 1024;
-            v[u] = b < count ? best_val[b] : kNegInf;
-            ix[u] = b < count ? best_idx[b] : 0x7fffffff;
+            const int b = base + u * 256;
+            v[u] = b < b1 ? best_val[b] : kNegInf;
+            ix[u] = b < b1 ? best_idx[b] : 0x7fffffff;
         }
 #pragma unroll
         for (int u = 0; u < kBatch; ++u)
@@ -489,16 +502,34 @@ __global__ __launch_bounds__(1024) static void argmax_records_kernel(const float
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int k = 0; k < static_cast<int>(blockDim.x) / kWaveSize; ++k)
+        for (int k = 0; k < 256 / kWaveSize; ++k)
             argmax_merge(bv, bi, sv[k], si[k]);
-        state->next = bi;
+        __hip_atomic_store(part_val + blockIdx.x, bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(part_idx + blockIdx.x, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(detail::kWaitVmcnt0); // the partial has completed
+        last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == kArgmaxGroups - 1;
+    }
+    __syncthreads();
+    if (!last || wave != 0)
+        return;
+    float v = kNegInf;
+    int ix = 0x7fffffff;
+    if (lane < kArgmaxGroups) {
+        v = __hip_atomic_load(part_val + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ix = __hip_atomic_load(part_idx + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    wave_argmax(v, ix);
+    if (lane == 0) {
+        __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        state->next = ix;
         if (state->chain) { // greedy chaining: the next launch decodes this token at pos + 1
-            gen[state->pos] = bi;
-            state->token = bi;
+            gen[state->pos] = ix;
+            state->token = ix;
             state->pos += 1;
         }
     }
 }
+static_assert(kArgmaxGroups <= kWaveSize, "one wave merges the partials");
 
 // ---- prefill glue ------------------------------------------------------------
 // hidden[t][:] = embed[ids[t]][:] (bf16 rows widened), one 16-byte pack of

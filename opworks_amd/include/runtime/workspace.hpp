@@ -23,6 +23,7 @@ struct WorkspaceSizes {
     int lm_records = 0;        // LM-head workgroups (one argmax record each)
     int64_t splitk_floats = 0; // split-K partial tiles of the prefill GEMMs
     int state_ints = 0;        // device step state
+    int argmax_groups = 0;     // workgroups of the records' reduction
     int attn_counter_ints = 0; // decode attention arrival counters (one cache line per kv head)
 };
 
@@ -47,6 +48,9 @@ struct Workspace {
     TypedDeviceBuffer<float> logits;        // [V] last row's logits
     TypedDeviceBuffer<float> lm_best_val;   // [records]
     TypedDeviceBuffer<int32_t> lm_best_idx; // [records]
+    TypedDeviceBuffer<float> lm_part_val;   // [argmax groups] partials of the records' reduction
+    TypedDeviceBuffer<int32_t> lm_part_idx; // [argmax groups]
+    TypedDeviceBuffer<int32_t> lm_counter;  // arrivals of the argmax groups (own 256-byte line), zero between launches
     TypedDeviceBuffer<int32_t> gen;         // [T] tokens of a chained greedy decode, by position
     TypedDeviceBuffer<int32_t> state;       // device step state
     WorkspaceSizes sizes;
@@ -74,6 +78,9 @@ struct Workspace {
         logits = TypedDeviceBuffer<float>(cfg.vocab_size);
         lm_best_val = TypedDeviceBuffer<float>(s.lm_records);
         lm_best_idx = TypedDeviceBuffer<int32_t>(s.lm_records);
+        lm_part_val = TypedDeviceBuffer<float>(s.argmax_groups);
+        lm_part_idx = TypedDeviceBuffer<int32_t>(s.argmax_groups);
+        lm_counter = TypedDeviceBuffer<int32_t>(64);
         gen = TypedDeviceBuffer<int32_t>(T);
         state = TypedDeviceBuffer<int32_t>(s.state_ints);
     }

@@ -119,10 +119,13 @@ def test_config4_prefill_full_size_sampled(ow, orc):
     assert float(np.sqrt(np.mean(err ** 2)) / np.sqrt(np.mean(exact ** 2))) <= 2e-6
 
 
-@pytest.mark.parametrize("qh,kv_rep,D", [(8, 1, 32), (16, 16, 64), (6, 3, 48), (8, 8, 16), (12, 2, 64)])
+@pytest.mark.parametrize("qh,kv_rep,D", [(8, 1, 32), (16, 16, 64), (6, 3, 48), (8, 8, 16), (12, 2, 64),
+                                         (10, 5, 64), (12, 6, 32), (7, 7, 12), (4, 4, 4), (4, 2, 60)])
 @pytest.mark.parametrize("length", [1, 100, 1000])
 def test_decode_head_shapes(ow, orc, qh, kv_rep, D, length):
-    """Other GQA ratios (kv_rep 3 rounds up to 4 waves) and head sizes."""
+    """Other GQA ratios (kv_rep 3 rounds up to 4 waves, 5-7 up to 8, partly idle) and head sizes (D = 4, 12,
+    60: head-dim packs past D are padding in the register-blocked chunk); the one-launch form matches the
+    two-launch form bit for bit on every shape."""
     cap = 1024
     kvh = qh // kv_rep
     q = orc.fill_normal(qh * D, SEED, 20, 0.0, 1.0)
@@ -135,6 +138,12 @@ def test_decode_head_shapes(ow, orc, qh, kv_rep, D, length):
     ref = orc.attention_decode(q, k, v, qh, kv_rep, D, length, cap)
     _, bound = orc.attention_explicit(q, k, v, 1, length, qh, kv_rep, D, cap)
     check(got, ref, bound[:, 0])
+    ws_n = ow.ops.attention_decode_workspace_size(qh, length, D)
+    ws = ow.DeviceBuffer.empty(ws_n)
+    counters = ow.DeviceBuffer.from_host(np.zeros(ow.ops.attention_decode_counters_size(qh, kv_rep), np.int32))
+    fused = ow.DeviceBuffer.empty(qh * D)
+    ow.ops.attention_decode_fused(dq, dk, dv, fused, qh, kv_rep, D, length, cap, ws, ws_n, counters)
+    assert np.array_equal(fused.to_host().view(np.uint32), out.to_host().view(np.uint32))
 
 
 @pytest.mark.parametrize("length,cap", [(1, 1), (2, 8), (63, 64), (64, 64), (65, 128), (767, 1024), (2048, 2048),
