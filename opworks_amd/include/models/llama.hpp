@@ -459,9 +459,9 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         hipStream_t st = s.stream;
         const LayerWeights<WT> &lw = w_.layers[static_cast<size_t>(l)];
         llama::QkvArgs<WT> qa{};
-        // layer 0 reads the step token's embedding row: fp32 tables directly in
-        // the qkv kernel, bf16 tables widened into the residual stream first
-        qa.hidden_in = (l == 0 && !kBf16) ? nullptr : s.workspace.step_hidden.data();
+        // layer 0 reads the step token's embedding row in the qkv kernel (bf16 rows widened as
+        // they are loaded), whose workgroup 0 also writes it into the residual stream
+        qa.hidden_in = l == 0 ? nullptr : s.workspace.step_hidden.data();
         qa.embed = w_.embed_tokens.data();
         qa.hidden_out = s.workspace.step_hidden.data();
         qa.gamma = lw.input_norm.data();
@@ -478,9 +478,6 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         qa.cap = s.cache.max_seq_len;
         if (stage_on(0)) {
             tick();
-            if (kBf16 && l == 0)
-                launch_async(st, llama::embed_token_kernel<WT>, detail::blocks_for64(H, 256), 256, w_.embed_tokens.data(),
-                             s.state(), s.workspace.step_hidden.data(), H);
             launch_async(st, llama::qkv_rope_kernel<kV, WT>, qkv_groups, llama::kBlock, qa);
         }
         llama::DecodeAttnArgs aa{};

@@ -73,8 +73,20 @@ template <typename WT> constexpr int kRowScale = std::is_same_v<WT, bf16> ? 2 : 
 // The (optionally RMS-normalised) vector goes to LDS and each wave reads its
 // kV packs from there. Waves with active == false still take part in the
 // barriers. xn = x * rsqrtf(mean(x^2) + eps) * gamma, ops::rms_norm's order.
-template <int kV, int kR = kRows, typename WT = float>
-__device__ __forceinline__ void block_gemv(const float *__restrict__ x, const float *__restrict__ gamma, float eps,
+// The input x is fp32, or (XT = bf16: a bf16 model's embedding row at layer 0)
+// bf16 widened exactly as it is loaded; copy_x_to receives the widened row.
+template <typename XT> __device__ __forceinline__ f32x4 load_x4(const XT *x, int c) {
+    if constexpr (std::is_same_v<XT, float>) {
+        return reinterpret_cast<const f32x4 *>(x)[c];
+    } else {
+        const uint2 b = reinterpret_cast<const uint2 *>(x)[c]; // elements 4c .. 4c+3, low half first
+        return f32x4{__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xffff0000u), __uint_as_float(b.y << 16),
+                     __uint_as_float(b.y & 0xffff0000u)};
+    }
+}
+
+template <int kV, int kR = kRows, typename WT = float, typename XT = float>
+__device__ __forceinline__ void block_gemv(const XT *__restrict__ x, const float *__restrict__ gamma, float eps,
                                            const WT *__restrict__ W, const int (&row)[kR], bool active,
                                            float *__restrict__ copy_x_to, float (&y)[kR]) {
     constexpr int H = 256 * kV;
@@ -86,14 +98,13 @@ __device__ __forceinline__ void block_gemv(const float *__restrict__ x, const fl
     __shared__ __attribute__((aligned(16))) float xs[H];
     __shared__ float red[kWavesPerBlock];
     const int tid = threadIdx.x, lane = tid % kWaveSize, wave = tid / kWaveSize;
-    const f32x4 *x4 = reinterpret_cast<const f32x4 *>(x);
     const f32x4 *g4 = reinterpret_cast<const f32x4 *>(gamma);
     f32x4 xv[kX], gv[kX];
 #pragma unroll
     for (int i = 0; i < kX; ++i) {
         const int c = tid + kBlock * i;
         if (c < kPacks) {
-            xv[i] = x4[c];
+            xv[i] = load_x4(x, c);
             if (gamma)
                 gv[i] = g4[c];
         }
@@ -206,7 +217,7 @@ __device__ __forceinline__ void block_gemv_split(const float *__restrict__ x, co
 // slot g / (D/4), j = 2 * (g % (D/4)). Layer 0 reads its input from the
 // embedding row of the step token and also writes it to the residual stream.
 template <typename WT> struct QkvArgs {
-    const float *hidden_in; // residual stream (or nullptr: use embed[token], fp32 weights only)
+    const float *hidden_in; // residual stream (or nullptr: layer 0 reads embed[token])
     const WT *embed;        // [V][H]
     float *hidden_out;      // written only when reading from the embedding
     const float *gamma;     // input RMSNorm weight
@@ -256,15 +267,13 @@ __global__ __launch_bounds__(kBlock) void qkv_rope_kernel(QkvArgs<WT> a) {
     const int slot = g / groups_per_head;
     const int j = 2 * (g % groups_per_head);
     const int pos = a.state->pos;
-    const float *src = a.hidden_in;
-    if constexpr (std::is_same_v<WT, float>) // bf16 models gather the row with embed_token_kernel first
-        if (!src)
-            src = a.embed + int64_t(a.state->token) * H;
     const int row[1] = {slot * a.D + j + (wave & 1) + (wave >> 1) * (a.D / 2)};
     float y[1];
-    // layer 0: workgroup 0 also writes the embedding row into the residual stream
-    block_gemv<kV, 1, WT>(src, a.gamma, a.eps, a.wqkv, row, true, (!a.hidden_in && g == 0) ? a.hidden_out : nullptr,
-                          y);
+    if (a.hidden_in)
+        block_gemv<kV, 1, WT>(a.hidden_in, a.gamma, a.eps, a.wqkv, row, true, nullptr, y);
+    else // layer 0: the step token's embedding row (widened if bf16); workgroup 0 also writes it into the residual stream
+        block_gemv<kV, 1, WT, WT>(a.embed + int64_t(a.state->token) * H, a.gamma, a.eps, a.wqkv, row, true,
+                                  g == 0 ? a.hidden_out : nullptr, y);
     if (lane == 0)
         res[wave] = y[0];
     __syncthreads();
@@ -551,7 +560,9 @@ __global__ __launch_bounds__(256) void embedding_kernel(const WT *__restrict__ e
     }
 }
 
-// Decode step of a bf16 model: hidden = embed[state.token] widened to fp32.
+// hidden = embed[state.token] widened to fp32: the "after embedding" capture of a
+// bf16 model's single-row debug prefill (the decode step itself reads the row in
+// layer 0's qkv kernel).
 template <typename WT>
 __global__ __launch_bounds__(256) void embed_token_kernel(const WT *__restrict__ embed,
                                                           const StepState *__restrict__ state,
