@@ -493,6 +493,7 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         aa.D = D;
         aa.cap = s.cache.max_seq_len;
         aa.max_chunks = s.workspace.sizes.attn_chunks;
+        aa.chunks_per_record = detail::decode_chunks_per_record(aa.kv_rep, aa.max_chunks);
         aa.scale = 1.f / std::sqrt(static_cast<float>(D));
         if (stage_on(1)) {
             tick();

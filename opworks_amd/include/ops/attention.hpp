@@ -387,8 +387,14 @@ struct DecodeAttnArgs {
     int *counters;                // [kvh * kAttnCounterStride], zero between launches; null: combine kernel
     int len, len_bias;
     int kv_rep, D, cap, max_chunks;
+    int chunks_per_record;        // 1, or 2: a workgroup computes two adjacent chunks and leaves one record
     float scale;
 };
+
+// Records of a kv head: one per chunk, or per pair of chunks.
+__device__ __forceinline__ int decode_records(const DecodeAttnArgs &a, int nchunks) {
+    return (nchunks + a.chunks_per_record - 1) / a.chunks_per_record;
+}
 
 // s_waitcnt operand of gfx9 for vmcnt(0) with expcnt and lgkmcnt left at their maxima
 // (vmcnt bits [3:0] and [15:14] = 0, expcnt [6:4] = 7, lgkmcnt [11:8] = 15): waits until
@@ -490,39 +496,45 @@ __device__ __forceinline__ float *decode_record(const DecodeAttnArgs &a, int h, 
     return a.partial + (int64_t(h) * a.max_chunks + chunk) * (a.D + 2);
 }
 
-// Register-blocked (kv head, chunk) workgroup for kWaves <= 8 waves (kv_rep <= 8 q heads).
-// Thread t holds key slots i < kPer = 16 / kWaves: key t/16 + (kWaves * 4) * i, head-dim
-// pack dq = t % 16 of it (the row padded to 16 packs; packs >= D/4 and keys >= n are zero),
-// loaded straight from HBM into registers with the q packs of every head of the group, so
-// K and V never pass through LDS and no wave re-reads the chunk:
-//  * scores: the thread's kPer x kWaves partial dot products (always 16) are summed over
-//    the 16 lanes of its row by a DPP reduce-scatter (row_ror 8, row_half_mirror, quad_perm
-//    ^2, ^1: each step keeps half the values and adds the partner lane's other half), after
-//    which lane dq of the row holds value dq, i.e. head dq % kWaves of slot dq / kWaves;
-//  * softmax: wave h reads head h's 64 scores from LDS (lane = key);
+// Register-blocked (kv head, record) workgroup for kWaves <= 8 waves per chunk (kv_rep <= 8 q
+// heads), computing kSub adjacent chunks (1, or 2 with two groups of kWaves waves) and leaving one
+// record. In each group, thread t holds key slots i < kPer = 16 / kWaves: key t/16 + (kWaves * 4) * i,
+// head-dim pack dq = t % 16 of it (the row padded to 16 packs; packs >= D/4 and keys past the
+// length are zero), loaded straight from HBM into registers with the q packs of every head of the
+// group, so K and V never pass through LDS and no wave re-reads the chunk:
+//  * scores: the thread's kPer x kWaves partial dot products (always 16) are summed over the 16
+//    lanes of its row by a DPP reduce-scatter (row_ror 8, row_half_mirror, quad_perm ^2, ^1: each
+//    step keeps half the values and adds the partner lane's other half), after which lane dq of
+//    the row holds value dq, i.e. head dq % kWaves of slot dq / kWaves;
+//  * softmax: wave h of the group reads head h's 64 scores from LDS (lane = key);
 //  * P V: each thread accumulates its slots' V packs for every head (kWaves packs of 4),
 //    reduce-scatters them over the wave's four rows with v_permlane32_swap then
 //    v_permlane16_swap, and the waves' partial outputs are summed through LDS.
-// About 10 KB of LDS traffic per workgroup, against the 128 KB of the one-head-per-wave
-// form. Same record layout and merge as decode_attention_chunk.
-template <int kWaves>
-__device__ __forceinline__ bool decode_attention_chunk_rb(const DecodeAttnArgs &a, int kvh, int chunk) {
+// With kSub = 2 the two chunks' (m, l, acc) are then combined in the workgroup (M = max, each
+// rescaled by e^(m - M)), so a kv head has half as many records to merge; a second chunk past
+// the length contributes nothing. About 10 KB of LDS traffic per chunk, against the 128 KB of
+// the one-head-per-wave form. The records and their merge are those of decode_attention_chunk.
+template <int kWaves, int kSub>
+__device__ __forceinline__ bool decode_attention_chunk_rb(const DecodeAttnArgs &a, int kvh, int rec) {
     static_assert(kWaves >= 1 && kWaves <= 8 && (kWaves & (kWaves - 1)) == 0, "1, 2, 4 or 8 waves");
+    static_assert(kSub == 1 || kSub == 2, "one or two chunks per record");
     constexpr int C = kAttnChunk;
-    constexpr int T = kWaves * kWaveSize;
-    constexpr int kRowStep = T / 16;          // keys between a thread's slots
+    constexpr int TH = kWaves * kWaveSize;    // threads per chunk
+    constexpr int kRowStep = TH / 16;         // keys between a thread's slots
     constexpr int kPer = 16 / kWaves;         // key slots per thread
     constexpr int kOut = 4 * kWaves;          // P V values per thread: kWaves heads x 4 dims
     constexpr int kOStride = kOut + 4;        // floats per dq column of a wave's partial outputs (kOut used)
     static_assert(kPer * kWaves == 16, "16 partial scores per thread");
     const int len = decode_len(a);
     const int nchunks = (len + C - 1) / C;
-    if (chunk >= nchunks)
+    const int nrec = (nchunks + kSub - 1) / kSub;
+    if (rec >= nrec)
         return false;
-    const int k0 = chunk * C;
-    const int n = len - k0 < C ? len - k0 : C;
+    const int sub = threadIdx.x / TH, t = threadIdx.x % TH; // chunk of this thread's group, thread in it
+    const int k0 = (rec * kSub + sub) * C;
+    const int n = len - k0 < 0 ? 0 : (len - k0 < C ? len - k0 : C); // 0: a second chunk past the length
     const int D = a.D, P = D / 4, rep = a.kv_rep;
-    const int t = threadIdx.x, wave = t / kWaveSize, lane = t % kWaveSize;
+    const int wave = t / kWaveSize, lane = t % kWaveSize;
     const int dq = t % 16, row = t / 16, row4 = lane / 16;
     const bool dq_ok = dq < P;
     const f32x4 *kh = reinterpret_cast<const f32x4 *>(a.kcache + (int64_t(kvh) * a.cap + k0) * D);
@@ -540,9 +552,9 @@ __device__ __forceinline__ bool decode_attention_chunk_rb(const DecodeAttnArgs &
 #pragma unroll
     for (int h = 0; h < kWaves; ++h)
         qv[h] = dq_ok && h < rep ? q4[h * P + dq] : zero;
-    __shared__ float Ss[kWaves][C];                        // scaled scores, [head][key]
-    __shared__ __attribute__((aligned(16))) float Ps[C][kWaves]; // probabilities, [key][head]
-    __shared__ __attribute__((aligned(16))) float Os[kWaves][16 * kOStride]; // per-wave P V partials
+    __shared__ float Ss[kSub][kWaves][C];                        // scaled scores, [head][key]
+    __shared__ __attribute__((aligned(16))) float Ps[kSub][C][kWaves]; // probabilities, [key][head]
+    __shared__ __attribute__((aligned(16))) float Os[kSub][kWaves][16 * kOStride]; // per-wave P V partials
     // scores: 16 partial dot products, then the row reduce-scatter
     float v[16];
 #pragma unroll
@@ -575,19 +587,22 @@ __device__ __forceinline__ bool decode_attention_chunk_rb(const DecodeAttnArgs &
     {
         const int h = dq % kWaves, key = row + kRowStep * (dq / kWaves);
         if (h < rep)
-            Ss[h][key] = key < n ? v[0] * a.scale : kNegInf;
+            Ss[sub][h][key] = key < n ? v[0] * a.scale : kNegInf;
     }
     __syncthreads();
-    // softmax of head `wave` over the chunk's keys (lane = key)
+    // softmax of head `wave` over the chunk's keys (lane = key); an empty chunk leaves m = -inf
     const bool head_ok = wave < rep;
     const int h = kvh * rep + (head_ok ? wave : 0);
-    float m = 0.f, l = 0.f;
+    float m = kNegInf, l = 0.f;
     if (head_ok) {
-        const float sc = Ss[wave][lane];
-        m = wave::max(sc);
-        const float pr = lane < n ? expf(sc - m) : 0.f;
-        l = wave::sum(pr);
-        Ps[lane][wave] = pr;
+        float pr = 0.f;
+        if (n > 0) {
+            const float sc = Ss[sub][wave][lane];
+            m = wave::max(sc);
+            pr = lane < n ? expf(sc - m) : 0.f;
+            l = wave::sum(pr);
+        }
+        Ps[sub][lane][wave] = pr;
     }
     __syncthreads();
     // P V: this thread's slots for every head of the group
@@ -600,7 +615,7 @@ __device__ __forceinline__ bool decode_attention_chunk_rb(const DecodeAttnArgs &
         const int key = row + kRowStep * i;
 #pragma unroll
         for (int hh = 0; hh < kWaves; ++hh) {
-            const float pr = Ps[key][hh];
+            const float pr = Ps[sub][key][hh];
 #pragma unroll
             for (int c = 0; c < 4; ++c)
                 o[4 * hh + c] = fmaf(pr, vv[i][c], o[4 * hh + c]);
@@ -623,30 +638,54 @@ __device__ __forceinline__ bool decode_attention_chunk_rb(const DecodeAttnArgs &
     }
 #pragma unroll
     for (int k = 0; k < kWaves; ++k)
-        Os[wave][dq * kOStride + row4 * kWaves + k] = o[k];
+        Os[sub][wave][dq * kOStride + row4 * kWaves + k] = o[k];
     __syncthreads();
-    if (head_ok && lane < D) { // wave = head, lane = head-dim element d: value 4 * head + d % 4 of column d / 4
+    // wave = head, lane = head-dim element d: value 4 * head + d % 4 of column d / 4
+    float acc = 0.f;
+    if (head_ok && lane < D) {
         const int j = 4 * wave + lane % 4, col = lane / 4;
-        float acc = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w)
-            acc += Os[w][col * kOStride + j];
-        float *rec = decode_record(a, h, chunk);
-        if (a.counters) {
+            acc += Os[sub][w][col * kOStride + j];
+    }
+    if constexpr (kSub == 2) { // combine the two chunks into the record of group 0
+        __shared__ float Ah[kWaves][kAttnMaxD], Mh[kWaves], Lh[kWaves];
+        if (sub == 1 && head_ok) {
+            if (lane < D)
+                Ah[wave][lane] = acc;
             if (lane == 0) {
-                record_store<true>(rec, m);
-                record_store<true>(rec + 1, l);
+                Mh[wave] = m;
+                Lh[wave] = l;
             }
-            record_store<true>(rec + 2 + lane, acc);
-        } else {
-            if (lane == 0) {
-                rec[0] = m;
-                rec[1] = l;
-            }
-            rec[2 + lane] = acc;
+        }
+        __syncthreads();
+        if (sub == 0 && head_ok) {
+            const float m1 = Mh[wave], M = fmaxf(m, m1);
+            const float a0 = expf(m - M), a1 = m1 == kNegInf ? 0.f : expf(m1 - M);
+            l = l * a0 + Lh[wave] * a1;
+            if (lane < D)
+                acc = acc * a0 + Ah[wave][lane] * a1;
+            m = M;
         }
     }
-    return a.counters && decode_count_in_and_merge(a, kvh, nchunks, h, head_ok, lane);
+    const bool writer = sub == 0 && head_ok;
+    if (writer && lane < D) {
+        float *r = a.partial + (int64_t(h) * a.max_chunks + rec) * (D + 2);
+        if (a.counters) {
+            if (lane == 0) {
+                record_store<true>(r, m);
+                record_store<true>(r + 1, l);
+            }
+            record_store<true>(r + 2 + lane, acc);
+        } else {
+            if (lane == 0) {
+                r[0] = m;
+                r[1] = l;
+            }
+            r[2 + lane] = acc;
+        }
+    }
+    return a.counters && decode_count_in_and_merge(a, kvh, nrec, h, writer, lane);
 }
 
 // One (kv head, chunk) workgroup of the decode attention with one wave per q head, for
@@ -747,10 +786,10 @@ __device__ __forceinline__ bool decode_attention_chunk(const DecodeAttnArgs &a, 
     return a.counters && decode_count_in_and_merge(a, kvh, nchunks, h, head_ok, lane);
 }
 
-template <int kWaves>
-__global__ __launch_bounds__(kWaves *kWaveSize) void attention_decode_partial_kernel(DecodeAttnArgs a) {
+template <int kWaves, int kSub>
+__global__ __launch_bounds__(kSub *kWaves *kWaveSize) void attention_decode_partial_kernel(DecodeAttnArgs a) {
     if constexpr (kWaves <= 8)
-        decode_attention_chunk_rb<kWaves>(a, blockIdx.x, blockIdx.y);
+        decode_attention_chunk_rb<kWaves, kSub>(a, blockIdx.x, blockIdx.y);
     else
         decode_attention_chunk<kWaves>(a, blockIdx.x, blockIdx.y);
 }
@@ -761,29 +800,46 @@ __global__ __launch_bounds__(kWaves *kWaveSize) void attention_decode_partial_ke
 // workgroups measured slower (2048 keys: 8.34 against 7.90 us per call).
 __global__ __launch_bounds__(kAttnMaxRep *kWaveSize) static void attention_decode_combine_kernel(DecodeAttnArgs a) {
     const int len = decode_len(a);
-    const int nchunks = (len + kAttnChunk - 1) / kAttnChunk; // <= max_chunks <= 2 * kWaveSize
+    const int nrec = decode_records(a, (len + kAttnChunk - 1) / kAttnChunk); // <= max_chunks <= 2 * kWaveSize
     const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
-    decode_combine_head<false>(a, blockIdx.x * a.kv_rep + wave, nchunks, lane);
+    decode_combine_head<false>(a, blockIdx.x * a.kv_rep + wave, nrec, lane);
 }
 
 // Enqueues the partial and combine kernels (or the fused partial kernel alone
 // when a.counters is set): grid (kvh, max_chunks) with kv_rep rounded up to a
 // power of two waves per workgroup.
-inline void attention_decode_launch(const DecodeAttnArgs &a, int kvh, hipStream_t stream) {
-    const dim3 grid(kvh, a.max_chunks);
+// Chunks per record: two when a kv head would otherwise have more than 16 records, so the merge
+// reads at most 16 per head in one batch (2048 keys: 7.3 -> 6.x us per fused call); the load
+// phase of 128 workgroups x 64 KB measured 3.0 against 2.7 us for 256 x 32 KB. Groups of more
+// than 8 q heads keep one chunk per workgroup (their one-wave-per-head form).
+inline int decode_chunks_per_record(int kv_rep, int max_chunks) { return kv_rep <= 8 && max_chunks > 16 ? 2 : 1; }
+
+template <int kSub> inline void attention_decode_launch_sub(const DecodeAttnArgs &a, int kvh, hipStream_t stream) {
+    const dim3 grid(kvh, (a.max_chunks + kSub - 1) / kSub);
     const int rep = a.kv_rep;
     if (rep <= 1)
-        launch_async(stream, attention_decode_partial_kernel<1>, grid, kWaveSize, a);
+        launch_async(stream, attention_decode_partial_kernel<1, kSub>, grid, kSub * kWaveSize, a);
     else if (rep <= 2)
-        launch_async(stream, attention_decode_partial_kernel<2>, grid, 2 * kWaveSize, a);
+        launch_async(stream, attention_decode_partial_kernel<2, kSub>, grid, kSub * 2 * kWaveSize, a);
     else if (rep <= 4)
-        launch_async(stream, attention_decode_partial_kernel<4>, grid, 4 * kWaveSize, a);
+        launch_async(stream, attention_decode_partial_kernel<4, kSub>, grid, kSub * 4 * kWaveSize, a);
     else if (rep <= 8)
-        launch_async(stream, attention_decode_partial_kernel<8>, grid, 8 * kWaveSize, a);
+        launch_async(stream, attention_decode_partial_kernel<8, kSub>, grid, kSub * 8 * kWaveSize, a);
+    else if constexpr (kSub == 1)
+        launch_async(stream, attention_decode_partial_kernel<16, 1>, grid, 16 * kWaveSize, a);
     else
-        launch_async(stream, attention_decode_partial_kernel<16>, grid, 16 * kWaveSize, a);
+        throw std::invalid_argument("attention_decode: chunk pairs need at most 8 q heads per kv head");
+}
+
+inline void attention_decode_launch(const DecodeAttnArgs &a, int kvh, hipStream_t stream) {
+    require(a.chunks_per_record == decode_chunks_per_record(a.kv_rep, a.max_chunks),
+            "attention_decode: chunks per record must follow decode_chunks_per_record");
+    if (a.chunks_per_record == 2)
+        attention_decode_launch_sub<2>(a, kvh, stream);
+    else
+        attention_decode_launch_sub<1>(a, kvh, stream);
     if (!a.counters)
-        launch_async(stream, attention_decode_combine_kernel, kvh, rep * kWaveSize, a);
+        launch_async(stream, attention_decode_combine_kernel, kvh, a.kv_rep * kWaveSize, a);
 }
 
 } // namespace opworks::detail
@@ -863,6 +919,7 @@ inline void attention_decode_enqueue(const float *q, const float *kcache, const 
     a.D = head_dim;
     a.cap = max_seq;
     a.max_chunks = max_chunks;
+    a.chunks_per_record = decode_chunks_per_record(kv_rep, max_chunks);
     a.scale = 1.f / std::sqrt(static_cast<float>(head_dim));
     attention_decode_launch(a, num_q_heads / kv_rep, stream);
 }
