@@ -146,8 +146,10 @@ def test_decode_head_shapes(ow, orc, qh, kv_rep, D, length):
     assert np.array_equal(fused.to_host().view(np.uint32), out.to_host().view(np.uint32))
 
 
-@pytest.mark.parametrize("length,cap", [(1, 1), (2, 8), (63, 64), (64, 64), (65, 128), (767, 1024), (2048, 2048),
-                                        (8192, 8192)])
+# 1025 and 1600 keys: 17 and 25 chunks, past 16 records per head, so two chunks per workgroup with the
+# second chunk of the last pair past the length (1025) or partial (1600)
+@pytest.mark.parametrize("length,cap", [(1, 1), (2, 8), (63, 64), (64, 64), (65, 128), (767, 1024), (1025, 2048),
+                                        (1600, 1664), (2048, 2048), (8192, 8192)])
 @pytest.mark.parametrize("use_ws", [False, True])
 def test_decode_matches_oracle(ow, orc, length, cap, use_ws):
     qh, kv_rep, D = 32, 4, 64
@@ -169,7 +171,7 @@ def test_decode_matches_oracle(ow, orc, length, cap, use_ws):
 
 
 @pytest.mark.parametrize("kv_rep", [1, 2, 3, 4, 8, 16])
-@pytest.mark.parametrize("length", [1, 63, 64, 65, 1024, 8192])
+@pytest.mark.parametrize("length", [1, 63, 64, 65, 1024, 1025, 1600, 8192])
 def test_decode_fused_merge_matches_two_kernels(ow, orc, kv_rep, length):
     """The one-launch form (the last chunk workgroup of each kv head merges the head group's records,
     read back with agent-coherent loads after an agent-scope counter) against the two-kernel form
