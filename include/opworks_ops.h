@@ -169,11 +169,14 @@ int opw_argmax_f32(const float *x, int n, int *out, void *stream);
 /* ---- kernels behind the Scan / Transform / GatherScatter builders. The reference builders
  *      carry only the operation metadata (include/builders/scan.cuh:7-43, transform.cuh:7-38,
  *      gather_scatter.cuh:7-36) and leave the kernel to their apply() callback. ---- */
-/* Floats of workspace opw_scan_f32 needs for n elements (0 up to 8192); 16-byte aligned. */
+/* Floats of workspace opw_scan_f32 needs for n elements (0 up to 8192); 16-byte aligned.
+ * Its contents on entry do not matter; word 1 holds the number of timed-out waits of the
+ * last scan that used it (0 unless the scan is broken). */
 int opw_scan_workspace_size(int n);
 /* op: 0 = sum, 1 = maximum (fmaxf, identity -inf); inclusive: 1 = out[i] covers x[0..i],
  * 0 = x[0..i-1] with out[0] = identity. In place (out == in) is allowed. workspace == NULL
- * selects the stream-ordered-allocation convenience overload. */
+ * selects the stream-ordered-allocation convenience overload. Scans sharing a workspace
+ * must not run concurrently. */
 int opw_scan_f32(const float *in, float *out, int n, int op, int inclusive, float *workspace, int workspace_size,
                  void *stream);
 /* out [cols][rows] = transpose of in [rows][cols]; not in place. */

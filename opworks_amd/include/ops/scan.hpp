@@ -10,22 +10,32 @@
 // ScanOp::maximum; fmaxf drops NaN operands, so a prefix of NaNs alone scans
 // to -inf.
 //
-// gfx950 design: reduce-then-scan over tiles of kScanTile elements, three
-// launches, no atomics and no inter-workgroup waiting, so the result is the
-// same bit pattern on every run for a given n.
-//  1. scan_tile_reduce_kernel: workgroup b combines tile b -> partial[b].
-//  2. scan_partials_kernel: one workgroup turns partial[] into exclusive tile
-//     prefixes in place (each lane scans a contiguous run, then a workgroup
-//     scan of the run totals).
-//  3. scan_tile_kernel: workgroup b rescans tile b in four rounds of 2048
-//     contiguous elements: a lane scans its 16-byte pack, a wave scans the
-//     lane totals with DPP row shifts and row broadcasts, LDS carries the
-//     wave totals, and the tile prefix enters as the first operand.
-// Inputs of at most one tile take launch 3 alone and need no workspace.
-// The partial buffer must be 16-byte aligned (any hipMalloc'd workspace is).
-// HBM traffic is 12 B per element (two reads, one write) against 8 B of
-// compulsory traffic. In-place scans (out == in) are allowed: every element
-// is read by the lane that later writes it, before the write.
+// gfx950 design: one pass over tiles of kScanTile elements. Each workgroup
+// takes the next tile index from a counter (so every lower tile is already
+// running or done), loads its tile into registers, publishes the tile total,
+// then builds its tile prefix from totals published by lower tiles:
+//   prefix(t) = S(super groups before t's) (+) G(groups before t's in its
+//               super group) (+) T(tiles before t in its group),
+// with 64 tiles to a group and 64 groups to a super group. Each of the three
+// terms is one wave's inclusive scan over at most 64 published values, so
+// its association is fixed by the tile index alone: the result is the same
+// bit pattern on every run, whatever order the workgroups ran in. The last
+// tile of a group publishes the group total (a scan over its 64 tile totals)
+// and the last group's last tile the super-group total, so no tile waits on
+// a chain longer than three levels. Totals travel as 64-bit words holding the
+// value and a valid flag, written and read with agent-scope atomics (sc1
+// accesses, coherent across the XCDs' L2 caches). Every wait is on a lower
+// tile, bounded, and counts a timeout into the workspace.
+//
+// A fill kernel clears the counter and the flags before each scan, so the
+// workspace can be any caller memory. The tile then rescans its elements in
+// four rounds of 2048 contiguous elements: a lane scans its 16-byte pack, a
+// wave scans the lane totals with DPP row shifts and row broadcasts, LDS
+// carries the wave totals, and the tile prefix enters as the first operand.
+// Inputs of at most one tile take a single workgroup and need no workspace.
+// HBM traffic is 8 B per element (one read, one write), the compulsory
+// amount. In-place scans (out == in) are allowed: every element is read by
+// the lane that later writes it, before the write.
 
 #include <cmath>
 
@@ -40,8 +50,6 @@ constexpr int kScanThreads = 512;
 constexpr int kScanRounds = 4;
 constexpr int kScanRound = kScanThreads * 4;           // elements per round (2048)
 constexpr int kScanTile = kScanRound * kScanRounds;    // elements per workgroup (8192)
-constexpr int kScanPartialThreads = 1024;
-constexpr int kScanPartialBatch = 4;                   // 16-byte packs a lane loads per round trip
 
 struct ScanSumOp {
     static __device__ __forceinline__ float identity() { return 0.f; }
@@ -89,111 +97,78 @@ __device__ __forceinline__ f32x4 scan_load(const float *in, int64_t e, int64_t n
     return v;
 }
 
-template <typename Op, bool kPacked>
-__global__ __launch_bounds__(kScanThreads) void scan_tile_reduce_kernel(const float *__restrict__ in,
-                                                                        float *__restrict__ partial, int64_t n) {
-    const int64_t base = int64_t(blockIdx.x) * kScanTile + 4 * threadIdx.x;
-    f32x4 v[kScanRounds];
-#pragma unroll
-    for (int r = 0; r < kScanRounds; ++r)
-        v[r] = scan_load<Op, kPacked>(in, base + int64_t(r) * kScanRound, n);
-    float acc = Op::identity();
-#pragma unroll
-    for (int r = 0; r < kScanRounds; ++r)
-        acc = Op::combine(acc, Op::combine(Op::combine(v[r][0], v[r][1]), Op::combine(v[r][2], v[r][3])));
-    acc = wave::reduce(acc, Op::identity(), [](float a, float b) { return Op::combine(a, b); });
-    __shared__ float totals[kScanThreads / kWaveSize];
-    const int wid = threadIdx.x / kWaveSize;
-    if (threadIdx.x % kWaveSize == 0)
-        totals[wid] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float t = Op::identity();
-#pragma unroll
-        for (int w = 0; w < kScanThreads / kWaveSize; ++w)
-            t = Op::combine(t, totals[w]);
-        partial[blockIdx.x] = t;
+inline int scan_tile_count(int n) { return static_cast<int>(blocks_for64(n, kScanTile)); }
+
+// Workspace, in 32-bit words from a 16-byte aligned base: word 0 the tile
+// counter, word 1 the count of waits that timed out (both on a 256-byte line
+// of their own), then the tile totals, the group totals and the super-group
+// totals, one 64-bit word each: value bits in the low half, 1 in the high
+// half once published, 0 while not.
+constexpr int kScanGroup = 64;          // tiles per group, groups per super group
+constexpr int kScanHeaderWords = 64;
+constexpr int kScanSpinLimit = 1 << 18; // polls before a wait gives up (a fraction of a second)
+
+struct ScanLayout {
+    int tiles, groups, supers;
+    __host__ __device__ int64_t words() const { return kScanHeaderWords + 2 * (int64_t(tiles) + groups + supers); }
+};
+
+inline ScanLayout scan_layout(int n) {
+    const int tiles = scan_tile_count(n);
+    const int groups = (tiles + kScanGroup - 1) / kScanGroup;
+    return {tiles, groups, (groups + kScanGroup - 1) / kScanGroup};
+}
+
+__device__ __forceinline__ uint64_t scan_publishable(float v) {
+    return (uint64_t(1) << 32) | __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ void scan_publish(uint64_t *slot, float v) {
+    __hip_atomic_store(slot, scan_publishable(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls a published total of a lower tile (agent-coherent 64-bit loads, so the value and its
+// flag arrive together). A wait that outlasts kScanSpinLimit polls counts itself in `timeouts`
+// and returns NaN, so a broken protocol ends the kernel and shows in the output.
+__device__ __forceinline__ float scan_wait_total(const uint64_t *slot, uint32_t *timeouts) {
+    for (int spin = 0;; ++spin) {
+        const uint64_t w = __hip_atomic_load(const_cast<uint64_t *>(slot), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (w >> 32)
+            return __builtin_bit_cast(float, uint32_t(w));
+        if (spin == kScanSpinLimit) {
+            __hip_atomic_fetch_add(timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return __builtin_nanf("");
+        }
+        __builtin_amdgcn_s_sleep(2);
     }
 }
 
-// partial[0..count) -> exclusive prefixes, in place. Lane t owns the
-// contiguous run [t * per, (t + 1) * per) with per a multiple of 4, which it
-// reads as 16-byte packs, kScanPartialBatch per round trip, and keeps in
-// registers between the run total and the rewrite.
-template <typename Op>
-__global__ __launch_bounds__(kScanPartialThreads) void scan_partials_kernel(float *__restrict__ partial, int count) {
-    constexpr int kWaves = kScanPartialThreads / kWaveSize;
-    constexpr int kPer = 4 * kScanPartialBatch;
-    const int per = ((count + kScanPartialThreads - 1) / kScanPartialThreads + 3) / 4 * 4;
-    const int begin = threadIdx.x * per;
-    const int end = begin + per < count ? begin + per : count;
-    auto load_batch = [&](int b, f32x4 *v) {
-#pragma unroll
-        for (int j = 0; j < kScanPartialBatch; ++j) {
-            const int i = b + 4 * j;
-            if (i + 4 <= end) {
-                v[j] = *reinterpret_cast<const f32x4 *>(partial + i);
-            } else {
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    v[j][k] = i + k < end ? partial[i + k] : Op::identity();
-            }
-        }
-    };
-    float run = Op::identity();
-    for (int b = begin; b < end; b += kPer) {
-        f32x4 v[kScanPartialBatch];
-        load_batch(b, v);
-#pragma unroll
-        for (int j = 0; j < kScanPartialBatch; ++j)
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                run = Op::combine(run, v[j][k]);
-    }
-    const float incl = wave_inclusive_scan<Op>(run);
-    const float excl = wave_shift_up<Op>(incl);
-    __shared__ float wave_tot[kWaves];
-    const int wid = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
-    if (lane == kWaveSize - 1)
-        wave_tot[wid] = incl;
-    __syncthreads();
-    float prefix = Op::identity();
-    for (int w = 0; w < wid; ++w)
-        prefix = Op::combine(prefix, wave_tot[w]);
-    prefix = Op::combine(prefix, excl);
-    for (int b = begin; b < end; b += kPer) {
-        f32x4 v[kScanPartialBatch];
-        load_batch(b, v);
-#pragma unroll
-        for (int j = 0; j < kScanPartialBatch; ++j) {
-            const int i = b + 4 * j;
-            f32x4 y;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                y[k] = prefix;
-                prefix = Op::combine(prefix, v[j][k]);
-            }
-            if (i + 4 <= end) {
-                *reinterpret_cast<f32x4 *>(partial + i) = y;
-            } else {
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    if (i + k < end)
-                        partial[i + k] = y[k];
-            }
-        }
-    }
+// Zeroes `quads` 16-byte words of the workspace: the counter, the timeout count and every flag.
+__global__ __launch_bounds__(256) static void scan_clear_kernel(uint4 *ws, int64_t quads) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i < quads)
+        ws[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
-// `tile_prefix` is null for a single-tile scan (prefix = identity).
-template <typename Op, bool kPacked, bool kInclusive>
-__global__ __launch_bounds__(kScanThreads) void scan_tile_kernel(const float *in, float *out,
-                                                                 const float *__restrict__ tile_prefix, int64_t n) {
+// One workgroup per tile. kOnePass = false: the single-tile scan (tile 0, no workspace).
+template <typename Op, bool kPacked, bool kInclusive, bool kOnePass>
+__global__ __launch_bounds__(kScanThreads) void scan_kernel(const float *in, float *out, uint32_t *ws,
+                                                            ScanLayout lay, int64_t n) {
     constexpr int kWaves = kScanThreads / kWaveSize;
     __shared__ float wave_tot[kScanRounds][kWaves];
-    const int wid = threadIdx.x / kWaveSize;
-    const int64_t tile = int64_t(blockIdx.x) * kScanTile;
-    float carry = tile_prefix ? tile_prefix[blockIdx.x] : Op::identity();
+    __shared__ float level[3]; // exclusive prefixes over super groups, groups, tiles
+    __shared__ float own_group_total;
+    __shared__ int tile_id;
+    const int wid = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
+    int t = 0;
+    if constexpr (kOnePass) {
+        if (threadIdx.x == 0)
+            tile_id = __hip_atomic_fetch_add(reinterpret_cast<int *>(ws), 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        t = tile_id;
+    }
+    const int64_t tile = int64_t(t) * kScanTile;
     f32x4 x[kScanRounds];
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r)
@@ -209,10 +184,57 @@ __global__ __launch_bounds__(kScanThreads) void scan_tile_kernel(const float *in
         s[r][3] = Op::combine(s[r][2], x[r][3]);
         const float incl = wave_inclusive_scan<Op>(s[r][3]);
         lane_excl[r] = wave_shift_up<Op>(incl);
-        if (threadIdx.x % kWaveSize == kWaveSize - 1)
+        if (lane == kWaveSize - 1)
             wave_tot[r][wid] = incl;
     }
     __syncthreads();
+    float carry = Op::identity();
+    if constexpr (kOnePass) {
+        // The tile total in a fixed order (rounds, then waves), published at once.
+        float total = Op::identity();
+#pragma unroll
+        for (int r = 0; r < kScanRounds; ++r)
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w)
+                total = Op::combine(total, wave_tot[r][w]);
+        uint64_t *tile_tot = reinterpret_cast<uint64_t *>(ws + kScanHeaderWords);
+        uint64_t *group_tot = tile_tot + lay.tiles;
+        uint64_t *super_tot = group_tot + lay.groups;
+        uint32_t *timeouts = ws + 1;
+        if (threadIdx.x == 0)
+            scan_publish(tile_tot + t, total);
+        const int g = t / kScanGroup, j = t % kScanGroup, sg = g / kScanGroup, gj = g % kScanGroup;
+        const bool closes_group = j == kScanGroup - 1, closes_super = closes_group && gj == kScanGroup - 1;
+        // Waves 0, 1, 2 scan the totals of the lower tiles in this group, the lower groups in this
+        // super group and the lower super groups. Lane 63 of wave 0 carries this tile's own total,
+        // which completes the group total when this is the group's last tile.
+        float v = Op::identity();
+        if (wid < 3) {
+            const uint64_t *src = wid == 0 ? tile_tot + int64_t(g) * kScanGroup
+                                  : wid == 1 ? group_tot + int64_t(sg) * kScanGroup
+                                             : super_tot;
+            const int count = wid == 0 ? j : wid == 1 ? gj : sg;
+            if (lane < count)
+                v = scan_wait_total(src + lane, timeouts);
+            if (wid == 0 && lane == kWaveSize - 1)
+                v = total;
+            const float incl = wave_inclusive_scan<Op>(v);
+            const float before = count == 0 ? Op::identity() : wave::readlane(incl, count - 1);
+            if (lane == 0)
+                level[wid] = before;
+            if (wid == 0 && closes_group && lane == kWaveSize - 1) {
+                scan_publish(group_tot + g, incl);
+                own_group_total = incl;
+            }
+        }
+        __syncthreads();
+        if (closes_super && wid == 1) {
+            const float incl = wave_inclusive_scan<Op>(lane == kWaveSize - 1 ? own_group_total : v);
+            if (lane == kWaveSize - 1)
+                scan_publish(super_tot + sg, incl);
+        }
+        carry = Op::combine(Op::combine(level[2], level[1]), level[0]);
+    }
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
         float before = carry, round_total = carry;
@@ -247,50 +269,53 @@ __global__ __launch_bounds__(kScanThreads) void scan_tile_kernel(const float *in
     }
 }
 
-inline int scan_tile_count(int n) { return static_cast<int>(blocks_for64(n, kScanTile)); }
-
 template <typename Op, bool kPacked, bool kInclusive>
-void scan_launch(const float *in, float *out, int n, float *partial, hipStream_t stream) {
-    const int tiles = scan_tile_count(n);
-    if (tiles <= 1) {
-        launch_async(stream, scan_tile_kernel<Op, kPacked, kInclusive>, 1, kScanThreads, in, out,
-                     static_cast<const float *>(nullptr), static_cast<int64_t>(n));
+void scan_launch(const float *in, float *out, int n, float *workspace, hipStream_t stream) {
+    const ScanLayout lay = scan_layout(n);
+    if (lay.tiles <= 1) {
+        launch_async(stream, scan_kernel<Op, kPacked, kInclusive, false>, 1, kScanThreads, in, out,
+                     static_cast<uint32_t *>(nullptr), lay, static_cast<int64_t>(n));
         return;
     }
-    launch_async(stream, scan_tile_reduce_kernel<Op, kPacked>, tiles, kScanThreads, in, partial,
+    uint32_t *ws = reinterpret_cast<uint32_t *>(workspace);
+    const int64_t quads = (lay.words() + 3) / 4;
+    launch_async(stream, scan_clear_kernel, static_cast<int>(blocks_for64(quads, 256)), 256,
+                 reinterpret_cast<uint4 *>(ws), quads);
+    launch_async(stream, scan_kernel<Op, kPacked, kInclusive, true>, lay.tiles, kScanThreads, in, out, ws, lay,
                  static_cast<int64_t>(n));
-    launch_async(stream, scan_partials_kernel<Op>, 1, kScanPartialThreads, partial, tiles);
-    launch_async(stream, scan_tile_kernel<Op, kPacked, kInclusive>, tiles, kScanThreads, in, out,
-                 static_cast<const float *>(partial), static_cast<int64_t>(n));
 }
 
 template <typename Op>
-void scan_dispatch(const float *in, float *out, int n, bool inclusive, float *partial, hipStream_t stream) {
+void scan_dispatch(const float *in, float *out, int n, bool inclusive, float *workspace, hipStream_t stream) {
     const bool packed = aligned16(in) && aligned16(out);
     if (packed && inclusive)
-        scan_launch<Op, true, true>(in, out, n, partial, stream);
+        scan_launch<Op, true, true>(in, out, n, workspace, stream);
     else if (packed)
-        scan_launch<Op, true, false>(in, out, n, partial, stream);
+        scan_launch<Op, true, false>(in, out, n, workspace, stream);
     else if (inclusive)
-        scan_launch<Op, false, true>(in, out, n, partial, stream);
+        scan_launch<Op, false, true>(in, out, n, workspace, stream);
     else
-        scan_launch<Op, false, false>(in, out, n, partial, stream);
+        scan_launch<Op, false, false>(in, out, n, workspace, stream);
 }
 
 } // namespace opworks::detail
 
 namespace opworks::ops {
 
-// Workspace size in floats: one per 8192-element tile, 0 for a single tile.
+// Workspace size in floats (32-bit words): 0 for a single tile of 8192
+// elements, else a 64-word header plus two words per tile, per group of 64
+// tiles and per super group of 4096 tiles, rounded up to a 16-byte multiple.
+// Its contents on entry do not matter: each scan clears what it uses.
 inline int scan_workspace_size(int n) {
     detail::validate_size(n);
-    const int tiles = detail::scan_tile_count(n);
-    return tiles <= 1 ? 0 : tiles;
+    const detail::ScanLayout lay = detail::scan_layout(n);
+    return lay.tiles <= 1 ? 0 : static_cast<int>((lay.words() + 3) / 4 * 4);
 }
 
 // Allocation-free asynchronous path; capturable into a HIP graph. `maximum`
 // selects the prefix maximum, else the prefix sum. The workspace must stay
-// alive until the stream completes and must not overlap the input or output.
+// alive until the stream completes and must not overlap the input or output;
+// scans that share a workspace must not run at the same time.
 inline void scan(const float *in, float *out, int n, bool maximum, bool inclusive, DeviceSpan<float> workspace,
                  hipStream_t stream = nullptr) {
     const int need = scan_workspace_size(n);

@@ -101,6 +101,28 @@ def test_scan_in_place_and_deterministic(ow, orc):
     assert np.array_equal(bits(d.to_host()), bits(first))
 
 
+def test_scan_levels_and_stale_workspace_exact(ow):
+    """The one-pass protocol across a second super group of tiles (4096 tiles each), ending in a
+    partial group and a partial tile, on a workspace whose every flag starts set: x[i] = (i mod 3) - 1
+    has prefix sums of -1 or 0 in any order, so every output is checked bit for bit, and a tile given
+    a wrong or stale prefix shows up. The second call reuses the first call's workspace contents."""
+    n = (1 << 25) + 3 * 64 * 8192 + 100
+    i = np.arange(n, dtype=np.int64)
+    x = (i % 3 - 1).astype(np.float32)
+    d = upload(ow, x)
+    out = ow.DeviceBuffer.empty(n)
+    ws_n = ow.ops.scan_workspace_size(n)
+    ws = upload(ow, np.full(ws_n, -1, np.int32), dtype=np.int32)
+    for inclusive in (True, False, True):
+        ow.ops.scan(d, out, n, "sum", inclusive, ws, ws_n)
+        want = np.where((i + (1 if inclusive else 0)) % 3 == 0, 0.0, -1.0).astype(np.float32)
+        assert np.array_equal(out.to_host(), want), inclusive
+        assert ws.to_host()[1] == 0  # no wait timed out
+    ow.ops.scan(d, out, n, "maximum", True, ws, ws_n)
+    got = out.to_host()
+    assert np.array_equal(got[:3], np.array([-1, 0, 1], np.float32)) and np.all(got[2:] == 1.0)
+
+
 def test_scan_full_size_bound(ow, orc):
     """2^26 elements (8192 tiles, the multi-level path at scale) within the bar."""
     n = 1 << 26
