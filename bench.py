@@ -123,7 +123,8 @@ def roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) 
             "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
-TRAFFIC_FILES = (ROOT / "profiles" / "llama_decode_traffic.md", ROOT / "profiles" / "stream_ops_traffic.md")
+TRAFFIC_FILES = (ROOT / "profiles" / "llama_decode_traffic.md", ROOT / "profiles" / "stream_ops_traffic.md",
+                 ROOT / "profiles" / "scan_transpose_gather_traffic.md")
 
 
 def profiled_traffic(stage: str):
@@ -400,7 +401,7 @@ def wl_scan(stream, steps, warmup):
     gbs = nbytes / ms / 1e6
     return {"workload": "scan_sum_inclusive_n2^28", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
             "moved_bytes": 8 * n, "kernel": "scan_clear_kernel+scan_kernel",
-            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("scan"))}
 
 
 def wl_transpose(stream, steps, warmup):
@@ -413,7 +414,8 @@ def wl_transpose(stream, steps, warmup):
     nbytes = 8 * rows * cols
     gbs = nbytes / ms / 1e6
     return {"workload": "transpose_8192x8192", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
-            "kernel": "transpose_kernel<true>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+            "kernel": "transpose_kernel<true>",
+            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("transpose"))}
 
 
 def wl_gather(stream, steps, warmup):
@@ -429,7 +431,8 @@ def wl_gather(stream, steps, warmup):
     nbytes = 12 * n
     gbs = nbytes / ms / 1e6
     return {"workload": "gather_random_permutation_n2^26", "unit": "GB/s", "value": gbs, "ms": ms,
-            "bytes": nbytes, "kernel": "gather_kernel<true>", "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+            "bytes": nbytes, "kernel": "gather_kernel<true>",
+            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("gather"))}
 
 
 WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "layernorm": wl_layernorm, "gemm": wl_gemm, "gemm_bf16": wl_gemm_bf16, "attention": wl_attention,
