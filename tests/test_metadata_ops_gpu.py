@@ -101,12 +101,17 @@ def test_scan_in_place_and_deterministic(ow, orc):
     assert np.array_equal(bits(d.to_host()), bits(first))
 
 
-def test_scan_levels_and_stale_workspace_exact(ow):
-    """The one-pass protocol across a second super group of tiles (4096 tiles each), ending in a
-    partial group and a partial tile, on a workspace whose every flag starts set: x[i] = (i mod 3) - 1
-    has prefix sums of -1 or 0 in any order, so every output is checked bit for bit, and a tile given
-    a wrong or stale prefix shows up. The second call reuses the first call's workspace contents."""
-    n = (1 << 25) + 3 * 64 * 8192 + 100
+TILE = 8192  # elements per scan tile; 64 tiles make a group, 64 groups a super group
+
+
+@pytest.mark.parametrize("n", [2 * TILE, 64 * TILE, 64 * TILE + 1, 65 * TILE - 3, 4096 * TILE, 4096 * TILE + 1,
+                               (1 << 25) + 3 * 64 * TILE + 100])
+def test_scan_levels_and_stale_workspace_exact(ow, n):
+    """The one-pass protocol at each level's edges (exactly one group or super group of tiles and
+    one element past it) and across a second super group ending in a partial group and a partial
+    tile, on a workspace whose every flag starts set: x[i] = (i mod 3) - 1 has prefix sums of -1 or 0
+    in any order, so every output is checked bit for bit, and a tile given a wrong or stale prefix
+    shows up. Later calls reuse the earlier calls' workspace contents."""
     i = np.arange(n, dtype=np.int64)
     x = (i % 3 - 1).astype(np.float32)
     d = upload(ow, x)
