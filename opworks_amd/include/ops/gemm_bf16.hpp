@@ -10,15 +10,21 @@
 //  * workgroup tile 256 x 256, 512 threads = 8 waves in 2 x 4; each wave owns
 //    128 x 64 = 4 x 2 v_mfma_f32_32x32x16_bf16 tiles (128 accumulator
 //    registers);
-//  * K tile 64 (147 KB of LDS, one workgroup per CU); fp32 A is staged raw
-//    (twice the registers of bf16) and rounded when written to LDS;
+//  * K tile 64 (128 KB of LDS with bf16 A, 144 KB with fp32 A; one workgroup
+//    per CU);
 //  * an MFMA operand is 8 consecutive k of one row per lane, so both operands
-//    keep their k-contiguous global layout in LDS; rows are padded by 16 bytes,
-//    which puts the 16-byte reads of consecutive rows on disjoint bank groups;
-//  * LDS double buffered, next tile's global loads issued before the current
-//    tile's MFMAs and staged into LDS halfway through them, one barrier per K
-//    tile; inside a tile the next MFMA step's fragments are read while the
-//    current step's MFMAs run; same XCD-banded tile order as the fp32 kernel.
+//    keep their k-contiguous global layout in LDS; the reads of eight
+//    consecutive rows fall on disjoint bank groups, by XOR-swizzled 16-byte
+//    chunks (chunk c of row r in slot c ^ (r & 7)) where loads go straight to
+//    LDS and by 16 bytes of row padding where they are staged in registers;
+//  * with bf16 A both operands go from global memory straight into LDS
+//    (gfx950 global_load_lds_dwordx4, no register staging); with fp32 A both
+//    are loaded into registers (A raw, rounded when written to LDS) and
+//    stored halfway through the current tile's MFMAs;
+//  * LDS double buffered, the next tile's loads issued before the current
+//    tile's MFMAs, one barrier per K tile; inside a tile the next MFMA step's
+//    fragments are read while the current step's MFMAs run; same XCD-banded
+//    tile order as the fp32 kernel.
 
 #include <cstdint>
 
@@ -35,6 +41,15 @@ using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 constexpr int kBfBM = 256, kBfBN = 256;
 constexpr int kBfBK = 32; // K granularity of split-K planning (the smaller of the two K tiles)
 constexpr int kBfThreads = 512;
+// s_waitcnt operand (gfx9 encoding) for vmcnt(0) with expcnt and lgkmcnt at their maxima: waits
+// until every vector memory access of the wave, direct-to-LDS loads included, has completed.
+constexpr int kGemmWaitVmcnt0 = 0x0F70;
+
+// 16 bytes per lane from global memory straight into LDS (gfx950 global_load_lds_dwordx4): lane l
+// of the wave writes lds_block + 16 l, whatever address it loads from.
+__device__ __forceinline__ void load_lds16(const void *src, void *lds_block) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_block, 16, 0, 0);
+}
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return static_cast<uint32_t>(float_to_bf16_rne(lo)) | (static_cast<uint32_t>(float_to_bf16_rne(hi)) << 16);
@@ -49,10 +64,19 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     static_assert(std::is_same_v<TA, float> || std::is_same_v<TA, uint16_t>, "A is fp32 or bf16 bits");
     constexpr bool kF32A = std::is_same_v<TA, float>;
     constexpr int BK = 64; // against 32: 945 -> 1013-1030 TFLOP/s (bf16 A), 512-token bf16 TTFT 4.5 -> 4.05 ms
-    constexpr int kLd = BK + 8;                        // bf16 elements per padded LDS row
+    // Both operands go straight from global memory into LDS (gfx950 global_load_lds_dwordx4)
+    // on the vector path with bf16 A. With fp32 A, which is rounded on the way in registers,
+    // and on the scalar path both are staged through registers.
+    constexpr bool kDirect = kVec && !kF32A;
+    // LDS rows: a direct load writes 1 KB of consecutive bytes, so its rows are unpadded, with
+    // chunk c of row r in slot c ^ (r & 7): the 16-byte reads of eight consecutive rows at one k
+    // land on eight different bank groups. Register staging pads each row by 16 bytes instead,
+    // which does the same and keeps every read offset a compile-time constant (the swizzle took
+    // the fp32-A kernel past 256 registers).
+    constexpr int kRowE = kDirect ? BK : BK + 8;       // bf16 elements per LDS row
     constexpr int kCPR = BK / 8;                       // 16-byte chunks (8 k) per tile row
     constexpr int kPer = kBfBM * kCPR / kBfThreads;    // chunks per thread per operand
-    constexpr int kStage = (kBfBM + kBfBN) * kLd;      // uint16 elements per stage
+    constexpr int kStage = (kBfBM + kBfBN) * kRowE;    // uint16 elements per stage
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kStage];
 
     const int tiles_m = (M + kBfBM - 1) / kBfBM, tiles_n = (N + kBfBN - 1) / kBfBN;
@@ -62,12 +86,21 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     const int tid = threadIdx.x, lane = tid % kWaveSize, wave = tid / kWaveSize;
     const int wm = wave / 4, wn = wave % 4; // 2 x 4 waves
     const int l32 = lane % 32, half = lane / 32;
+    // The compiler does not count direct loads as writes to the array: without a store it may
+    // treat the array as never written and drop the reads. This one never runs (M >= 0).
+    if (kDirect && M < 0)
+        lds[tid] = 0;
 
-    // Staging: each operand tile is 256 rows x BK k in chunks of 8 k, kPer chunks per thread.
-    // The vector path loads unconditionally from clamped addresses into raw registers (fp32 A
-    // is rounded to bf16 only when staged): a load under a branch makes the compiler wait for
-    // every load in flight before the next one. Rows past M or N then hold copies of the last
-    // row, which only feed outputs that are not stored; the K tail is zeroed when staged.
+    auto swz = [](int row, int chunk) {
+        return row * kRowE + ((kDirect ? chunk ^ (row & 7) : chunk) << 3);
+    };
+
+    // Register staging: chunk tid + kBfThreads * i of each operand tile (256 rows x BK k),
+    // row (tid + kBfThreads * i) / kCPR. The vector path loads unconditionally from clamped
+    // addresses into raw registers (fp32 A is rounded to bf16 only when staged): a load under
+    // a branch makes the compiler wait for every load in flight before the next one. Rows past
+    // M or N then hold copies of the last row, which only feed outputs that are not stored; the
+    // K tail is zeroed when staged.
     using AStage = std::conditional_t<kF32A, f32x4, u32x4>;
     constexpr int kAParts = kF32A ? 2 : 1;
     AStage ra[kPer][kAParts];
@@ -82,7 +115,8 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
         return u32x4{e[0] | (uint32_t(e[1]) << 16), e[2] | (uint32_t(e[3]) << 16), e[4] | (uint32_t(e[5]) << 16),
                      e[6] | (uint32_t(e[7]) << 16)};
     };
-    auto global_load = [&](int kt) {
+    // Register loads of tile kt: operand A unless with_a is false, operand B if with_b.
+    auto global_load = [&](int kt, bool with_a, bool with_b) {
         const int k0 = kt * BK;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
@@ -90,29 +124,35 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
             if constexpr (kVec) {
                 const int ar = m0 + r < M ? m0 + r : M - 1, br = n0 + r < N ? n0 + r : N - 1;
                 const int kc = k < K ? k : K - 8;
+                if (with_a) {
 #pragma unroll
-                for (int p = 0; p < kAParts; ++p)
-                    ra[i][p] = *reinterpret_cast<const AStage *>(A + int64_t(ar) * K + kc + 4 * p);
-                rb[i] = *reinterpret_cast<const u32x4 *>(W + int64_t(br) * K + kc);
-            } else {
-                if constexpr (kF32A) {
-#pragma unroll
-                    for (int p = 0; p < 2; ++p)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            const int kk = k + 4 * p + j;
-                            ra[i][p][j] = (m0 + r < M && kk < K) ? A[int64_t(m0 + r) * K + kk] : 0.f;
-                        }
-                } else {
-                    ra[i][0] = load_chunk_bf16(A, m0 + r, M, k);
+                    for (int p = 0; p < kAParts; ++p)
+                        ra[i][p] = *reinterpret_cast<const AStage *>(A + int64_t(ar) * K + kc + 4 * p);
                 }
-                rb[i] = load_chunk_bf16(W, n0 + r, N, k);
+                if (with_b)
+                    rb[i] = *reinterpret_cast<const u32x4 *>(W + int64_t(br) * K + kc);
+            } else {
+                if (with_a) {
+                    if constexpr (kF32A) {
+#pragma unroll
+                        for (int p = 0; p < 2; ++p)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) {
+                                const int kk = k + 4 * p + j;
+                                ra[i][p][j] = (m0 + r < M && kk < K) ? A[int64_t(m0 + r) * K + kk] : 0.f;
+                            }
+                    } else {
+                        ra[i][0] = load_chunk_bf16(A, m0 + r, M, k);
+                    }
+                }
+                if (with_b)
+                    rb[i] = load_chunk_bf16(W, n0 + r, N, k);
             }
         }
     };
-    auto lds_store = [&](int buf, int kt, bool zero_tail) {
+    auto lds_store = [&](int buf, int kt, bool zero_tail, bool with_a, bool with_b) {
         uint16_t *As = lds + buf * kStage;
-        uint16_t *Bs = As + kBfBM * kLd;
+        uint16_t *Bs = As + kBfBM * kRowE;
         const int k0 = kt * BK;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
@@ -130,9 +170,27 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
                     bv[j] = k < K ? bv[j] : 0u;
                 }
             }
-            const int off = chunk_row(i) * kLd + chunk_k(i);
-            *reinterpret_cast<u32x4 *>(As + off) = av;
-            *reinterpret_cast<u32x4 *>(Bs + off) = bv;
+            const int off = swz(chunk_row(i), chunk_k(i) / 8);
+            if (with_a)
+                *reinterpret_cast<u32x4 *>(As + off) = av;
+            if (with_b)
+                *reinterpret_cast<u32x4 *>(Bs + off) = bv;
+        }
+    };
+    // Direct loads of tile kt (full K tiles of the vector path): the wave's instruction i
+    // writes the 1 KB block of rows 8 * wave + 64 * i .. + 7, lane l at byte 16 l, i.e. row
+    // + l / 8, slot l % 8, which holds chunk (l % 8) ^ (l / 8) of that row.
+    const int d_row = lane >> 3, d_chunk = (lane & 7) ^ d_row;
+    auto direct_load = [&](int buf, int kt) {
+        const int k0 = kt * BK + 8 * d_chunk;
+        uint16_t *As = lds + buf * kStage;
+        uint16_t *Bs = As + kBfBM * kRowE;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int block = 8 * wave + 64 * i, r = block + d_row;
+            const int ar = m0 + r < M ? m0 + r : M - 1, br = n0 + r < N ? n0 + r : N - 1;
+            load_lds16(A + int64_t(ar) * K + k0, As + block * kRowE);
+            load_lds16(W + int64_t(br) * K + k0, Bs + block * kRowE);
         }
     };
 
@@ -151,19 +209,19 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     // 1019-1025 TFLOP/s).
     auto compute = [&](int buf, auto &&stage_next) {
         const uint16_t *As = lds + buf * kStage;
-        const uint16_t *Bs = As + kBfBM * kLd;
+        const uint16_t *Bs = As + kBfBM * kRowE;
         constexpr int kSteps = BK / 16;
         bf16x8 a[2][4], b[2][2];
         auto read = [&](int s, bf16x8 (&fa)[4], bf16x8 (&fb)[2]) {
-            const int kk = 16 * s + 8 * half;
+            const int ch = 2 * s + half; // k 16 s + 8 half .. + 7
 #pragma unroll
             for (int bm = 0; bm < 4; ++bm)
                 fa[bm] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                                        As + (wm * 128 + bm * 32 + l32) * kLd + kk));
+                                                        As + swz(wm * 128 + bm * 32 + l32, ch)));
 #pragma unroll
             for (int bn = 0; bn < 2; ++bn)
                 fb[bn] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                                        Bs + (wn * 64 + bn * 32 + l32) * kLd + kk));
+                                                        Bs + swz(wn * 64 + bn * 32 + l32, ch)));
         };
         read(0, a[0], b[0]);
 #pragma unroll
@@ -204,23 +262,43 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     // of the K tile) after the loop, with the tail zeroed; the scalar path bounds every element.
     const int kt_full = kVec ? (K / BK < kt_end ? (K / BK > kt_begin ? K / BK : kt_begin) : kt_end) : kt_end;
     if (kt_begin < kt_full) {
-        global_load(kt_begin);
-        lds_store(0, kt_begin, false);
+        // Each K tile: the next tile's loads are issued first (direct loads straight into the
+        // idle stage, or into registers, stored halfway through the MFMA steps), then the MFMAs,
+        // then every wave waits for its loads and the workgroup syncs once.
+        // (Direct loads against register staging: 129-132 -> 125-127 us at 4096^3, bf16 A.)
+        if constexpr (kDirect) {
+            direct_load(0, kt_begin);
+        } else {
+            global_load(kt_begin, true, true);
+            lds_store(0, kt_begin, false, true, true);
+        }
+        if constexpr (kDirect)
+            __builtin_amdgcn_s_waitcnt(kGemmWaitVmcnt0); // this wave's direct loads have landed
         __syncthreads();
         for (int kt = kt_begin; kt < kt_full; ++kt) {
             const int buf = (kt - kt_begin) & 1;
             // past the last tile: a reload of a valid tile, staged into the idle buffer
             const int next = kt + 1 < kt_full ? kt + 1 : kt;
-            global_load(next);
-            __builtin_amdgcn_sched_barrier(0); // the loads stay at the top, in flight during the MFMAs
             // the idle buffer was last read before the previous barrier
-            compute(buf, [&] { lds_store(buf ^ 1, next, false); });
+            if constexpr (kDirect)
+                direct_load(buf ^ 1, next);
+            else
+                global_load(next, true, true);
+            __builtin_amdgcn_sched_barrier(0); // the loads stay at the top, in flight during the MFMAs
+            compute(buf, [&] {
+                if constexpr (!kDirect)
+                    lds_store(buf ^ 1, next, false, true, true);
+            });
+            if constexpr (kDirect) {
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_waitcnt(kGemmWaitVmcnt0);
+            }
             __syncthreads();
         }
     }
-    if (kt_full < kt_end) { // the partial last K tile (vector path)
-        global_load(kt_full);
-        lds_store(0, kt_full, true);
+    if (kt_full < kt_end) { // the partial last K tile (vector path), staged through registers
+        global_load(kt_full, true, true);
+        lds_store(0, kt_full, true, true, true);
         __syncthreads();
         compute(0, [] {});
     }
