@@ -13,10 +13,11 @@
 //  * K tile 64 (128 KB of LDS with bf16 A, 144 KB with fp32 A; one workgroup
 //    per CU);
 //  * an MFMA operand is 8 consecutive k of one row per lane, so both operands
-//    keep their k-contiguous global layout in LDS; the reads of eight
+//    keep their k-contiguous global layout in LDS; the reads of 16
 //    consecutive rows fall on disjoint bank groups, by XOR-swizzled 16-byte
-//    chunks (chunk c of row r in slot c ^ (r & 7)) where loads go straight to
-//    LDS and by 16 bytes of row padding where they are staged in registers;
+//    chunks (chunk c of row r in slot c ^ ((r >> 1) & 7)) where loads go
+//    straight to LDS and by 16 bytes of row padding where they are staged in
+//    registers;
 //  * with bf16 A both operands go from global memory straight into LDS
 //    (gfx950 global_load_lds_dwordx4, no register staging); with fp32 A both
 //    are loaded into registers (A raw, rounded when written to LDS) and
@@ -69,10 +70,11 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     // and on the scalar path both are staged through registers.
     constexpr bool kDirect = kVec && !kF32A;
     // LDS rows: a direct load writes 1 KB of consecutive bytes, so its rows are unpadded, with
-    // chunk c of row r in slot c ^ (r & 7): the 16-byte reads of eight consecutive rows at one k
-    // land on eight different bank groups. Register staging pads each row by 16 bytes instead,
-    // which does the same and keeps every read offset a compile-time constant (the swizzle took
-    // the fp32-A kernel past 256 registers).
+    // chunk c of row r in slot c ^ ((r >> 1) & 7). The LDS serves 256 bytes a cycle, 16 lanes of
+    // a 16-byte read, and the reads of 16 consecutive rows at one k then fall on 16 different
+    // 16-byte bank groups (with c ^ (r & 7) they fell on 8, two lanes each). Register staging
+    // pads each row by 16 bytes instead (a 144-byte stride), which does the same and keeps every
+    // read offset a compile-time constant (the swizzle took the fp32-A kernel past 256 registers).
     constexpr int kRowE = kDirect ? BK : BK + 8;       // bf16 elements per LDS row
     constexpr int kCPR = BK / 8;                       // 16-byte chunks (8 k) per tile row
     constexpr int kPer = kBfBM * kCPR / kBfThreads;    // chunks per thread per operand
@@ -92,7 +94,7 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
         lds[tid] = 0;
 
     auto swz = [](int row, int chunk) {
-        return row * kRowE + ((kDirect ? chunk ^ (row & 7) : chunk) << 3);
+        return row * kRowE + ((kDirect ? chunk ^ ((row >> 1) & 7) : chunk) << 3);
     };
 
     // Register staging: chunk tid + kBfThreads * i of each operand tile (256 rows x BK k),
@@ -179,8 +181,9 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     };
     // Direct loads of tile kt (full K tiles of the vector path): the wave's instruction i
     // writes the 1 KB block of rows 8 * wave + 64 * i .. + 7, lane l at byte 16 l, i.e. row
-    // + l / 8, slot l % 8, which holds chunk (l % 8) ^ (l / 8) of that row.
-    const int d_row = lane >> 3, d_chunk = (lane & 7) ^ d_row;
+    // r = block + l / 8, slot l % 8, which holds chunk (l % 8) ^ ((r >> 1) & 7) of that row;
+    // (r >> 1) & 7 = (4 (wave & 1) + l / 16) & 7 for every i.
+    const int d_row = lane >> 3, d_chunk = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
     auto direct_load = [&](int buf, int kt) {
         const int k0 = kt * BK + 8 * d_chunk;
         uint16_t *As = lds + buf * kStage;
