@@ -388,8 +388,8 @@ def wl_llama(stream, steps, warmup, bf16=False, prompt_len=512, new_tokens=256, 
 
 def wl_scan(stream, steps, warmup):
     """ScanBuilder's kernel: inclusive prefix sum over n = 2^28 fp32. Algorithmic bytes 8 B/element (read x,
-    write out); the one-pass design moves the same 8, plus 16 B per 8192-element tile of published
-    totals and a 0.3 MB workspace clear."""
+    write out); the one-pass design moves the same 8, plus the published totals (8 B per
+    16384-element unit) and a small workspace clear."""
     n = 1 << 28
     x = ow.DeviceBuffer.empty(n)
     ow.fill_uniform(x, SEED, 3, -1.0, 1.0, stream=stream)
@@ -400,7 +400,7 @@ def wl_scan(stream, steps, warmup):
     nbytes = 8 * n
     gbs = nbytes / ms / 1e6
     return {"workload": "scan_sum_inclusive_n2^28", "unit": "GB/s", "value": gbs, "ms": ms, "bytes": nbytes,
-            "moved_bytes": 8 * n, "kernel": "scan_clear_kernel+scan_kernel",
+            "moved_bytes": 8 * n, "kernel": "scan_clear_kernel+scan_pair_kernel",
             "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("scan"))}
 
 

@@ -169,7 +169,7 @@ int opw_argmax_f32(const float *x, int n, int *out, void *stream);
 /* ---- kernels behind the Scan / Transform / GatherScatter builders. The reference builders
  *      carry only the operation metadata (include/builders/scan.cuh:7-43, transform.cuh:7-38,
  *      gather_scatter.cuh:7-36) and leave the kernel to their apply() callback. ---- */
-/* Floats of workspace opw_scan_f32 needs for n elements (0 up to 8192); 16-byte aligned.
+/* Floats of workspace opw_scan_f32 needs for n elements (0 up to 16384); 16-byte aligned.
  * Its contents on entry do not matter; word 1 holds the number of timed-out waits of the
  * last scan that used it (0 unless the scan is broken). */
 int opw_scan_workspace_size(int n);

@@ -30,6 +30,7 @@
 #include <cstdint>
 
 #include "../core/bf16.hpp"
+#include "../core/lds_direct.hpp"
 #include "../core/hip_utils.hpp"
 #include "elementwise.hpp"
 #include "gemm_f32.hpp"
@@ -42,15 +43,6 @@ using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 constexpr int kBfBM = 256, kBfBN = 256;
 constexpr int kBfBK = 32; // K granularity of split-K planning (the smaller of the two K tiles)
 constexpr int kBfThreads = 512;
-// s_waitcnt operand (gfx9 encoding) for vmcnt(0) with expcnt and lgkmcnt at their maxima: waits
-// until every vector memory access of the wave, direct-to-LDS loads included, has completed.
-constexpr int kGemmWaitVmcnt0 = 0x0F70;
-
-// 16 bytes per lane from global memory straight into LDS (gfx950 global_load_lds_dwordx4): lane l
-// of the wave writes lds_block + 16 l, whatever address it loads from.
-__device__ __forceinline__ void load_lds16(const void *src, void *lds_block) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_block, 16, 0, 0);
-}
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return static_cast<uint32_t>(float_to_bf16_rne(lo)) | (static_cast<uint32_t>(float_to_bf16_rne(hi)) << 16);
@@ -276,7 +268,7 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
             lds_store(0, kt_begin, false, true, true);
         }
         if constexpr (kDirect)
-            __builtin_amdgcn_s_waitcnt(kGemmWaitVmcnt0); // this wave's direct loads have landed
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0Only); // this wave's direct loads have landed
         __syncthreads();
         for (int kt = kt_begin; kt < kt_full; ++kt) {
             const int buf = (kt - kt_begin) & 1;
@@ -294,7 +286,7 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
             });
             if constexpr (kDirect) {
                 __builtin_amdgcn_sched_barrier(0);
-                __builtin_amdgcn_s_waitcnt(kGemmWaitVmcnt0);
+                __builtin_amdgcn_s_waitcnt(kWaitVmcnt0Only);
             }
             __syncthreads();
         }

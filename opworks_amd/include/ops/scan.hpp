@@ -10,29 +10,31 @@
 // ScanOp::maximum; fmaxf drops NaN operands, so a prefix of NaNs alone scans
 // to -inf.
 //
-// gfx950 design: one pass over tiles of kScanTile elements. Each workgroup
-// takes the next tile index from a counter (so every lower tile is already
-// running or done), loads its tile into registers, publishes the tile total,
-// then builds its tile prefix from totals published by lower tiles:
+// gfx950 design: one pass over units of elements: a pair of 8192-element
+// tiles when input and output are 16-byte aligned (one tile in registers, the
+// other loaded straight into LDS), else one tile. Each workgroup takes the
+// next unit index from a counter (so every lower unit is already running or
+// done), loads its unit, publishes the unit's total, then builds its prefix
+// from totals published by lower units:
 //   prefix(t) = S(super groups before t's) (+) G(groups before t's in its
-//               super group) (+) T(tiles before t in its group),
-// with 64 tiles to a group and 64 groups to a super group. Each of the three
+//               super group) (+) T(units before t in its group),
+// with 64 units to a group and 64 groups to a super group. Each of the three
 // terms is one wave's inclusive scan over at most 64 published values, so
-// its association is fixed by the tile index alone: the result is the same
+// its association is fixed by the unit index alone: the result is the same
 // bit pattern on every run, whatever order the workgroups ran in. The last
-// tile of a group publishes the group total (a scan over its 64 tile totals)
-// and the last group's last tile the super-group total, so no tile waits on
+// unit of a group publishes the group total (a scan over its 64 unit totals)
+// and the last group's last unit the super-group total, so no unit waits on
 // a chain longer than three levels. Totals travel as 64-bit words holding the
 // value and a valid flag, written and read with agent-scope atomics (sc1
 // accesses, coherent across the XCDs' L2 caches). Every wait is on a lower
-// tile, bounded, and counts a timeout into the workspace.
+// unit, bounded, and counts a timeout into the workspace.
 //
 // A fill kernel clears the counter and the flags before each scan, so the
-// workspace can be any caller memory. The tile then rescans its elements in
-// four rounds of 2048 contiguous elements: a lane scans its 16-byte pack, a
-// wave scans the lane totals with DPP row shifts and row broadcasts, LDS
-// carries the wave totals, and the tile prefix enters as the first operand.
-// Inputs of at most one tile take a single workgroup and need no workspace.
+// workspace can be any caller memory. A tile is then rescanned in four rounds
+// of 2048 contiguous elements: a lane scans its 16-byte pack, a wave scans
+// the lane totals with DPP row shifts and row broadcasts, LDS carries the
+// wave totals, and the prefix enters as the first operand. Inputs of at most
+// one unit take a single workgroup and need no workspace.
 // HBM traffic is 8 B per element (one read, one write), the compulsory
 // amount. In-place scans (out == in) are allowed: every element is read by
 // the lane that later writes it, before the write.
@@ -40,6 +42,7 @@
 #include <cmath>
 
 #include "../core/device_span.hpp"
+#include "../core/lds_direct.hpp"
 #include "../core/hip_utils.hpp"
 #include "../core/wave.hpp"
 #include "elementwise.hpp" // f32x4, aligned16
@@ -97,26 +100,24 @@ __device__ __forceinline__ f32x4 scan_load(const float *in, int64_t e, int64_t n
     return v;
 }
 
-inline int scan_tile_count(int n) { return static_cast<int>(blocks_for64(n, kScanTile)); }
-
-// Workspace, in 32-bit words from a 16-byte aligned base: word 0 the tile
+// Workspace, in 32-bit words from a 16-byte aligned base: word 0 the unit
 // counter, word 1 the count of waits that timed out (both on a 256-byte line
-// of their own), then the tile totals, the group totals and the super-group
+// of their own), then the unit totals, the group totals and the super-group
 // totals, one 64-bit word each: value bits in the low half, 1 in the high
 // half once published, 0 while not.
-constexpr int kScanGroup = 64;          // tiles per group, groups per super group
+constexpr int kScanGroup = 64;          // units per group, groups per super group
 constexpr int kScanHeaderWords = 64;
 constexpr int kScanSpinLimit = 1 << 18; // polls before a wait gives up (a fraction of a second)
 
 struct ScanLayout {
-    int tiles, groups, supers;
-    __host__ __device__ int64_t words() const { return kScanHeaderWords + 2 * (int64_t(tiles) + groups + supers); }
+    int units, groups, supers; // units: pairs of tiles
+    __host__ __device__ int64_t words() const { return kScanHeaderWords + 2 * (int64_t(units) + groups + supers); }
 };
 
-inline ScanLayout scan_layout(int n) {
-    const int tiles = scan_tile_count(n);
-    const int groups = (tiles + kScanGroup - 1) / kScanGroup;
-    return {tiles, groups, (groups + kScanGroup - 1) / kScanGroup};
+inline ScanLayout scan_pair_layout(int n) {
+    const int pairs = static_cast<int>(blocks_for64(n, 2 * kScanTile));
+    const int groups = (pairs + kScanGroup - 1) / kScanGroup;
+    return {pairs, groups, (groups + kScanGroup - 1) / kScanGroup};
 }
 
 __device__ __forceinline__ uint64_t scan_publishable(float v) {
@@ -150,32 +151,16 @@ __global__ __launch_bounds__(256) static void scan_clear_kernel(uint4 *ws, int64
         ws[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
-// One workgroup per tile. kOnePass = false: the single-tile scan (tile 0, no workspace).
-template <typename Op, bool kPacked, bool kInclusive, bool kOnePass>
-__global__ __launch_bounds__(kScanThreads) void scan_kernel(const float *in, float *out, uint32_t *ws,
-                                                            ScanLayout lay, int64_t n) {
-    constexpr int kWaves = kScanThreads / kWaveSize;
-    __shared__ float wave_tot[kScanRounds][kWaves];
-    __shared__ float level[3]; // exclusive prefixes over super groups, groups, tiles
-    __shared__ float own_group_total;
-    __shared__ int tile_id;
-    const int wid = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
-    int t = 0;
-    if constexpr (kOnePass) {
-        if (threadIdx.x == 0)
-            tile_id = __hip_atomic_fetch_add(reinterpret_cast<int *>(ws), 1, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        t = tile_id;
-    }
-    const int64_t tile = int64_t(t) * kScanTile;
-    f32x4 x[kScanRounds];
-#pragma unroll
-    for (int r = 0; r < kScanRounds; ++r)
-        x[r] = scan_load<Op, kPacked>(in, tile + int64_t(r) * kScanRound + 4 * threadIdx.x, n);
-    // lane and wave scans of all rounds first, so one barrier serves the tile
-    f32x4 s[kScanRounds];
-    float lane_excl[kScanRounds];
+constexpr int kScanWaves = kScanThreads / kWaveSize;
+constexpr int kScanPair = 2 * kScanTile; // elements of a unit (a pair of tiles)
+
+// Lane and wave scans of a tile held as kScanRounds packs per lane: s = the lane's inclusive
+// scan of each pack, lane_excl = the wave-exclusive prefix of its pack total, wave_tot[r][w] =
+// wave w's round-r total (read after a barrier).
+template <typename Op>
+__device__ __forceinline__ void scan_tile_local(const f32x4 (&x)[kScanRounds], f32x4 (&s)[kScanRounds],
+                                                float (&lane_excl)[kScanRounds], float (*wave_tot)[kScanWaves],
+                                                int wid, int lane) {
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
         s[r][0] = x[r][0];
@@ -187,76 +172,37 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(const float *in, flo
         if (lane == kWaveSize - 1)
             wave_tot[r][wid] = incl;
     }
-    __syncthreads();
-    float carry = Op::identity();
-    if constexpr (kOnePass) {
-        // The tile total in a fixed order (rounds, then waves), published at once.
-        float total = Op::identity();
-#pragma unroll
-        for (int r = 0; r < kScanRounds; ++r)
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w)
-                total = Op::combine(total, wave_tot[r][w]);
-        uint64_t *tile_tot = reinterpret_cast<uint64_t *>(ws + kScanHeaderWords);
-        uint64_t *group_tot = tile_tot + lay.tiles;
-        uint64_t *super_tot = group_tot + lay.groups;
-        uint32_t *timeouts = ws + 1;
-        if (threadIdx.x == 0)
-            scan_publish(tile_tot + t, total);
-        const int g = t / kScanGroup, j = t % kScanGroup, sg = g / kScanGroup, gj = g % kScanGroup;
-        const bool closes_group = j == kScanGroup - 1, closes_super = closes_group && gj == kScanGroup - 1;
-        // Waves 0, 1, 2 scan the totals of the lower tiles in this group, the lower groups in this
-        // super group and the lower super groups. Lane 63 of wave 0 carries this tile's own total,
-        // which completes the group total when this is the group's last tile.
-        float v = Op::identity();
-        if (wid < 3) {
-            const uint64_t *src = wid == 0 ? tile_tot + int64_t(g) * kScanGroup
-                                  : wid == 1 ? group_tot + int64_t(sg) * kScanGroup
-                                             : super_tot;
-            const int count = wid == 0 ? j : wid == 1 ? gj : sg;
-            if (lane < count)
-                v = scan_wait_total(src + lane, timeouts);
-            if (wid == 0 && lane == kWaveSize - 1)
-                v = total;
-            const float incl = wave_inclusive_scan<Op>(v);
-            const float before = count == 0 ? Op::identity() : wave::readlane(incl, count - 1);
-            if (lane == 0)
-                level[wid] = before;
-            if (wid == 0 && closes_group && lane == kWaveSize - 1) {
-                scan_publish(group_tot + g, incl);
-                own_group_total = incl;
-            }
-        }
-        __syncthreads();
-        if (closes_super && wid == 1) {
-            const float incl = wave_inclusive_scan<Op>(lane == kWaveSize - 1 ? own_group_total : v);
-            if (lane == kWaveSize - 1)
-                scan_publish(super_tot + sg, incl);
-        }
-        carry = Op::combine(Op::combine(level[2], level[1]), level[0]);
-    }
+}
+
+// Writes the tile starting at element `base`: every output combines the running carry, the
+// wave totals before it, its lane's prefix and its own pack scan; carry leaves as the carry
+// into the next tile.
+template <typename Op, bool kPacked, bool kInclusive>
+__device__ __forceinline__ void scan_tile_emit(float *out, int64_t base, int64_t n, float &carry,
+                                               const f32x4 (&s)[kScanRounds], const float (&lane_excl)[kScanRounds],
+                                               const float (*wave_tot)[kScanWaves], int wid) {
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
         float before = carry, round_total = carry;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < kScanWaves; ++w) {
             if (w < wid)
                 before = Op::combine(before, wave_tot[r][w]);
             round_total = Op::combine(round_total, wave_tot[r][w]);
         }
-        const float base = Op::combine(before, lane_excl[r]);
+        const float b0 = Op::combine(before, lane_excl[r]);
         f32x4 y;
         if constexpr (kInclusive) {
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                y[k] = Op::combine(base, s[r][k]);
+                y[k] = Op::combine(b0, s[r][k]);
         } else {
-            y[0] = base;
+            y[0] = b0;
 #pragma unroll
             for (int k = 1; k < 4; ++k)
-                y[k] = Op::combine(base, s[r][k - 1]);
+                y[k] = Op::combine(b0, s[r][k - 1]);
         }
-        const int64_t e = tile + int64_t(r) * kScanRound + 4 * threadIdx.x;
+        const int64_t e = base + int64_t(r) * kScanRound + 4 * threadIdx.x;
         if (kPacked && e + 4 <= n) {
             __builtin_nontemporal_store(y, reinterpret_cast<f32x4 *>(out + e));
         } else {
@@ -269,11 +215,173 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(const float *in, flo
     }
 }
 
+// LDS of the prefix protocol.
+struct ScanPrefixLds {
+    float level[3]; // exclusive prefixes over super groups, groups, units
+    float own_group_total;
+};
+
+// The exclusive prefix of unit t whose total is `total` (every thread calls this; it
+// publishes the unit's total and, for the last unit of a group or super group, that total).
+template <typename Op>
+__device__ __forceinline__ float scan_unit_prefix(uint32_t *ws, const ScanLayout &lay, int t, float total,
+                                                  ScanPrefixLds &sh, int wid, int lane) {
+    uint64_t *unit_tot = reinterpret_cast<uint64_t *>(ws + kScanHeaderWords);
+    uint64_t *group_tot = unit_tot + lay.units;
+    uint64_t *super_tot = group_tot + lay.groups;
+    uint32_t *timeouts = ws + 1;
+    if (threadIdx.x == 0)
+        scan_publish(unit_tot + t, total);
+    const int g = t / kScanGroup, j = t % kScanGroup, sg = g / kScanGroup, gj = g % kScanGroup;
+    const bool closes_group = j == kScanGroup - 1, closes_super = closes_group && gj == kScanGroup - 1;
+    // Waves 0, 1, 2 scan the totals of the lower units in this group, the lower groups in this
+    // super group and the lower super groups. Lane 63 of wave 0 carries this unit's own total,
+    // which completes the group total when this is the group's last unit.
+    float v = Op::identity();
+    if (wid < 3) {
+        const uint64_t *src = wid == 0 ? unit_tot + int64_t(g) * kScanGroup
+                              : wid == 1 ? group_tot + int64_t(sg) * kScanGroup
+                                         : super_tot;
+        const int count = wid == 0 ? j : wid == 1 ? gj : sg;
+        if (lane < count)
+            v = scan_wait_total(src + lane, timeouts);
+        if (wid == 0 && lane == kWaveSize - 1)
+            v = total;
+        const float incl = wave_inclusive_scan<Op>(v);
+        const float before = count == 0 ? Op::identity() : wave::readlane(incl, count - 1);
+        if (lane == 0)
+            sh.level[wid] = before;
+        if (wid == 0 && closes_group && lane == kWaveSize - 1) {
+            scan_publish(group_tot + g, incl);
+            sh.own_group_total = incl;
+        }
+    }
+    __syncthreads();
+    if (closes_super && wid == 1) {
+        const float incl = wave_inclusive_scan<Op>(lane == kWaveSize - 1 ? sh.own_group_total : v);
+        if (lane == kWaveSize - 1)
+            scan_publish(super_tot + sg, incl);
+    }
+    return Op::combine(Op::combine(sh.level[2], sh.level[1]), sh.level[0]);
+}
+
+__device__ __forceinline__ int scan_take_unit(uint32_t *ws, int *slot) {
+    if (threadIdx.x == 0)
+        *slot = __hip_atomic_fetch_add(reinterpret_cast<int *>(ws), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    return *slot;
+}
+
+// A scan of at most one tile: one workgroup, no workspace.
+template <typename Op, bool kPacked, bool kInclusive>
+__global__ __launch_bounds__(kScanThreads) void scan_kernel(const float *in, float *out, int64_t n) {
+    __shared__ float wave_tot[kScanRounds][kScanWaves];
+    const int wid = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
+    f32x4 x[kScanRounds];
+#pragma unroll
+    for (int r = 0; r < kScanRounds; ++r)
+        x[r] = scan_load<Op, kPacked>(in, int64_t(r) * kScanRound + 4 * threadIdx.x, n);
+    f32x4 s[kScanRounds];
+    float lane_excl[kScanRounds];
+    scan_tile_local<Op>(x, s, lane_excl, wave_tot, wid, lane);
+    __syncthreads();
+    float carry = Op::identity();
+    scan_tile_emit<Op, kPacked, kInclusive>(out, 0, n, carry, s, lane_excl, wave_tot, wid);
+}
+
+// One workgroup per pair of tiles: tile A is loaded into registers and tile B into LDS
+// (straight from global memory when the input is 16-byte aligned and the tile is whole), so a
+// workgroup holds 64 KB at the register cost of 32 KB and twice the bytes are in flight while
+// units wait for their prefixes (2^28 elements: 498 -> 410 us against one tile per workgroup).
+// The pair's total is A's total then B's; B's outputs continue A's carry. Aligned and unaligned
+// inputs take the same steps, so their results are the same bits. kOnePass = false: a single
+// pair, no workspace.
+template <typename Op, bool kPacked, bool kInclusive, bool kOnePass>
+__global__ __launch_bounds__(kScanThreads) void scan_pair_kernel(const float *in, float *out, uint32_t *ws,
+                                                                 ScanLayout lay, int64_t n) {
+    __shared__ float wave_tot[kScanRounds][kScanWaves];
+    __shared__ float wave_tot_b[kScanWaves];
+    __shared__ ScanPrefixLds sh;
+    __shared__ int unit;
+    __shared__ __attribute__((aligned(16))) float tile_b[kScanTile];
+    const int wid = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
+    if (n < 0) // never runs: an ordinary store, so the compiler treats tile_b as written
+        tile_b[threadIdx.x] = 0.f;
+    const int t = kOnePass ? scan_take_unit(ws, &unit) : 0;
+    const int64_t base_a = int64_t(t) * kScanPair, base_b = base_a + kScanTile;
+    // Tile B: wave instruction i fills the 1 KB block 8 i + wave of the tile; a tile that
+    // ends past n is loaded through registers instead, with the identity past the end.
+    const bool b_whole = kPacked && base_b + kScanTile <= n;
+    if (b_whole) {
+#pragma unroll
+        for (int i = 0; i < kScanTile / (256 * kScanWaves); ++i) {
+            const int blk = kScanWaves * i + wid;
+            load_lds16(in + base_b + 256 * blk + 4 * lane, tile_b + 256 * blk);
+        }
+    }
+    f32x4 x[kScanRounds];
+#pragma unroll
+    for (int r = 0; r < kScanRounds; ++r)
+        x[r] = scan_load<Op, kPacked>(in, base_a + int64_t(r) * kScanRound + 4 * threadIdx.x, n);
+    if (!b_whole) {
+#pragma unroll
+        for (int r = 0; r < kScanRounds; ++r)
+            *reinterpret_cast<f32x4 *>(tile_b + r * kScanRound + 4 * threadIdx.x) =
+                scan_load<Op, kPacked>(in, base_b + int64_t(r) * kScanRound + 4 * threadIdx.x, n);
+    }
+    f32x4 s[kScanRounds];
+    float lane_excl[kScanRounds];
+    scan_tile_local<Op>(x, s, lane_excl, wave_tot, wid, lane);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0Only); // this wave's direct loads of tile B have landed
+    __syncthreads();
+    {   // tile B's total, read from LDS in the order the output pass reads it
+        float bsum = Op::identity();
+#pragma unroll
+        for (int r = 0; r < kScanRounds; ++r) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(tile_b + r * kScanRound + 4 * threadIdx.x);
+            bsum = Op::combine(bsum, Op::combine(Op::combine(v[0], v[1]), Op::combine(v[2], v[3])));
+        }
+        bsum = wave::reduce(bsum, Op::identity(), [](float p, float q) { return Op::combine(p, q); });
+        if (lane == 0)
+            wave_tot_b[wid] = bsum;
+    }
+    __syncthreads();
+    float carry = Op::identity();
+    if constexpr (kOnePass) {
+        float total_a = Op::identity(), total_b = Op::identity();
+#pragma unroll
+        for (int r = 0; r < kScanRounds; ++r)
+#pragma unroll
+            for (int w = 0; w < kScanWaves; ++w)
+                total_a = Op::combine(total_a, wave_tot[r][w]);
+#pragma unroll
+        for (int w = 0; w < kScanWaves; ++w)
+            total_b = Op::combine(total_b, wave_tot_b[w]);
+        carry = scan_unit_prefix<Op>(ws, lay, t, Op::combine(total_a, total_b), sh, wid, lane);
+    }
+    scan_tile_emit<Op, kPacked, kInclusive>(out, base_a, n, carry, s, lane_excl, wave_tot, wid);
+    __syncthreads(); // tile A's wave totals have been read
+    {
+        f32x4 xb[kScanRounds];
+#pragma unroll
+        for (int r = 0; r < kScanRounds; ++r)
+            xb[r] = *reinterpret_cast<const f32x4 *>(tile_b + r * kScanRound + 4 * threadIdx.x);
+        scan_tile_local<Op>(xb, s, lane_excl, wave_tot, wid, lane);
+    }
+    __syncthreads();
+    scan_tile_emit<Op, kPacked, kInclusive>(out, base_b, n, carry, s, lane_excl, wave_tot, wid);
+}
+
+
 template <typename Op, bool kPacked, bool kInclusive>
 void scan_launch(const float *in, float *out, int n, float *workspace, hipStream_t stream) {
-    const ScanLayout lay = scan_layout(n);
-    if (lay.tiles <= 1) {
-        launch_async(stream, scan_kernel<Op, kPacked, kInclusive, false>, 1, kScanThreads, in, out,
+    if (n <= kScanTile) {
+        launch_async(stream, scan_kernel<Op, kPacked, kInclusive>, 1, kScanThreads, in, out, static_cast<int64_t>(n));
+        return;
+    }
+    const ScanLayout lay = scan_pair_layout(n);
+    if (lay.units == 1) {
+        launch_async(stream, scan_pair_kernel<Op, kPacked, kInclusive, false>, 1, kScanThreads, in, out,
                      static_cast<uint32_t *>(nullptr), lay, static_cast<int64_t>(n));
         return;
     }
@@ -281,7 +389,7 @@ void scan_launch(const float *in, float *out, int n, float *workspace, hipStream
     const int64_t quads = (lay.words() + 3) / 4;
     launch_async(stream, scan_clear_kernel, static_cast<int>(blocks_for64(quads, 256)), 256,
                  reinterpret_cast<uint4 *>(ws), quads);
-    launch_async(stream, scan_kernel<Op, kPacked, kInclusive, true>, lay.tiles, kScanThreads, in, out, ws, lay,
+    launch_async(stream, scan_pair_kernel<Op, kPacked, kInclusive, true>, lay.units, kScanThreads, in, out, ws, lay,
                  static_cast<int64_t>(n));
 }
 
@@ -302,14 +410,15 @@ void scan_dispatch(const float *in, float *out, int n, bool inclusive, float *wo
 
 namespace opworks::ops {
 
-// Workspace size in floats (32-bit words): 0 for a single tile of 8192
-// elements, else a 64-word header plus two words per tile, per group of 64
-// tiles and per super group of 4096 tiles, rounded up to a 16-byte multiple.
-// Its contents on entry do not matter: each scan clears what it uses.
+// Workspace size in floats (32-bit words): 0 up to one pair of 8192-element
+// tiles (16384 elements), else a 64-word header plus two words per pair, per
+// group of 64 pairs and per super group of 4096 pairs, rounded up to a
+// 16-byte multiple. Its contents on entry do not matter: each scan clears
+// what it uses.
 inline int scan_workspace_size(int n) {
     detail::validate_size(n);
-    const detail::ScanLayout lay = detail::scan_layout(n);
-    return lay.tiles <= 1 ? 0 : static_cast<int>((lay.words() + 3) / 4 * 4);
+    const detail::ScanLayout lay = detail::scan_pair_layout(n);
+    return lay.units <= 1 ? 0 : static_cast<int>((lay.words() + 3) / 4 * 4);
 }
 
 // Allocation-free asynchronous path; capturable into a HIP graph. `maximum`

@@ -93,11 +93,11 @@ def test_scan_transform_gather_contracts(ow):
     E = ow.OpworksError
     ops = ow.ops
     assert ops.scan_workspace_size(0) == 0
-    assert ops.scan_workspace_size(8192) == 0  # one tile: single launch
-    # a 64-word header, then 2 words per tile, per group of 64 tiles and per super group of 4096 tiles
-    assert ops.scan_workspace_size(8193) == 64 + 2 * (2 + 1 + 1)
-    assert ops.scan_workspace_size(1 << 28) == 64 + 2 * (32768 + 512 + 8)
-    assert ops.scan_workspace_size(2**31 - 1) == 64 + 2 * (262144 + 4096 + 64)
+    assert ops.scan_workspace_size(16384) == 0  # one unit (a pair of 8192-element tiles): no workspace
+    # a 64-word header, then 2 words per unit, per group of 64 units and per super group of 4096 units
+    assert ops.scan_workspace_size(16385) == 64 + 2 * (2 + 1 + 1)
+    assert ops.scan_workspace_size(1 << 28) == 64 + 2 * (16384 + 256 + 4)
+    assert ops.scan_workspace_size(2**31 - 1) == 64 + 2 * (131072 + 2048 + 32)
     ops.scan(None, None, 0)  # n == 0 is a no-op
     ops.transpose(None, None, 0, 5)
     ops.gather(None, 0, None, None, 0)
@@ -107,9 +107,9 @@ def test_scan_transform_gather_contracts(ow):
     with pytest.raises(E, match="non-null"):
         ops.scan(None, None, 4)
     with pytest.raises(E, match="workspace is too small"):
-        ops.scan(1, 1, 9000, workspace=1, workspace_size=1)
+        ops.scan(1, 1, 20000, workspace=1, workspace_size=1)
     with pytest.raises(E, match="16-byte aligned"):
-        ops.scan(1, 1, 9000, workspace=4, workspace_size=ops.scan_workspace_size(9000))
+        ops.scan(1, 1, 20000, workspace=4, workspace_size=ops.scan_workspace_size(20000))
     with pytest.raises(E, match="nonnegative"):
         ops.scan(None, None, -1)
     with pytest.raises(E, match="in place"):

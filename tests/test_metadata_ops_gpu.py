@@ -101,17 +101,19 @@ def test_scan_in_place_and_deterministic(ow, orc):
     assert np.array_equal(bits(d.to_host()), bits(first))
 
 
-TILE = 8192  # elements per scan tile; 64 tiles make a group, 64 groups a super group
+TILE = 8192       # elements per scan tile
+UNIT = 2 * TILE  # a unit of the one-pass protocol: a pair of tiles; 64 units make a group, 64 groups a super group
 
 
-@pytest.mark.parametrize("n", [2 * TILE, 64 * TILE, 64 * TILE + 1, 65 * TILE - 3, 4096 * TILE, 4096 * TILE + 1,
-                               (1 << 25) + 3 * 64 * TILE + 100])
+@pytest.mark.parametrize("n", [UNIT + TILE + 5, 2 * UNIT + TILE, 3 * UNIT - 1, 64 * UNIT, 64 * UNIT + 1,
+                               65 * UNIT - 3, 4096 * UNIT, 4096 * UNIT + 1, (1 << 26) + 3 * 64 * UNIT + 100])
 def test_scan_levels_and_stale_workspace_exact(ow, n):
-    """The one-pass protocol at each level's edges (exactly one group or super group of tiles and
-    one element past it) and across a second super group ending in a partial group and a partial
-    tile, on a workspace whose every flag starts set: x[i] = (i mod 3) - 1 has prefix sums of -1 or 0
-    in any order, so every output is checked bit for bit, and a tile given a wrong or stale prefix
-    shows up. Later calls reuse the earlier calls' workspace contents."""
+    """The one-pass protocol at each level's edges (exactly one group or super group of units and
+    one element past it), units whose second tile is partial or empty, and a second super group
+    ending in a partial group and a partial unit, on a workspace whose every flag starts set:
+    x[i] = (i mod 3) - 1 has prefix sums of -1 or 0 in any order, so every output is checked bit
+    for bit, and a unit given a wrong or stale prefix shows up. Later calls reuse the earlier
+    calls' workspace contents."""
     i = np.arange(n, dtype=np.int64)
     x = (i % 3 - 1).astype(np.float32)
     d = upload(ow, x)
@@ -129,7 +131,7 @@ def test_scan_levels_and_stale_workspace_exact(ow, n):
 
 
 def test_scan_full_size_bound(ow, orc):
-    """2^26 elements (8192 tiles, the multi-level path at scale) within the bar."""
+    """2^26 elements (4096 units, the multi-level path at scale) within the bar."""
     n = 1 << 26
     d = ow.DeviceBuffer.empty(n)
     ow.fill_normal(d, SEED, 9, 0.0, 1.0)
