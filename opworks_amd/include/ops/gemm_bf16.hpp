@@ -8,8 +8,7 @@
 //
 // Kernel shape (gfx950):
 //  * workgroup tile 256 x 256, 512 threads = 8 waves in 2 x 4; each wave owns
-//    128 x 64 = 4 x 2 v_mfma_f32_32x32x16_bf16 tiles (128 accumulator
-//    registers);
+//    128 x 64 outputs (128 accumulator registers);
 //  * K tile 64 (128 KB of LDS with bf16 A, 144 KB with fp32 A; one workgroup
 //    per CU);
 //  * an MFMA operand is 8 consecutive k of one row per lane, so both operands
@@ -19,15 +18,24 @@
 //    straight to LDS and by 16 bytes of row padding where they are staged in
 //    registers;
 //  * with bf16 A both operands go from global memory straight into LDS
-//    (gfx950 global_load_lds_dwordx4, no register staging); with fp32 A both
-//    are loaded into registers (A raw, rounded when written to LDS) and
-//    stored halfway through the current tile's MFMAs;
+//    (gfx950 global_load_lds_dwordx4, no register staging) and the wave tile
+//    is 8 x 4 v_mfma_f32_16x16x32_bf16 tiles, two MFMA steps per K tile. The
+//    workgroup syncs once per K tile, before the last step's MFMAs, whose
+//    operands are already in registers: the next tile's first fragments are
+//    read while those MFMAs run, so no step waits on the barrier's LDS reads;
+//  * with fp32 A both operands are loaded into registers (A raw, rounded when
+//    written to LDS) and stored halfway through the current tile's MFMAs, on
+//    4 x 2 v_mfma_f32_32x32x16_bf16 tiles (the 16x16 form's fragments would
+//    not fit beside the staging registers);
 //  * LDS double buffered, the next tile's loads issued before the current
-//    tile's MFMAs, one barrier per K tile; inside a tile the next MFMA step's
-//    fragments are read while the current step's MFMAs run; same XCD-banded
-//    tile order as the fp32 kernel.
+//    tile's MFMAs; inside a tile the next MFMA step's fragments are read while
+//    the current step's MFMAs run; same XCD-banded tile order as the fp32
+//    kernel.
+// On 4096^3 uniformly random bf16 operands the 16x16x32 and 32x32x16 forms gave
+// bit-identical outputs (measured on gfx950); the tests hold both to the oracle.
 
 #include <cstdint>
+#include <type_traits>
 
 #include "../core/bf16.hpp"
 #include "../core/lds_direct.hpp"
@@ -77,9 +85,11 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     int tm, tn;
     gemm_tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * kBfBM, n0 = tn * kBfBN;
-    const int tid = threadIdx.x, lane = tid % kWaveSize, wave = tid / kWaveSize;
+    const int tid = threadIdx.x, lane = tid % kWaveSize;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveSize); // uniform: LDS targets in scalar registers
     const int wm = wave / 4, wn = wave % 4; // 2 x 4 waves
     const int l32 = lane % 32, half = lane / 32;
+    const int l16 = lane % 16, quad = lane / 16;
     // The compiler does not count direct loads as writes to the array: without a store it may
     // treat the array as never written and drop the reads. This one never runs (M >= 0).
     if (kDirect && M < 0)
@@ -189,16 +199,55 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
         }
     };
 
-    f32x16 acc[4][2];
+    // Accumulators: 16x16 tiles (4 registers each) on the direct path, 32x32 tiles (16) otherwise.
+    constexpr int kTile = kDirect ? 16 : 32;
+    constexpr int FM = 128 / kTile, FN = 64 / kTile;
+    using Acc = std::conditional_t<kDirect, f32x4, f32x16>;
+    Acc acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-            acc[i][j] = f32x16{};
+        for (int j = 0; j < FN; ++j)
+            acc[i][j] = Acc{};
 
-    // One K tile: BK / 16 MFMA steps. The fragments are double buffered across steps: the next
-    // step's six reads are interleaved one per MFMA with the current step's first six MFMAs,
-    // so they arrive while the matrix core runs. stage_next() (the next tile's LDS stores, into
+    // Direct path, 16x16x32 MFMAs: fragment set p holds step s's operands, lane l reading row
+    // l % 16 of each 16-row tile at k 32 s + 8 (l / 16) .. + 7 (chunk 4 s + l / 16).
+    bf16x8 fa[2][FM], fb[2][FN];
+    auto read16 = [&](int buf, int s, int p) {
+        const uint16_t *As = lds + buf * kStage;
+        const uint16_t *Bs = As + kBfBM * kRowE;
+        const int ch = 4 * s + quad;
+#pragma unroll
+        for (int bm = 0; bm < FM; ++bm)
+            fa[p][bm] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
+                                                       As + swz(wm * 128 + bm * 16 + l16, ch)));
+#pragma unroll
+        for (int bn = 0; bn < FN; ++bn)
+            fb[p][bn] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
+                                                       Bs + swz(wn * 64 + bn * 16 + l16, ch)));
+    };
+    auto mfma16 = [&](int p) {
+        if constexpr (kDirect) {
+#pragma unroll
+            for (int bm = 0; bm < FM; ++bm)
+#pragma unroll
+                for (int bn = 0; bn < FN; ++bn)
+                    acc[bm][bn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[p][bm], fb[p][bn], acc[bm][bn], 0, 0, 0);
+        }
+    };
+    // The fragment reads issued with a step (FM + FN of them) go one per MFMA at its start.
+    auto interleave16 = [] {
+#pragma unroll
+        for (int j = 0; j < FM + FN; ++j) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0); // one fragment read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // one MFMA
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - FM - FN, 0);
+    };
+
+    // One K tile of the register-staged paths: BK / 16 MFMA steps on 32x32x16 tiles. The
+    // fragments are double buffered across steps: the next step's six reads are interleaved
+    // one per MFMA with the current step's first six MFMAs, so they arrive while the matrix core runs. stage_next() (the next tile's LDS stores, into
     // the other buffer) runs halfway, so its wait for the global loads and its LDS writes
     // overlap the second half's MFMAs (against staging after the last step: 990-999 ->
     // 1019-1025 TFLOP/s).
@@ -225,12 +274,14 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
                 read(s + 1, a[(s + 1) & 1], b[(s + 1) & 1]);
             if (s == kSteps / 2)
                 stage_next();
+            if constexpr (!kDirect) {
 #pragma unroll
-            for (int bm = 0; bm < 4; ++bm)
+                for (int bm = 0; bm < 4; ++bm)
 #pragma unroll
-                for (int bn = 0; bn < 2; ++bn)
-                    acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s & 1][bm], b[s & 1][bn], acc[bm][bn],
-                                                                          0, 0, 0);
+                    for (int bn = 0; bn < 2; ++bn)
+                        acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[s & 1][bm], b[s & 1][bn],
+                                                                              acc[bm][bn], 0, 0, 0);
+            }
         }
         __builtin_amdgcn_sched_group_barrier(0x100, 6, 0); // step 0's reads
 #pragma unroll
@@ -256,78 +307,150 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     // The vector path pipelines its full K tiles and runs a partial last tile (K not a multiple
     // of the K tile) after the loop, with the tail zeroed; the scalar path bounds every element.
     const int kt_full = kVec ? (K / BK < kt_end ? (K / BK > kt_begin ? K / BK : kt_begin) : kt_end) : kt_end;
-    if (kt_begin < kt_full) {
-        // Each K tile: the next tile's loads are issued first (direct loads straight into the
-        // idle stage, or into registers, stored halfway through the MFMA steps), then the MFMAs,
-        // then every wave waits for its loads and the workgroup syncs once.
-        // (Direct loads against register staging: 129-132 -> 125-127 us at 4096^3, bf16 A.)
-        if constexpr (kDirect) {
-            direct_load(0, kt_begin);
-        } else {
-            global_load(kt_begin, true, true);
-            lds_store(0, kt_begin, false, true, true);
+    if constexpr (kDirect) {
+      if (kt_begin < kt_full) {
+        // Per K tile: the next tile's direct loads into the idle stage, step 0's MFMAs with step
+        // 1's fragments read in between, then (every wave's loads landed, every read of this tile
+        // done) one barrier, and step 1's MFMAs with the next tile's step-0 fragments read in
+        // between. The idle stage was last read before the previous tile's barrier.
+        // (4096^3, bf16 A, on one box: 123-126 us with a barrier at the end of each tile on
+        // 32x32x16 tiles, 112-114 us with this barrier, 102.5-104 us on 16x16x32 tiles.)
+        direct_load(0, kt_begin);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0Only);
+        __syncthreads();
+        read16(0, 0, 0);
+        for (int kt = kt_begin; kt < kt_full; ++kt) {
+            const int buf = (kt - kt_begin) & 1;
+            // past the last tile: a reload of a valid tile into the idle stage, never read (a
+            // peeled last tile without it took the residual epilogue into spills)
+            const int next = kt + 1 < kt_full ? kt + 1 : kt;
+            direct_load(buf ^ 1, next);
+            __builtin_amdgcn_sched_barrier(0); // the loads stay at the top, in flight during the MFMAs
+            read16(buf, 1, 1);
+            mfma16(0);
+            interleave16();
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0Only); // this wave's loads of the next tile landed
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+            read16(buf ^ 1, 0, 0);
+            mfma16(1);
+            interleave16();
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if constexpr (kDirect)
-            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0Only); // this wave's direct loads have landed
+      }
+    } else if (kt_begin < kt_full) {
+        // Each K tile: the next tile's loads are issued first into registers, stored halfway
+        // through the MFMA steps, then the workgroup syncs once.
+        global_load(kt_begin, true, true);
+        lds_store(0, kt_begin, false, true, true);
         __syncthreads();
         for (int kt = kt_begin; kt < kt_full; ++kt) {
             const int buf = (kt - kt_begin) & 1;
-            // past the last tile: a reload of a valid tile, staged into the idle buffer
             const int next = kt + 1 < kt_full ? kt + 1 : kt;
-            // the idle buffer was last read before the previous barrier
-            if constexpr (kDirect)
-                direct_load(buf ^ 1, next);
-            else
-                global_load(next, true, true);
-            __builtin_amdgcn_sched_barrier(0); // the loads stay at the top, in flight during the MFMAs
-            compute(buf, [&] {
-                if constexpr (!kDirect)
-                    lds_store(buf ^ 1, next, false, true, true);
-            });
-            if constexpr (kDirect) {
-                __builtin_amdgcn_sched_barrier(0);
-                __builtin_amdgcn_s_waitcnt(kWaitVmcnt0Only);
-            }
+            global_load(next, true, true);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(buf, [&] { lds_store(buf ^ 1, next, false, true, true); });
             __syncthreads();
         }
     }
     if (kt_full < kt_end) { // the partial last K tile (vector path), staged through registers
+        __syncthreads(); // every wave is done with the stages (the direct path's last reads)
         global_load(kt_full, true, true);
         lds_store(0, kt_full, true, true, true);
         __syncthreads();
-        compute(0, [] {});
+        if constexpr (kDirect) {
+            read16(0, 0, 0);
+            read16(0, 1, 1);
+            mfma16(0);
+            mfma16(1);
+        } else {
+            compute(0, [] {});
+        }
     }
     if constexpr (kStore == GemmStore::partial)
         C += int64_t(blockIdx.y) * M * N;
 
+    // Accumulator register r of a 16x16 tile holds row 4 (l / 16) + r, column l % 16; of a 32x32
+    // tile, row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32. A tile inside C on both axes stores
+    // without bounds tests (each test compiled to an exec-mask branch per store).
+    auto store_tile = [&](auto checked_t) {
+        constexpr bool checked = decltype(checked_t)::value;
+        constexpr int kRegs = kDirect ? 4 : 16; // accumulator registers per tile
+        // A store counts in vmcnt like a load, so a load issued after stores waits for them too:
+        // every bias value is loaded before the first store, and the residual C values of a
+        // batch of tiles before its stores (one drain per batch, not one per element).
+        float bv[FN];
 #pragma unroll
-    for (int bn = 0; bn < 2; ++bn) {
-        const int col = n0 + wn * 64 + bn * 32 + l32;
-        const float bv = (bias != nullptr && col < N && kStore != GemmStore::partial) ? bias[col] : 0.f;
+        for (int bn = 0; bn < FN; ++bn)
+            bv[bn] = 0.f;
+        if (kStore != GemmStore::partial && bias != nullptr) { // one uniform test for every column
 #pragma unroll
-        for (int bm = 0; bm < 4; ++bm) {
+            for (int bn = 0; bn < FN; ++bn) {
+                const int col = n0 + wn * 64 + bn * kTile + (kDirect ? l16 : l32);
+                bv[bn] = (!checked || col < N) ? bias[col] : 0.f;
+            }
+        }
+        auto row_of = [&](int bm, int r) {
+            return kDirect ? m0 + wm * 128 + bm * 16 + 4 * quad + r
+                           : m0 + wm * 128 + bm * 32 + 8 * (r / 4) + 4 * half + (r % 4);
+        };
+        // residual loads per batch of 16 values: four 16x16 tiles or one 32x32 tile (larger batches
+        // pushed both paths into spills)
+        constexpr int kBatch = kDirect ? 4 : 1;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm * 128 + bm * 32 + 8 * (r / 4) + 4 * half + (r % 4);
-                if constexpr (kStore == GemmStore::partial) {
-                    if (row < M && col < N)
-                        C[int64_t(row) * N + col] = acc[bm][bn][r];
-                    continue;
+        for (int bn = 0; bn < FN; ++bn) {
+            const int col = n0 + wn * 64 + bn * kTile + (kDirect ? l16 : l32);
+            const bool col_ok = !checked || col < N;
+#pragma unroll
+            for (int bm0 = 0; bm0 < FM; bm0 += kBatch) {
+                float prev[kBatch][kRegs];
+                if constexpr (kStore == GemmStore::residual) {
+#pragma unroll
+                    for (int i = 0; i < kBatch; ++i)
+#pragma unroll
+                        for (int r = 0; r < kRegs; ++r) {
+                            const int row = row_of(bm0 + i, r);
+                            prev[i][r] = (!checked || (row < M && col_ok)) ? C[int64_t(row) * N + col] : 0.f;
+                        }
                 }
-                const float v = epi(acc[bm][bn][r] + bv);
-                if constexpr (kStore == GemmStore::swiglu) {
-                    const float partner = __shfl_xor(v, 1); // lane l ^ 1 holds column col ^ 1
-                    if ((l32 & 1) == 0 && row < M && col + 1 < N)
-                        C[int64_t(row) * (N / 2) + col / 2] = v / (1.f + expf(-v)) * partner;
-                } else if constexpr (kStore == GemmStore::residual) {
-                    if (row < M && col < N)
-                        C[int64_t(row) * N + col] += v;
-                } else {
-                    if (row < M && col < N)
-                        C[int64_t(row) * N + col] = v;
+#pragma unroll
+                for (int i = 0; i < kBatch; ++i) {
+                    const int bm = bm0 + i;
+#pragma unroll
+                    for (int r = 0; r < kRegs; ++r) {
+                        const int row = row_of(bm, r);
+                        const bool ok = !checked || (row < M && col_ok);
+                        if constexpr (kStore == GemmStore::partial) {
+                            if (ok)
+                                C[int64_t(row) * N + col] = acc[bm][bn][r];
+                            continue;
+                        }
+                        const float v = epi(acc[bm][bn][r] + bv[bn]);
+                        if constexpr (kStore == GemmStore::swiglu) {
+                            const float partner = __shfl_xor(v, 1); // lane l ^ 1 holds column col ^ 1
+                            if ((col & 1) == 0 && (!checked || (row < M && col + 1 < N)))
+                                C[int64_t(row) * (N / 2) + col / 2] = v / (1.f + expf(-v)) * partner;
+                        } else if constexpr (kStore == GemmStore::residual) {
+                            if (ok)
+                                C[int64_t(row) * N + col] = prev[i][r] + v;
+                        } else {
+                            if (ok)
+                                C[int64_t(row) * N + col] = v;
+                        }
+                    }
                 }
             }
         }
+    };
+    // The register-staged paths keep the checked form only: a second copy pushed them into spills.
+    if constexpr (kDirect) {
+        if (m0 + kBfBM <= M && n0 + kBfBN <= N)
+            store_tile(std::false_type{});
+        else
+            store_tile(std::true_type{});
+    } else {
+        store_tile(std::true_type{});
     }
 }
 

@@ -293,11 +293,28 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
         C += int64_t(blockIdx.y) * M * N;
 
     // ---- epilogue: accumulator register r of a 16 x 16 tile holds row
-    // 4 * grp + r, column l16.
+    // 4 * grp + r, column l16. A store counts in vmcnt like a load, so a load issued after stores
+    // waits for them too: every bias value is loaded before the first store, and a column group's
+    // residual C values before its stores (one drain per group, not one per element).
+    float bv[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
         const int col = n0 + wn * TN + j * 16 + l16;
-        const float bv = (bias != nullptr && col < N && kStore != GemmStore::partial) ? bias[col] : 0.f;
+        bv[j] = (bias != nullptr && col < N && kStore != GemmStore::partial) ? bias[col] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int col = n0 + wn * TN + j * 16 + l16;
+        float prev[FM][4];
+        if constexpr (kStore == GemmStore::residual) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = m0 + wm * TM + i * 16 + 4 * grp + r;
+                    prev[i][r] = (row < M && col < N) ? C[int64_t(row) * N + col] : 0.f;
+                }
+        }
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -308,14 +325,14 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
                         C[int64_t(row) * N + col] = acc[i][j][r];
                     continue;
                 }
-                const float v = epi(acc[i][j][r] + bv);
+                const float v = epi(acc[i][j][r] + bv[j]);
                 if constexpr (kStore == GemmStore::swiglu) {
                     const float partner = __shfl_xor(v, 1); // lane l ^ 1 holds column col ^ 1
                     if ((l16 & 1) == 0 && row < M && col + 1 < N)
                         C[int64_t(row) * (N / 2) + col / 2] = v / (1.f + expf(-v)) * partner;
                 } else if constexpr (kStore == GemmStore::residual) {
                     if (row < M && col < N)
-                        C[int64_t(row) * N + col] += v;
+                        C[int64_t(row) * N + col] = prev[i][r] + v;
                 } else {
                     if (row < M && col < N)
                         C[int64_t(row) * N + col] = v;
