@@ -21,8 +21,9 @@
 // Measured on 4096^3 fp32: 256 x 256 / 8 waves / 16x16x4 at 126-128 TFLOP/s,
 // against 117-120 for every 128 x 128 variant of 32x32x2 or 16x16x4 MFMA, K
 // tile 16 or 32, and one or two register staging sets.
-//  * operands are staged through LDS, double buffered, one barrier per K tile;
-//    the next tile's global loads are issued before the current tile's MFMAs;
+//  * operands are staged through LDS, double buffered, one barrier per K tile,
+//    before its last MFMA step; the next tile's global loads are issued before
+//    the current tile's MFMAs and its first fragments read during that step;
 //  * K is permuted per 16-lane group: in a K tile, MFMA step j of lane group g
 //    (lanes 16g .. 16g + 15) uses k = 4g + j. A product sum does not depend on
 //    the order of k, and this order lets a k-contiguous operand (A, and B in
@@ -232,42 +233,47 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
         for (int j = 0; j < FN; ++j)
             acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Each 16-k group of a K tile = four MFMA steps; lane group g reads k = 4g .. 4g + 3 of it.
-    auto compute = [&](int buf) {
+    // A K tile is one 16-k group = four MFMA steps; lane group g supplies k = 4g + e at step e.
+    // Fragments are held per step ([set][e][tile]), so a step's values die with it.
+    static_assert(BK == 16, "one 16-k group per K tile");
+    float fa[2][4][FM], fb[2][4][FN];
+    auto read_frags = [&](int buf, int p) {
         const float *As = lds + buf * kStage;
         const float *Bs = As + kA;
+        const int kk = 4 * grp;
 #pragma unroll
-        for (int h = 0; h < BK / 16; ++h) {
-            const int kk = 16 * h + 4 * grp;
-            f32x4 a[FM], b[FN];
+        for (int i = 0; i < FM; ++i) {
+            if constexpr (kAL == ALayout::mk) {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(As + (wm * TM + i * 16 + l16) * LdK + kk);
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                if constexpr (kAL == ALayout::mk) {
-                    a[i] = *reinterpret_cast<const f32x4 *>(As + (wm * TM + i * 16 + l16) * LdK + kk);
-                } else {
+                for (int e = 0; e < 4; ++e)
+                    fa[p][e][i] = v[e];
+            } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        a[i][e] = As[(kk + e) * LdM + wm * TM + i * 16 + l16];
-                }
+                for (int e = 0; e < 4; ++e)
+                    fa[p][e][i] = As[(kk + e) * LdM + wm * TM + i * 16 + l16];
             }
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                if constexpr (kB == BLayout::kn) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        b[j][e] = Bs[(kk + e) * LdN + wn * TN + j * 16 + l16];
-                } else {
-                    b[j] = *reinterpret_cast<const f32x4 *>(Bs + (wn * TN + j * 16 + l16) * LdK + kk);
-                }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int i = 0; i < FM; ++i)
-#pragma unroll
-                    for (int j = 0; j < FN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
         }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            if constexpr (kB == BLayout::kn) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    fb[p][e][j] = Bs[(kk + e) * LdN + wn * TN + j * 16 + l16];
+            } else {
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(Bs + (wn * TN + j * 16 + l16) * LdK + kk);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    fb[p][e][j] = v[e];
+            }
+        }
+    };
+    auto mfma_step = [&](int p, int e) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[p][e][i], fb[p][e][j], acc[i][j], 0, 0, 0);
     };
 
     // K tiles of this workgroup: all of them, or split blockIdx.y's contiguous share
@@ -275,7 +281,46 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
     const int per_split = (ktiles_all + gridDim.y - 1) / gridDim.y;
     const int kt_begin = blockIdx.y * per_split;
     const int kt_end = kt_begin + per_split < ktiles_all ? kt_begin + per_split : ktiles_all;
-    if (kt_begin < kt_end) {
+    // Tile kt from fragment set p: the next tile's global loads first, its LDS stores after two
+    // MFMA steps, one barrier before the last step (every store of the next tile done, every
+    // read of the stage it fills long done), and the next tile's fragments read into set p ^ 1
+    // while the last step's MFMAs run, so no step waits on a barrier's LDS reads. Past the last
+    // tile the next tile is a reload of this one, never used. (4096^3 kn: 1023-1027 us with a
+    // barrier at the end of each tile, 986-987 us with this one.)
+    auto k_tile = [&](int kt, auto p_t) {
+        constexpr int p = decltype(p_t)::value;
+        const int buf = (kt - kt_begin) & 1;
+        global_load(kt + 1 < kt_end ? kt + 1 : kt);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_step(p, 0);
+        mfma_step(p, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        lds_store(buf ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_step(p, 2);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        read_frags(buf ^ 1, p ^ 1);
+        mfma_step(p, 3);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // GemmBig in the nk layout keeps one barrier at the end of each tile: with two fragment sets
+    // its load addresses spilled to scratch inside the K loop.
+    constexpr bool kSplitBarrier = !(BM == 256 && kB == BLayout::nk);
+    if (kSplitBarrier && kt_begin < kt_end) {
+        global_load(kt_begin);
+        lds_store(0);
+        __syncthreads();
+        read_frags(0, 0);
+        int kt = kt_begin;
+        for (; kt + 1 < kt_end; kt += 2) { // two tiles per trip: each fragment set keeps its registers
+            k_tile(kt, std::integral_constant<int, 0>{});
+            k_tile(kt + 1, std::integral_constant<int, 1>{});
+        }
+        if (kt < kt_end)
+            k_tile(kt, std::integral_constant<int, 0>{});
+    } else if (kt_begin < kt_end) {
         global_load(kt_begin);
         lds_store(0);
         __syncthreads();
@@ -283,7 +328,10 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
             const int buf = (kt - kt_begin) & 1;
             if (kt + 1 < kt_end)
                 global_load(kt + 1);
-            compute(buf);
+            read_frags(buf, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                mfma_step(0, e);
             if (kt + 1 < kt_end)
                 lds_store(buf ^ 1);
             __syncthreads();
