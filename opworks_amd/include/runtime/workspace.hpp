@@ -6,6 +6,7 @@
 // reference keep its name (tokens, hidden, normed, q_heads, attn_heads,
 // attn_out, logits); the others serve this build's fused kernels: the fused
 // [q;k;v] projection output, the SwiGLU product, split-K partial tiles, the
+// bf16 copy of the gate/up GEMM input (bf16-weight models), the
 // one-row buffers of the decode step, the decode attention's chunk records
 // and arrival counters, the LM head's per-workgroup argmax records, the
 // device step state and the tokens a chained greedy decode produces.
@@ -25,6 +26,7 @@ struct WorkspaceSizes {
     int state_ints = 0;        // device step state
     int argmax_groups = 0;     // workgroups of the records' reduction
     int attn_counter_ints = 0; // decode attention arrival counters (one cache line per kv head)
+    bool bf16_inputs = false;  // bf16-weight model: a bf16 copy of the gate/up GEMM input
 };
 
 struct Workspace {
@@ -38,6 +40,7 @@ struct Workspace {
     TypedDeviceBuffer<float> attn_out;   // [T, qh D]
     TypedDeviceBuffer<float> act;        // [T, I] silu(gate) * up
     TypedDeviceBuffer<float> splitk;     // split-K partial tiles
+    TypedDeviceBuffer<bf16> normed_bf16; // [T, H] normed rounded to bf16 (bf16-weight models)
     // decode step: one row
     TypedDeviceBuffer<float> step_hidden;   // [H] residual stream
     TypedDeviceBuffer<float> step_q;        // [qh D] post-RoPE query
@@ -67,8 +70,11 @@ struct Workspace {
         attn_heads = TypedDeviceBuffer<float>(T * qw);
         attn_out = TypedDeviceBuffer<float>(T * qw);
         act = TypedDeviceBuffer<float>(T * I);
-        if (T >= 2) // only a multi-row prefill runs the GEMMs
+        if (T >= 2) { // only a multi-row prefill runs the GEMMs
             splitk = TypedDeviceBuffer<float>(s.splitk_floats);
+            if (s.bf16_inputs)
+                normed_bf16 = TypedDeviceBuffer<bf16>(T * H);
+        }
         step_hidden = TypedDeviceBuffer<float>(H);
         step_q = TypedDeviceBuffer<float>(qw);
         step_attn = TypedDeviceBuffer<float>(qw);
