@@ -11,11 +11,13 @@
 //  * BLayout::nk — B[n][k], k contiguous: ops::linear's Y = X W^T with HF
 //    [out, in] weights (reference include/ops/linear.cuh:18-73).
 //
-// Kernel shapes (gfx950), both on v_mfma_f32_16x16x4_f32 with K tiles of 16:
+// Kernel shapes (gfx950), all on v_mfma_f32_16x16x4_f32 with K tiles of 16:
 //  * GemmBig: workgroup tile 256 x 256, 512 threads = 8 waves in 4 x 2, each
 //    wave owns 64 x 128 = 4 x 8 MFMA tiles (128 accumulator registers); used
 //    when the output has at least 256 such tiles (one per CU) and K is not
 //    split, e.g. the 4096^3 GEMM;
+//  * GemmMid: 256 x 128, 512 threads = 8 waves in 4 x 2, each 64 x 64; when
+//    fewer than 256 GemmBig tiles but at least 256 of these cover the output;
 //  * GemmSmall: 128 x 128, 256 threads = 4 waves in 2 x 2, each 64 x 64; for
 //    smaller outputs and the split-K partial tiles.
 // Measured on 4096^3 fp32: 256 x 256 / 8 waves / 16x16x4 at 126-128 TFLOP/s,
@@ -65,6 +67,7 @@ template <int kBM, int kBN, int kWM, int kWN, int kBK = 16> struct GemmF32Shape 
 };
 using GemmSmall = GemmF32Shape<128, 128, 2, 2>;
 using GemmBig = GemmF32Shape<256, 256, 4, 2>; // a K tile of 32 measured 132.4 against 133.5 TFLOP/s
+using GemmMid = GemmF32Shape<256, 128, 4, 2>; // 8 waves of 64 x 64
 constexpr int kGemmBK = 16;
 constexpr int kNumXcd = 8;
 
@@ -128,14 +131,13 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
     // ---- global -> register staging: chunk idx = tid + T i of a tile whose
     // rows hold BK (k-contiguous) or BN (kn-layout B) floats
     f32x4 ra[CA], rb[CB];
-    static_assert(CA == CB, "A and B stage the same number of chunks per thread");
     static_assert(std::is_same_v<TB, float> || (std::is_same_v<TB, uint16_t> && kB == BLayout::nk),
                   "bf16 B is supported in the nk layout");
     // 4 consecutive k of one row: 16 bytes of fp32 or 8 bytes of bf16 (widened)
-    auto load_rows_k = [&](const auto *src, int row0, int rows_total, int k0, f32x4 *dst) {
+    auto load_rows_k = [&](const auto *src, int row0, int rows_total, int k0, f32x4 *dst, auto count) {
         using T = std::remove_cv_t<std::remove_pointer_t<decltype(src)>>;
 #pragma unroll
-        for (int i = 0; i < CA; ++i) {
+        for (int i = 0; i < decltype(count)::value; ++i) {
             const int idx = tid + T_ * i;
             const int r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
             const int gr = row0 + r, gk = k0 + c;
@@ -197,13 +199,13 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
     auto global_load = [&](int kt) {
         const int k0 = kt * BK;
         if constexpr (kAL == ALayout::mk)
-            load_rows_k(A, m0, M, k0, ra);
+            load_rows_k(A, m0, M, k0, ra, std::integral_constant<int, CA>{});
         else
             load_a_km(k0);
         if constexpr (kB == BLayout::kn)
             load_b_kn(k0);
         else
-            load_rows_k(B, n0, N, k0, rb);
+            load_rows_k(B, n0, N, k0, rb, std::integral_constant<int, CB>{});
     };
     auto lds_store = [&](int buf) {
         float *As = lds + buf * kStage;
@@ -307,7 +309,7 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
     };
     // GemmBig in the nk layout keeps one barrier at the end of each tile: with two fragment sets
     // its load addresses spilled to scratch inside the K loop.
-    constexpr bool kSplitBarrier = !(BM == 256 && kB == BLayout::nk);
+    constexpr bool kSplitBarrier = !(BM == 256 && BN == 256 && kB == BLayout::nk);
     if (kSplitBarrier && kt_begin < kt_end) {
         global_load(kt_begin);
         lds_store(0);
@@ -450,15 +452,20 @@ void gemm_f32_launch_shape(const float *A, const TB *B, const float *bias, float
 }
 
 // Enqueues C[M][N] = epi(A[M][K] B + bias) (written per kStore). K == 0 writes epi(bias or 0).
-// GemmBig when K is not split and its tiles alone cover every CU, else GemmSmall.
+// When K is not split: GemmBig when its tiles alone cover every CU, else GemmMid when its
+// 256 x 128 tiles do (the prefill gate/up projection at 512 rows: 280 -> 262 us against
+// GemmSmall); otherwise, and for split-K partials, GemmSmall.
 template <BLayout kB, typename Epi, GemmStore kStore = GemmStore::store, typename TB = float,
           ALayout kAL = ALayout::mk>
 void gemm_f32_launch(const float *A, const TB *B, const float *bias, float *C, int M, int N, int K, Epi epi,
                      hipStream_t stream, int splits = 1) {
     require(kStore != GemmStore::swiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
     const int64_t big_tiles = blocks_for64(M, GemmBig::BM) * blocks_for64(N, GemmBig::BN);
+    const int64_t mid_tiles = blocks_for64(M, GemmMid::BM) * blocks_for64(N, GemmMid::BN);
     if (splits == 1 && big_tiles >= 256)
         gemm_f32_launch_shape<GemmBig, kB, Epi, kStore, TB, kAL>(A, B, bias, C, M, N, K, epi, stream, splits);
+    else if (splits == 1 && mid_tiles >= 256)
+        gemm_f32_launch_shape<GemmMid, kB, Epi, kStore, TB, kAL>(A, B, bias, C, M, N, K, epi, stream, splits);
     else
         gemm_f32_launch_shape<GemmSmall, kB, Epi, kStore, TB, kAL>(A, B, bias, C, M, N, K, epi, stream, splits);
 }

@@ -75,11 +75,14 @@ def test_fused_matmul_transposed_a(ow, orc, M, N, K, b_t, act):
     check_kscaled(got if rows is None else got[rows], ref, absdot)
 
 
-@pytest.mark.parametrize("M,N,K", [(4100, 40, 4000), (4100, 37, 3999), (4096, 64, 4096)])
+@pytest.mark.parametrize("M,N,K", [(4100, 40, 4000), (4100, 37, 3999), (4096, 64, 4096), (520, 72, 16400),
+                                   (520, 37, 16400)])
 @pytest.mark.parametrize("b_t", [False, True])
 def test_big_tile_path_every_element(ow, orc, M, N, K, b_t):
-    """Outputs with at least 256 tiles of 256 x 256 take the 8-wave kernel; ragged edges, the
-    scalar-load variant (inner dim 37) and both B layouts, every output element checked."""
+    """Outputs with at least 256 tiles of 256 x 256 take the 8-wave 256 x 256 kernel, outputs with
+    fewer but at least 256 tiles of 256 x 128 (M = 520, 16400 columns: 195 and 387) the 8-wave
+    256 x 128 one; ragged edges, an odd number of K tiles (inner dim 72), the scalar-load variant
+    (inner dim 37) and both B layouts, every output element checked."""
     A = orc.fill_normal(M * N, SEED, 6, 0.0, 1.0)
     B = orc.fill_normal(N * K, SEED, 7, 0.0, 1.0)
     bias = orc.fill_uniform(K, SEED, 8, -0.1, 0.1)
