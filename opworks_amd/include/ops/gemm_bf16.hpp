@@ -247,10 +247,10 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
 
     // One K tile of the register-staged paths: BK / 16 MFMA steps on 32x32x16 tiles. The
     // fragments are double buffered across steps: the next step's six reads are interleaved
-    // one per MFMA with the current step's first six MFMAs, so they arrive while the matrix core runs. stage_next() (the next tile's LDS stores, into
-    // the other buffer) runs halfway, so its wait for the global loads and its LDS writes
-    // overlap the second half's MFMAs (against staging after the last step: 990-999 ->
-    // 1019-1025 TFLOP/s).
+    // one per MFMA with the current step's first six MFMAs, so they arrive while the matrix
+    // core runs. stage_next() (the next tile's LDS stores, into the other buffer) runs halfway,
+    // so its wait for the global loads and its LDS writes overlap the second half's MFMAs
+    // (against staging after the last step: 990-999 -> 1019-1025 TFLOP/s).
     auto compute = [&](int buf, auto &&stage_next) {
         const uint16_t *As = lds + buf * kStage;
         const uint16_t *Bs = As + kBfBM * kRowE;
