@@ -225,6 +225,51 @@ def wl_layernorm(stream, steps, warmup):
             "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("layernorm"))}
 
 
+# Timed in a child process that imports only torch: torch's own HIP runtime did not see the GPU
+# from a process where this library's runtime already holds it.
+LIBRARY_REFERENCE_CHILD = r"""
+import json, sys, torch
+kind, n, calls, seed = sys.argv[1], int(sys.argv[2]), int(sys.argv[3]), int(sys.argv[4])
+dev = torch.device("cuda", 0)
+g = torch.Generator(device=dev).manual_seed(seed)
+dt = torch.bfloat16 if kind == "bf16" else torch.float32
+a = (torch.randn(n, n, device=dev, generator=g) / 64).to(dt)
+b = (torch.randn(n, n, device=dev, generator=g) / 64).to(dt)
+rhs = b.t() if kind == "bf16" else b
+out = torch.empty(n, n, device=dev, dtype=dt)
+import time
+t_end = time.perf_counter() + 0.3  # back-to-back calls past the clock ramp, as this library's workloads get
+while time.perf_counter() < t_end:
+    for _ in range(10):
+        torch.matmul(a, rhs, out=out)
+    torch.cuda.synchronize()
+e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+e0.record()
+for _ in range(calls):
+    torch.matmul(a, rhs, out=out)
+e1.record()
+torch.cuda.synchronize()
+print(json.dumps({"ms": e0.elapsed_time(e1) / calls, "torch": torch.__version__}))
+"""
+
+
+def library_reference(kind, n=4096, calls=50):
+    """The vendor library on the same problem, for comparison only (opt-in, --library-reference):
+    torch.matmul (hipBLASLt on ROCm) on n^3 N(0, 1/64) operands, `calls` back-to-back calls
+    between two events after 0.3 s of untimed ones (the clock ramp). kind "f32": fp32 A @ B; "bf16": bf16 A @ W^T with
+    a bf16 result (half the output bytes of this library's fp32 result)."""
+    import subprocess
+
+    proc = subprocess.run([sys.executable, "-c", LIBRARY_REFERENCE_CHILD, kind, str(n), str(calls), str(SEED)],
+                          capture_output=True, text=True, timeout=600)
+    if proc.returncode != 0:
+        return {"impl": "torch.matmul", "error": proc.stderr.strip().splitlines()[-1:]}
+    r = json.loads(proc.stdout.strip().splitlines()[-1])
+    ms = r["ms"]
+    return {"impl": f"torch {r['torch']} matmul ({'bf16 in/out, A @ W^T' if kind == 'bf16' else 'fp32'})",
+            "ms": round(ms, 5), "value": round(2.0 * n ** 3 / ms / 1e9, 2), "unit": "TFLOP/s"}
+
+
 def wl_gemm(stream, steps, warmup):
     """Config 3: C = relu(A @ B + bias), M = N = K = 4096 fp32, A, B ~ N(0, 1/64); 2*4096^3 flop."""
     n = 4096
@@ -630,6 +675,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="all", help="all | " + " | ".join(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--library-reference", action="store_true",
+                    help="also time torch.matmul (hipBLASLt) beside the gemm and gemm_bf16 workloads")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -643,6 +690,15 @@ def main() -> int:
         results[name] = WORKLOADS[name](stream.handle, args.steps, args.warmup)
         print(f"[bench] {name}: {results[name]['value']:.1f} {results[name]['unit']} "
               f"({results[name]['ms']:.4f} ms/step)", file=sys.stderr, flush=True)
+    if args.library_reference:  # after every workload of this library, so it cannot disturb them
+        for name, kind in (("gemm", "f32"), ("gemm_bf16", "bf16")):
+            if name in results:
+                ref = library_reference(kind)
+                if "value" in ref:
+                    ref["ratio"] = round(results[name]["value"] / ref["value"], 4)  # this library / the vendor's
+                results[name]["library_reference"] = ref
+                print(f"[bench] {name} library reference: {ref.get('value', ref.get('error'))}", file=sys.stderr,
+                      flush=True)
     if not args.no_cpu:  # the oracle on this host beside every GPU figure (bounded samples)
         for name in names:
             if name != headline and name in CPU_SAMPLES:
