@@ -103,6 +103,20 @@ __device__ __forceinline__ void gemm_tile_of(int bid, int tiles_m, int tiles_n, 
     tn = in_group / gsize;
 }
 
+// Buffer loads of the nk vector path: a descriptor over the rest of the operand from a uniform
+// base (moved to each K tile's first element), and a 32-bit byte offset per lane. A load at or
+// past num_records reads zeros, so an out-of-range chunk (a row past the edge, the K tail) takes
+// offset kBufOob instead of a branch around its load; num_records is capped below kBufOob. The
+// per-lane offsets stay below 2^31 because gemm_vec_ok sends larger operands to the scalar path.
+constexpr uint32_t kBufOob = 0x7FFFFFF0u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t operand_rsrc(const void *base, int64_t bytes) {
+    const uint32_t n = bytes <= 0 ? 0u : (bytes >= int64_t(kBufOob) ? kBufOob : static_cast<uint32_t>(bytes));
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, n, 0x00020000); // raw, dword data
+}
+__device__ __forceinline__ f32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
 // TB: float, or uint16_t for bf16 weights in the nk layout, widened exactly to
 // fp32 (bits << 16) while staged, so the products are fp32 x fp32 on the
 // matrix core (the reference's rows 2..15 path for bf16 weights).
@@ -119,6 +133,10 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
     constexpr int kA = kAL == ALayout::mk ? BM * LdK : BK * LdM;    // floats of the A stage
     constexpr int kStage = kA + (kB == BLayout::kn ? BK * LdN : BN * LdK);
     __shared__ __attribute__((aligned(16))) float lds[2 * kStage];
+    // nk GEMMs (both operands k-contiguous) load through buffer descriptors, which freed the
+    // registers their split-barrier pipeline needed (4096^3 nk: 1032 -> 977-980 us); the kn and
+    // km layouts keep plain loads (buffer loads measured 1.3% slower on the kn config).
+    constexpr bool kBufLoads = kB == BLayout::nk && kAL == ALayout::mk;
 
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     int tm, tn;
@@ -136,21 +154,28 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
     // 4 consecutive k of one row: 16 bytes of fp32 or 8 bytes of bf16 (widened)
     auto load_rows_k = [&](const auto *src, int row0, int rows_total, int k0, f32x4 *dst, auto count) {
         using T = std::remove_cv_t<std::remove_pointer_t<decltype(src)>>;
+        const T *base = src + int64_t(row0) * K + k0; // this tile's first element of the operand
+        [[maybe_unused]] const auto rsrc =
+            operand_rsrc(base, (int64_t(rows_total - row0) * K - k0) * int64_t(sizeof(T)));
 #pragma unroll
         for (int i = 0; i < decltype(count)::value; ++i) {
             const int idx = tid + T_ * i;
             const int r = idx / (BK / 4), c = (idx % (BK / 4)) * 4;
             const int gr = row0 + r, gk = k0 + c;
             const bool in = gr < rows_total;
-            if constexpr (kVec && std::is_same_v<T, float>) {
+            if constexpr (kVec && !kBufLoads) {
                 dst[i] = (in && gk < K) ? *reinterpret_cast<const f32x4 *>(src + int64_t(gr) * K + gk)
                                         : f32x4{0.f, 0.f, 0.f, 0.f};
             } else if constexpr (kVec) {
-                using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
-                const u32x2 b = (in && gk < K) ? *reinterpret_cast<const u32x2 *>(src + int64_t(gr) * K + gk)
-                                               : u32x2{0u, 0u};
-                dst[i] = f32x4{__builtin_bit_cast(float, b[0] << 16), __builtin_bit_cast(float, b[0] & 0xffff0000u),
-                               __builtin_bit_cast(float, b[1] << 16), __builtin_bit_cast(float, b[1] & 0xffff0000u)};
+                const uint32_t off = (in && gk < K) ? uint32_t(r * K + c) * uint32_t(sizeof(T)) : kBufOob;
+                if constexpr (std::is_same_v<T, float>) {
+                    dst[i] = buf_load16(rsrc, off);
+                } else {
+                    using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+                    const u32x2 b = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, off, 0, 0));
+                    dst[i] = f32x4{__builtin_bit_cast(float, b[0] << 16), __builtin_bit_cast(float, b[0] & 0xffff0000u),
+                                   __builtin_bit_cast(float, b[1] << 16), __builtin_bit_cast(float, b[1] & 0xffff0000u)};
+                }
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -309,7 +334,7 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_f32_mfma_kernel(const fl
     };
     // GemmBig in the nk layout keeps one barrier at the end of each tile: with two fragment sets
     // its load addresses spilled to scratch inside the K loop.
-    constexpr bool kSplitBarrier = !(BM == 256 && BN == 256 && kB == BLayout::nk);
+    constexpr bool kSplitBarrier = true;
     if (kSplitBarrier && kt_begin < kt_end) {
         global_load(kt_begin);
         lds_store(0);
@@ -430,11 +455,15 @@ inline int splitk_factor(int tiles, int ktiles, int target) {
 }
 
 // 16-byte loads need aligned operands and 4-element runs along each contiguous dimension.
+// The nk vector path's buffer offsets reach 256 rows of a k-contiguous operand from a tile's
+// base, in bytes below 2^31 (kBufOob).
 inline bool gemm_vec_ok(const void *a, const void *b, int M, int K, int N, ALayout a_layout, BLayout b_layout) {
     const bool aligned = aligned16(a) && aligned16(b);
     const bool a_runs = a_layout == ALayout::mk ? K % 4 == 0 : M % 4 == 0;
     const bool b_runs = b_layout == BLayout::nk ? K % 4 == 0 : N % 4 == 0;
-    return aligned && a_runs && b_runs;
+    const bool buffer_loads = a_layout == ALayout::mk && b_layout == BLayout::nk;
+    const bool fits = !buffer_loads || int64_t(256) * K * 4 < int64_t(kBufOob);
+    return aligned && a_runs && b_runs && fits;
 }
 
 template <typename Shape, BLayout kB, typename Epi, GemmStore kStore, typename TB = float,
