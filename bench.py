@@ -232,10 +232,10 @@ import json, sys, torch
 kind, n, calls, seed = sys.argv[1], int(sys.argv[2]), int(sys.argv[3]), int(sys.argv[4])
 dev = torch.device("cuda", 0)
 g = torch.Generator(device=dev).manual_seed(seed)
-dt = torch.bfloat16 if kind == "bf16" else torch.float32
+dt = torch.bfloat16 if kind == "bf16" else torch.float32  # kinds: f32 (A @ B), f32nk and bf16 (A @ W^T)
 a = (torch.randn(n, n, device=dev, generator=g) / 64).to(dt)
 b = (torch.randn(n, n, device=dev, generator=g) / 64).to(dt)
-rhs = b.t() if kind == "bf16" else b
+rhs = b if kind == "f32" else b.t()
 out = torch.empty(n, n, device=dev, dtype=dt)
 import time
 t_end = time.perf_counter() + 0.3  # back-to-back calls past the clock ramp, as this library's workloads get
@@ -257,7 +257,7 @@ def library_reference(kind, n=4096, calls=50):
     """The vendor library on the same problem, for comparison only (opt-in, --library-reference):
     torch.matmul (hipBLASLt on ROCm) on n^3 N(0, 1/64) operands, `calls` back-to-back calls
     between two events after 0.3 s of untimed ones (the clock ramp). kind "f32": fp32 A @ B; "bf16": bf16 A @ W^T with
-    a bf16 result (half the output bytes of this library's fp32 result)."""
+    a bf16 result (half the output bytes of this library's fp32 result); "f32nk": fp32 X @ W^T."""
     import subprocess
 
     proc = subprocess.run([sys.executable, "-c", LIBRARY_REFERENCE_CHILD, kind, str(n), str(calls), str(SEED)],
@@ -266,7 +266,8 @@ def library_reference(kind, n=4096, calls=50):
         return {"impl": "torch.matmul", "error": proc.stderr.strip().splitlines()[-1:]}
     r = json.loads(proc.stdout.strip().splitlines()[-1])
     ms = r["ms"]
-    return {"impl": f"torch {r['torch']} matmul ({'bf16 in/out, A @ W^T' if kind == 'bf16' else 'fp32'})",
+    desc = {"f32": "fp32, A @ B", "f32nk": "fp32, X @ W^T", "bf16": "bf16 in/out, A @ W^T"}[kind]
+    return {"impl": f"torch {r['torch']} matmul ({desc})",
             "ms": round(ms, 5), "value": round(2.0 * n ** 3 / ms / 1e9, 2), "unit": "TFLOP/s"}
 
 
@@ -304,6 +305,20 @@ def wl_gemm_bf16(stream, steps, warmup):
     tf = flop / ms / 1e9
     return {"workload": "gemm_bf16_relu_bias_4096^3", "unit": "TFLOP/s", "value": tf, "ms": ms, "flop": flop,
             "kernel": "gemm_bf16_mfma_kernel<bf16>", "roofline": roofline(tf, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma")}
+
+
+def wl_linear(stream, steps, warmup):
+    """ops::linear at config 3's size: Y = X W^T with X [4096][4096] and W [4096][4096] in the HF
+    [out][in] layout (the GEMM's nk form, both operands k-contiguous), fp32, no bias; 2*4096^3 flop."""
+    n = 4096
+    X, W, Y = (ow.DeviceBuffer.empty(n * n) for _ in range(3))
+    ow.fill_normal(X, SEED, 300, 0.0, 1.0 / 64, stream=stream)
+    ow.fill_normal(W, SEED, 301, 0.0, 1.0 / 64, stream=stream)
+    ms = Timer(stream).run(lambda i: ow.ops.linear(X, W, Y, n, n, n, stream=stream), steps, warmup)
+    flop = 2.0 * n ** 3
+    tf = flop / ms / 1e9
+    return {"workload": "linear_f32_4096^3_hf_weights", "unit": "TFLOP/s", "value": tf, "ms": ms, "flop": flop,
+            "kernel": "gemm_f32_mfma_kernel<nk>", "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma")}
 
 
 def wl_attention(stream, steps, warmup):
@@ -480,7 +495,7 @@ def wl_gather(stream, steps, warmup):
             "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("gather"))}
 
 
-WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "layernorm": wl_layernorm, "gemm": wl_gemm, "gemm_bf16": wl_gemm_bf16, "attention": wl_attention,
+WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm": wl_rmsnorm, "layernorm": wl_layernorm, "gemm": wl_gemm, "gemm_bf16": wl_gemm_bf16, "linear": wl_linear, "attention": wl_attention,
              "attention_decode": wl_attention_decode, "scan": wl_scan, "transpose": wl_transpose,
              "gather": wl_gather, "llama": wl_llama,
              # the reference's published configurations (README.md:320-339, RTX 4080 SUPER, 128 new tokens)
@@ -495,7 +510,7 @@ HEADLINE = "llama"
 
 
 # --------------------------------------------------------------- CPU baseline
-CPU_SAMPLES = ("map", "reduce", "softmax", "rmsnorm", "layernorm", "gemm", "gemm_bf16", "attention", "attention_decode", "scan",
+CPU_SAMPLES = ("map", "reduce", "softmax", "rmsnorm", "layernorm", "gemm", "gemm_bf16", "linear", "attention", "attention_decode", "scan",
                "transpose", "gather", "llama", "llama_bf16")
 
 
@@ -567,6 +582,13 @@ def _cpu_work(name: str):
                 2.0 * len(sample) * n * n / 1e12, "TFLOP/s",
                 f"oracle orc_mat_mul_rows (fp32, plus its float64 |a·b| bound), {len(sample)} of the 4096 rows of "
                 "relu(A·B+bias)", 3.0)
+    if name == "linear":
+        n, sample = 4096, np.arange(0, 4096, 64)
+        X = orc.fill_normal(n * n, SEED, 300, 0.0, 1.0 / 64, mt=True)
+        W = orc.fill_normal(n * n, SEED, 301, 0.0, 1.0 / 64, mt=True)
+        return (lambda: orc.mat_mul_rows(X, W, n, n, n, rows=sample, b_transposed=True),
+                2.0 * len(sample) * n * n / 1e12, "TFLOP/s",
+                f"oracle orc_mat_mul_rows (fp32, W in [out][in]), {len(sample)} of the 4096 rows of X W^T", 3.0)
     if name == "attention":
         T, qh, kvh, D = 2048, 32, 8, 64
         q = orc.fill_normal(qh * T * D, SEED, 400, 0.0, 1.0, mt=True)
@@ -691,7 +713,7 @@ def main() -> int:
         print(f"[bench] {name}: {results[name]['value']:.1f} {results[name]['unit']} "
               f"({results[name]['ms']:.4f} ms/step)", file=sys.stderr, flush=True)
     if args.library_reference:  # after every workload of this library, so it cannot disturb them
-        for name, kind in (("gemm", "f32"), ("gemm_bf16", "bf16")):
+        for name, kind in (("gemm", "f32"), ("gemm_bf16", "bf16"), ("linear", "f32nk")):
             if name in results:
                 ref = library_reference(kind)
                 if "value" in ref:
