@@ -49,6 +49,15 @@ int opw_event_destroy(void *event);
 int opw_event_record(void *event, void *stream);
 int opw_event_synchronize(void *event);
 int opw_event_elapsed_ms(void *start, void *stop, float *ms);
+/* HIP graph capture (global mode) of what is enqueued on `stream` (a created stream, not NULL)
+ * between begin and end; end instantiates it into *graph_exec. The reference's equivalent is the
+ * caller's own cudaStreamBeginCapture around its ops (tests/unit/framework.cu:154-169); these exist
+ * so a host without HIP headers can capture and replay library calls. A capture the runtime
+ * refuses (an allocation or synchronization while it is open) returns -1 with its message. */
+int opw_graph_capture_begin(void *stream);
+int opw_graph_capture_end(void *stream, void **graph_exec);
+int opw_graph_launch(void *graph_exec, void *stream);
+int opw_graph_destroy(void *graph_exec);
 
 /* ---- seeded synthetic inputs (counter-based; bit-identical to the CPU
  * restatement in oracle/, so the checker regenerates the same arrays) ---- */
@@ -128,8 +137,10 @@ int opw_convert_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, void *st
 int opw_attention_prefill_f32(const float *q_heads, const float *kcache, const float *vcache, float *out, int T, int S,
                               int q_offset, int num_q_heads, int kv_rep, int head_dim, int cap, void *stream);
 /* One query per head against `len` cache entries (reference: ops::attention_decode,
- * include/ops/attention_decode.cuh:99-109; q/out [num_q_heads][head_dim], len <= 8192).
- * Scratch comes from stream-ordered allocation ... */
+ * include/ops/attention_decode.cuh:98-109; q/out [num_q_heads][head_dim], len <= 8192). The
+ * reference's contract: one launch, nothing allocated (graph-capturable), head_dim in [1, 64], q and
+ * caches at any 4-byte alignment, any kv_rep; q head h reads kv head h / kv_rep, so the caches hold
+ * ceil(num_q_heads / kv_rep) kv heads of max_seq rows. */
 int opw_attention_decode_f32(const float *q, const float *kcache, const float *vcache, float *out, int num_q_heads,
                              int kv_rep, int head_dim, int len, int max_seq, void *stream);
 /* ... or from a caller workspace of opw_attention_decode_workspace_size() floats (no allocation). */

@@ -22,7 +22,7 @@ PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "lib" / "libopworks_amd.so"
 
 __all__ = [
-    "OpworksError", "lib", "DeviceBuffer", "DeviceView", "Stream", "Event", "ops", "fill_uniform", "fill_normal",
+    "OpworksError", "lib", "DeviceBuffer", "DeviceView", "Stream", "Event", "Graph", "ops", "fill_uniform", "fill_normal",
     "device_name", "device_count", "synchronize", "cu_count",
 ]
 
@@ -55,6 +55,10 @@ _SIGNATURES = {
     "opw_event_record": (c_int, [c_void_p, c_void_p]),
     "opw_event_synchronize": (c_int, [c_void_p]),
     "opw_event_elapsed_ms": (c_int, [c_void_p, c_void_p, POINTER(c_float)]),
+    "opw_graph_capture_begin": (c_int, [c_void_p]),
+    "opw_graph_capture_end": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "opw_graph_launch": (c_int, [c_void_p, c_void_p]),
+    "opw_graph_destroy": (c_int, [c_void_p]),
     "opw_fill_uniform_f32": (c_int, [c_void_p, c_int64, c_uint64, c_uint64, c_float, c_float, c_void_p]),
     "opw_fill_normal_f32": (c_int, [c_void_p, c_int64, c_uint64, c_uint64, c_float, c_float, c_void_p]),
     "opw_map_scale_add_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_float, c_void_p]),
@@ -203,6 +207,38 @@ class Event:
     def __del__(self) -> None:
         if getattr(self, "handle", None) and _lib is not None:
             _lib.opw_event_destroy(self.handle)
+            self.handle = None
+
+
+class Graph:
+    """A HIP graph captured from the library calls enqueued on one Stream:
+
+        g = Graph.capture(stream, lambda: ops.attention_decode(..., stream=stream))
+        g.launch(stream)
+
+    Capture runs in global mode, so a call that allocates or synchronizes while it is open
+    makes capture fail with OpworksError."""
+
+    def __init__(self, handle: int) -> None:
+        self.handle = handle
+
+    @classmethod
+    def capture(cls, stream: "Stream", body) -> "Graph":
+        check(lib().opw_graph_capture_begin(stream.handle))
+        try:
+            body()
+        finally:
+            h = c_void_p()
+            rc = lib().opw_graph_capture_end(stream.handle, ctypes.byref(h))
+        check(rc)
+        return cls(h.value)
+
+    def launch(self, stream: "Stream") -> None:
+        check(lib().opw_graph_launch(self.handle, stream.handle))
+
+    def __del__(self) -> None:
+        if getattr(self, "handle", None) and _lib is not None:
+            _lib.opw_graph_destroy(self.handle)
             self.handle = None
 
 

@@ -210,6 +210,54 @@ int opw_device_synchronize(void) {
     });
 }
 
+// Graph capture of the work enqueued on one library stream, in global mode as the reference's
+// framework test captures (tests/unit/framework.cu:154-169): a capture-unsafe call such as a
+// blocking allocation or a synchronization while it is open invalidates it. A capture that the
+// runtime refuses comes back as -1 with the runtime's message instead of aborting.
+static void capture_check(hipError_t st, const char *what) {
+    if (st != hipSuccess)
+        throw std::runtime_error(std::string(what) + " failed: " + hipGetErrorString(st));
+}
+
+int opw_graph_capture_begin(void *stream) {
+    return guard([&] {
+        opworks::detail::require(stream != nullptr, "graph capture needs a created stream, not the null stream");
+        capture_check(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeGlobal),
+                      "hipStreamBeginCapture");
+        return 0;
+    });
+}
+
+int opw_graph_capture_end(void *stream, void **graph_exec) {
+    return guard([&] {
+        opworks::detail::require(stream != nullptr && graph_exec != nullptr, "null stream or graph pointer");
+        hipGraph_t graph = nullptr;
+        capture_check(hipStreamEndCapture(as_stream(stream), &graph), "hipStreamEndCapture");
+        hipGraphExec_t exec = nullptr;
+        const hipError_t st = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        OPWORKS_HIP_CHECK(hipGraphDestroy(graph));
+        capture_check(st, "hipGraphInstantiate");
+        *graph_exec = exec;
+        return 0;
+    });
+}
+
+int opw_graph_launch(void *graph_exec, void *stream) {
+    return guard([&] {
+        opworks::detail::require(graph_exec != nullptr, "null graph");
+        OPWORKS_HIP_CHECK(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), as_stream(stream)));
+        return 0;
+    });
+}
+
+int opw_graph_destroy(void *graph_exec) {
+    return guard([&] {
+        if (graph_exec)
+            OPWORKS_HIP_CHECK(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)));
+        return 0;
+    });
+}
+
 int opw_event_create(void **event) {
     return guard([&] {
         opworks::detail::require(event != nullptr, "null event pointer");

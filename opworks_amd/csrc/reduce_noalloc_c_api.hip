@@ -41,8 +41,11 @@ struct Product {
 
 // Device address of `scratch` on the current device, looked up once per device
 // with that device current. Host code passes this pointer, never the array's
-// name (a host-side stand-in).
-float *scratch_on_current_device() {
+// name (a host-side stand-in). The lookup is set-up work, not stream work, so it
+// is done on a call made outside graph capture: a first call on a device that
+// arrives while `s` is capturing is refused instead of resolving the symbol
+// inside the capture.
+float *scratch_on_current_device(hipStream_t s) {
     static std::mutex lock;
     static std::array<float *, opworks::detail::kMaxDevices> addresses{};
     int dev = 0;
@@ -51,6 +54,12 @@ float *scratch_on_current_device() {
     std::lock_guard<std::mutex> hold(lock);
     float *&p = addresses[static_cast<size_t>(dev)];
     if (!p) {
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        if (s != nullptr)
+            OPWORKS_HIP_CHECK(hipStreamIsCapturing(s, &capture));
+        opworks::detail::require(capture == hipStreamCaptureStatusNone,
+                                 "opw_reduce_f32_noalloc: make the first call on a device outside graph capture "
+                                 "(it looks up the device's scratch address)");
         void *addr = nullptr;
         const hipError_t st = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
         if (st != hipSuccess)
@@ -61,7 +70,7 @@ float *scratch_on_current_device() {
 }
 
 template <typename Op> void reduce_into_scratch(const float *in, float *out, int n, hipStream_t s) {
-    opworks::ops::reduce<Op>(in, out, n, opworks::DeviceSpan<float>(scratch_on_current_device(), kNoAllocPartials), s);
+    opworks::ops::reduce<Op>(in, out, n, opworks::DeviceSpan<float>(scratch_on_current_device(s), kNoAllocPartials), s);
 }
 
 } // namespace

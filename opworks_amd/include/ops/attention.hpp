@@ -805,6 +805,128 @@ __global__ __launch_bounds__(kAttnMaxRep *kWaveSize) static void attention_decod
     decode_combine_head<false>(a, blockIdx.x * a.kv_rep + wave, nrec, lane);
 }
 
+// ---- decode, scratch-free form (the reference signature) -----------------------------------
+// ops::attention_decode keeps the reference's contract (include/ops/attention_decode.cuh:98-109):
+// no workspace and no allocation, any head_dim <= 64, q and caches at any 4-byte alignment, any
+// kv_rep, and num_q_heads need not be a multiple of kv_rep (q head h reads kv head h / kv_rep).
+// With no scratch there is nowhere to leave split-KV records, so one workgroup owns a q head, as
+// in the reference's grid. Its kSingleWaves waves take kSingleKeys-key chunks round robin, each
+// wave with its own online-softmax state (m, l, unnormalised acc), and the wave states are merged
+// in wave order at the end. A chunk is a contiguous run of n * D floats of the cache: K and V are
+// read together with coalesced 4-byte buffer loads (one memory round trip per chunk; lanes past
+// the chunk read zeros from the descriptor's range check) and staged in the wave's own LDS rows
+// of kAttnMaxD + 1 floats, an odd stride, so the lane = key reads of the score loop hit distinct
+// banks. Scores are the d-ascending fmaf chain of the reference's dot product; P V (lane = d) is
+// key-ascending within a chunk.
+// Workgroup b serves q head (b % 8) * (qh / 8) + b / 8 when 8 divides qh: under the round-robin
+// dispatch of workgroups to the 8 XCDs, consecutive q heads, which share a kv head, then run on
+// one XCD and read their K/V through the same L2.
+constexpr int kSingleWaves = 8;
+constexpr int kSingleKeys = 32;
+constexpr int kSingleStride = kAttnMaxD + 1;
+constexpr int kSinglePer = kSingleKeys * kAttnMaxD / kWaveSize; // chunk floats per lane at most
+
+__global__ __launch_bounds__(kSingleWaves *kWaveSize) static void attention_decode_single_kernel(
+    const float *__restrict__ q, const float *__restrict__ kcache, const float *__restrict__ vcache,
+    float *__restrict__ out, int num_q_heads, int kv_rep, int D, int len, int max_seq, float scale) {
+    __shared__ float Qs[kAttnMaxD];
+    __shared__ float Ks[kSingleWaves][kSingleKeys * kSingleStride];
+    __shared__ float Vs[kSingleWaves][kSingleKeys * kSingleStride];
+    __shared__ float Ps[kSingleWaves][kSingleKeys];
+    __shared__ float Wm[kSingleWaves], Wl[kSingleWaves];
+    __shared__ float Wacc[kSingleWaves][kAttnMaxD];
+    const int b = blockIdx.x;
+    const int h = num_q_heads % 8 == 0 ? (b % 8) * (num_q_heads / 8) + b / 8 : b;
+    const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
+    const int64_t kv_base = int64_t(h / kv_rep) * max_seq * D;
+    if (threadIdx.x < D)
+        Qs[threadIdx.x] = q[int64_t(h) * D + threadIdx.x];
+    __syncthreads();
+    // element e = lane + 64 i of a chunk is key e / D, dimension e % D; stepped without division
+    const int key0 = lane / D, d0 = lane % D, key_step = kWaveSize / D, d_step = kWaveSize % D;
+    const int per = (kSingleKeys * D + kWaveSize - 1) / kWaveSize; // loads per lane per chunk
+    float *ks = Ks[wave], *vs = Vs[wave];
+    float m = kNegInf, l = 0.f, acc = 0.f;
+    for (int c0 = wave * kSingleKeys; c0 < len; c0 += kSingleWaves * kSingleKeys) {
+        const int n = len - c0 < kSingleKeys ? len - c0 : kSingleKeys;
+        const int64_t off = kv_base + int64_t(c0) * D;
+        const __amdgpu_buffer_rsrc_t ksrc = operand_rsrc(kcache + off, int64_t(n) * D * 4);
+        const __amdgpu_buffer_rsrc_t vsrc = operand_rsrc(vcache + off, int64_t(n) * D * 4);
+        float kr[kSinglePer], vr[kSinglePer];
+#pragma unroll
+        for (int i = 0; i < kSinglePer; ++i) {
+            if (i < per) {
+                kr[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ksrc, 4 * lane, 4 * kWaveSize * i, 0));
+                vr[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vsrc, 4 * lane, 4 * kWaveSize * i, 0));
+            }
+        }
+        {
+            int key = key0, d = d0;
+#pragma unroll
+            for (int i = 0; i < kSinglePer; ++i) {
+                if (i < per && key < n) {
+                    ks[key * kSingleStride + d] = kr[i];
+                    vs[key * kSingleStride + d] = vr[i];
+                }
+                key += key_step;
+                d += d_step;
+                if (d >= D) {
+                    d -= D;
+                    ++key;
+                }
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        float s = 0.f;
+        if (lane < n)
+            for (int d = 0; d < D; ++d)
+                s = fmaf(Qs[d], ks[lane * kSingleStride + d], s);
+        const float sc = lane < n ? s * scale : kNegInf;
+        const float mn = fmaxf(m, wave::max(sc)); // finite: the chunk has at least one key
+        const float corr = m == kNegInf ? 0.f : expf(m - mn);
+        const float p = lane < n ? expf(sc - mn) : 0.f;
+        l = l * corr + wave::sum(p);
+        m = mn;
+        if (lane < kSingleKeys)
+            Ps[wave][lane] = p;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < D) {
+            float o = acc * corr;
+            for (int k = 0; k < n; ++k)
+                o = fmaf(Ps[wave][k], vs[k * kSingleStride + lane], o);
+            acc = o;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if (lane < D)
+        Wacc[wave][lane] = acc;
+    if (lane == 0) {
+        Wm[wave] = m;
+        Wl[wave] = l;
+    }
+    __syncthreads();
+    if (wave != 0 || lane >= D)
+        return;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kSingleWaves; ++w)
+        M = fmaxf(M, Wm[w]);
+    float L = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSingleWaves; ++w) {
+        const float f = Wm[w] == kNegInf ? 0.f : expf(Wm[w] - M); // a wave past the length holds nothing
+        L = fmaf(Wl[w], f, L);
+        o = fmaf(Wacc[w][lane], f, o);
+    }
+    out[int64_t(h) * D + lane] = o / L;
+}
+
 // Enqueues the partial and combine kernels (or the fused partial kernel alone
 // when a.counters is set): grid (kvh, max_chunks) with kv_rep rounded up to a
 // power of two waves per workgroup.
@@ -952,19 +1074,21 @@ inline void attention_decode_fused(const float *q, const float *kcache, const fl
                                      workspace_size, nullptr, 0, 0, counters, stream);
 }
 
-// Reference signature (include/ops/attention_decode.cuh:99-109): scratch comes
-// from stream-ordered allocation.
+// Reference signature and contract (include/ops/attention_decode.cuh:98-109): one
+// scratch-free launch that allocates nothing, so it can be captured in a graph;
+// accepts any head_dim in [1, 64], any 4-byte alignment of q and the caches, and
+// any kv_rep (q head h reads kv head h / kv_rep). The caches hold
+// ceil(num_q_heads / kv_rep) kv heads of max_seq rows.
 inline void attention_decode(const float *q, const float *kcache, const float *vcache, float *out, int num_q_heads,
                              int kv_rep, int head_dim, int len, int max_seq, hipStream_t stream = nullptr) {
-    detail::require(num_q_heads > 0 && kv_rep > 0 && head_dim > 0, "attention_decode requires positive head shape");
-    detail::require(len > 0 && len <= max_seq, "attention_decode length outside the cache capacity");
-    detail::require(len <= detail::kAttnDecodeMaxLen, "attention_decode length exceeds the shared-memory kernel limit");
-    const int ws = attention_decode_workspace_size(num_q_heads, len, head_dim);
-    float *scratch = nullptr;
-    OPWORKS_HIP_CHECK(hipMallocAsync(reinterpret_cast<void **>(&scratch), sizeof(float) * ws, stream));
-    attention_decode_ws(q, kcache, vcache, out, num_q_heads, kv_rep, head_dim, len, max_seq, scratch, ws, nullptr, 0,
-                        0, stream);
-    OPWORKS_HIP_CHECK(hipFreeAsync(scratch, stream));
+    detail::require(num_q_heads > 0 && kv_rep > 0 && head_dim > 0, "attention_decode: head counts and head_dim must be positive");
+    detail::require(head_dim <= detail::kAttnMaxD, "attention_decode: head_dim must be at most 64");
+    detail::require(len > 0 && len <= max_seq, "attention_decode: len must be in [1, max_seq]");
+    detail::require(len <= detail::kAttnDecodeMaxLen, "attention_decode: len must be at most 8192");
+    detail::require(q && kcache && vcache && out, "attention_decode: null pointer");
+    const float scale = 1.f / std::sqrt(static_cast<float>(head_dim));
+    launch_async(stream, detail::attention_decode_single_kernel, num_q_heads, detail::kSingleWaves * kWaveSize,
+                         q, kcache, vcache, out, num_q_heads, kv_rep, head_dim, len, max_seq, scale);
 }
 
 } // namespace opworks::ops

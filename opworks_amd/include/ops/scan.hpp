@@ -23,11 +23,18 @@
 // its association is fixed by the unit index alone: the result is the same
 // bit pattern on every run, whatever order the workgroups ran in. The last
 // unit of a group publishes the group total (a scan over its 64 unit totals)
-// and the last group's last unit the super-group total, so no unit waits on
-// a chain longer than three levels. Totals travel as 64-bit words holding the
-// value and a valid flag, written and read with agent-scope atomics (sc1
-// accesses, coherent across the XCDs' L2 caches). Every wait is on a lower
-// unit, bounded, and counts a timeout into the workspace.
+// and the last group's last unit the super-group total. A unit waits on unit
+// and group totals of its own super group, which do not chain; the super-group
+// totals do form a chain, since the unit that closes super group s publishes
+// after its workgroup barrier, which follows its wait for the totals of super
+// groups 0 .. s-1 (at most 2^31 / 2^26 = 32 links). Totals travel as 64-bit
+// words holding the value and flags, written and read with agent-scope atomics
+// (sc1 accesses, coherent across the XCDs' L2 caches). Every wait is on a lower
+// unit and bounded: a wait that gives up counts a timeout into the workspace
+// and poisons the unit, whose outputs are then NaN (for the prefix maximum as
+// well, where a NaN operand would otherwise vanish in fmaxf), and so is every
+// group or super-group total it publishes; a unit that reads a poisoned total
+// is poisoned in turn.
 //
 // A fill kernel clears the counter and the flags before each scan, so the
 // workspace can be any caller memory. A tile is then rescanned in four rounds
@@ -120,24 +127,34 @@ inline ScanLayout scan_pair_layout(int n) {
     return {pairs, groups, (groups + kScanGroup - 1) / kScanGroup};
 }
 
-__device__ __forceinline__ uint64_t scan_publishable(float v) {
-    return (uint64_t(1) << 32) | __builtin_bit_cast(uint32_t, v);
-}
+// High half of a published word: bit 0 = published, bit 1 = poisoned (the total depends on a
+// wait that gave up).
+constexpr uint32_t kScanPublished = 1u, kScanPoisoned = 2u;
 
-__device__ __forceinline__ void scan_publish(uint64_t *slot, float v) {
-    __hip_atomic_store(slot, scan_publishable(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void scan_publish(uint64_t *slot, float v, bool poisoned = false) {
+    const uint64_t flags = kScanPublished | (poisoned ? kScanPoisoned : 0u);
+    __hip_atomic_store(slot, (flags << 32) | __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Polls a published total of a lower tile (agent-coherent 64-bit loads, so the value and its
-// flag arrive together). A wait that outlasts kScanSpinLimit polls counts itself in `timeouts`
-// and returns NaN, so a broken protocol ends the kernel and shows in the output.
-__device__ __forceinline__ float scan_wait_total(const uint64_t *slot, uint32_t *timeouts) {
+// flags arrive together). A wait that outlasts `spin_limit` polls counts itself in `timeouts`,
+// sets `poisoned` and returns NaN; so does reading a poisoned total, without the count.
+__device__ __forceinline__ float scan_wait_total(const uint64_t *slot, uint32_t *timeouts, bool &poisoned,
+                                                 int spin_limit = kScanSpinLimit) {
     for (int spin = 0;; ++spin) {
         const uint64_t w = __hip_atomic_load(const_cast<uint64_t *>(slot), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (w >> 32)
+        const uint32_t flags = uint32_t(w >> 32);
+        if (flags & kScanPublished) {
+            if (flags & kScanPoisoned) {
+                poisoned = true;
+                return __builtin_nanf("");
+            }
             return __builtin_bit_cast(float, uint32_t(w));
-        if (spin == kScanSpinLimit) {
+        }
+        if (spin >= spin_limit) {
             __hip_atomic_fetch_add(timeouts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            poisoned = true;
             return __builtin_nanf("");
         }
         __builtin_amdgcn_s_sleep(2);
@@ -180,7 +197,7 @@ __device__ __forceinline__ void scan_tile_local(const f32x4 (&x)[kScanRounds], f
 template <typename Op, bool kPacked, bool kInclusive>
 __device__ __forceinline__ void scan_tile_emit(float *out, int64_t base, int64_t n, float &carry,
                                                const f32x4 (&s)[kScanRounds], const float (&lane_excl)[kScanRounds],
-                                               const float (*wave_tot)[kScanWaves], int wid) {
+                                               const float (*wave_tot)[kScanWaves], int wid, bool poisoned = false) {
 #pragma unroll
     for (int r = 0; r < kScanRounds; ++r) {
         float before = carry, round_total = carry;
@@ -202,6 +219,8 @@ __device__ __forceinline__ void scan_tile_emit(float *out, int64_t base, int64_t
             for (int k = 1; k < 4; ++k)
                 y[k] = Op::combine(b0, s[r][k - 1]);
         }
+        if (poisoned)
+            y = f32x4{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
         const int64_t e = base + int64_t(r) * kScanRound + 4 * threadIdx.x;
         if (kPacked && e + 4 <= n) {
             __builtin_nontemporal_store(y, reinterpret_cast<f32x4 *>(out + e));
@@ -219,13 +238,17 @@ __device__ __forceinline__ void scan_tile_emit(float *out, int64_t base, int64_t
 struct ScanPrefixLds {
     float level[3]; // exclusive prefixes over super groups, groups, units
     float own_group_total;
+    int poisoned[3]; // the wave's level depends on a wait that gave up
 };
 
 // The exclusive prefix of unit t whose total is `total` (every thread calls this; it
 // publishes the unit's total and, for the last unit of a group or super group, that total).
+// `poisoned` is set in every thread when the prefix depends on a wait that gave up; the
+// returned prefix is then NaN.
 template <typename Op>
 __device__ __forceinline__ float scan_unit_prefix(uint32_t *ws, const ScanLayout &lay, int t, float total,
-                                                  ScanPrefixLds &sh, int wid, int lane) {
+                                                  ScanPrefixLds &sh, int wid, int lane, bool &poisoned,
+                                                  int spin_limit = kScanSpinLimit) {
     uint64_t *unit_tot = reinterpret_cast<uint64_t *>(ws + kScanHeaderWords);
     uint64_t *group_tot = unit_tot + lay.units;
     uint64_t *super_tot = group_tot + lay.groups;
@@ -243,16 +266,20 @@ __device__ __forceinline__ float scan_unit_prefix(uint32_t *ws, const ScanLayout
                               : wid == 1 ? group_tot + int64_t(sg) * kScanGroup
                                          : super_tot;
         const int count = wid == 0 ? j : wid == 1 ? gj : sg;
+        bool lane_bad = false;
         if (lane < count)
-            v = scan_wait_total(src + lane, timeouts);
+            v = scan_wait_total(src + lane, timeouts, lane_bad, spin_limit);
         if (wid == 0 && lane == kWaveSize - 1)
             v = total;
+        const bool wave_bad = __builtin_amdgcn_ballot_w64(lane_bad) != 0;
         const float incl = wave_inclusive_scan<Op>(v);
         const float before = count == 0 ? Op::identity() : wave::readlane(incl, count - 1);
-        if (lane == 0)
+        if (lane == 0) {
             sh.level[wid] = before;
+            sh.poisoned[wid] = wave_bad;
+        }
         if (wid == 0 && closes_group && lane == kWaveSize - 1) {
-            scan_publish(group_tot + g, incl);
+            scan_publish(group_tot + g, incl, wave_bad);
             sh.own_group_total = incl;
         }
     }
@@ -260,8 +287,11 @@ __device__ __forceinline__ float scan_unit_prefix(uint32_t *ws, const ScanLayout
     if (closes_super && wid == 1) {
         const float incl = wave_inclusive_scan<Op>(lane == kWaveSize - 1 ? sh.own_group_total : v);
         if (lane == kWaveSize - 1)
-            scan_publish(super_tot + sg, incl);
+            scan_publish(super_tot + sg, incl, sh.poisoned[0] || sh.poisoned[1]);
     }
+    poisoned = sh.poisoned[0] || sh.poisoned[1] || sh.poisoned[2];
+    if (poisoned)
+        return __builtin_nanf("");
     return Op::combine(Op::combine(sh.level[2], sh.level[1]), sh.level[0]);
 }
 
@@ -298,7 +328,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(const float *in, flo
 // pair, no workspace.
 template <typename Op, bool kPacked, bool kInclusive, bool kOnePass>
 __global__ __launch_bounds__(kScanThreads) void scan_pair_kernel(const float *in, float *out, uint32_t *ws,
-                                                                 ScanLayout lay, int64_t n) {
+                                                                 ScanLayout lay, int64_t n, int spin_limit) {
     __shared__ float wave_tot[kScanRounds][kScanWaves];
     __shared__ float wave_tot_b[kScanWaves];
     __shared__ ScanPrefixLds sh;
@@ -347,6 +377,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_pair_kernel(const float *in
     }
     __syncthreads();
     float carry = Op::identity();
+    bool poisoned = false;
     if constexpr (kOnePass) {
         float total_a = Op::identity(), total_b = Op::identity();
 #pragma unroll
@@ -357,9 +388,9 @@ __global__ __launch_bounds__(kScanThreads) void scan_pair_kernel(const float *in
 #pragma unroll
         for (int w = 0; w < kScanWaves; ++w)
             total_b = Op::combine(total_b, wave_tot_b[w]);
-        carry = scan_unit_prefix<Op>(ws, lay, t, Op::combine(total_a, total_b), sh, wid, lane);
+        carry = scan_unit_prefix<Op>(ws, lay, t, Op::combine(total_a, total_b), sh, wid, lane, poisoned, spin_limit);
     }
-    scan_tile_emit<Op, kPacked, kInclusive>(out, base_a, n, carry, s, lane_excl, wave_tot, wid);
+    scan_tile_emit<Op, kPacked, kInclusive>(out, base_a, n, carry, s, lane_excl, wave_tot, wid, poisoned);
     __syncthreads(); // tile A's wave totals have been read
     {
         f32x4 xb[kScanRounds];
@@ -369,7 +400,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_pair_kernel(const float *in
         scan_tile_local<Op>(xb, s, lane_excl, wave_tot, wid, lane);
     }
     __syncthreads();
-    scan_tile_emit<Op, kPacked, kInclusive>(out, base_b, n, carry, s, lane_excl, wave_tot, wid);
+    scan_tile_emit<Op, kPacked, kInclusive>(out, base_b, n, carry, s, lane_excl, wave_tot, wid, poisoned);
 }
 
 
@@ -382,7 +413,7 @@ void scan_launch(const float *in, float *out, int n, float *workspace, hipStream
     const ScanLayout lay = scan_pair_layout(n);
     if (lay.units == 1) {
         launch_async(stream, scan_pair_kernel<Op, kPacked, kInclusive, false>, 1, kScanThreads, in, out,
-                     static_cast<uint32_t *>(nullptr), lay, static_cast<int64_t>(n));
+                     static_cast<uint32_t *>(nullptr), lay, static_cast<int64_t>(n), kScanSpinLimit);
         return;
     }
     uint32_t *ws = reinterpret_cast<uint32_t *>(workspace);
@@ -390,7 +421,7 @@ void scan_launch(const float *in, float *out, int n, float *workspace, hipStream
     launch_async(stream, scan_clear_kernel, static_cast<int>(blocks_for64(quads, 256)), 256,
                  reinterpret_cast<uint4 *>(ws), quads);
     launch_async(stream, scan_pair_kernel<Op, kPacked, kInclusive, true>, lay.units, kScanThreads, in, out, ws, lay,
-                 static_cast<int64_t>(n));
+                 static_cast<int64_t>(n), kScanSpinLimit);
 }
 
 template <typename Op>

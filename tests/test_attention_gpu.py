@@ -124,8 +124,9 @@ def test_config4_prefill_full_size_sampled(ow, orc):
 @pytest.mark.parametrize("length", [1, 100, 1000])
 def test_decode_head_shapes(ow, orc, qh, kv_rep, D, length):
     """Other GQA ratios (kv_rep 3 rounds up to 4 waves, 5-7 up to 8, partly idle) and head sizes (D = 4, 12,
-    60: head-dim packs past D are padding in the register-blocked chunk); the one-launch form matches the
-    two-launch form bit for bit on every shape."""
+    60: head-dim packs past D are padding in the register-blocked chunk): the reference-signature op and the
+    split-KV form against the oracle, and the one-launch split-KV form matches the two-launch form bit for bit
+    on every shape."""
     cap = 1024
     kvh = qh // kv_rep
     q = orc.fill_normal(qh * D, SEED, 20, 0.0, 1.0)
@@ -140,10 +141,115 @@ def test_decode_head_shapes(ow, orc, qh, kv_rep, D, length):
     check(got, ref, bound[:, 0])
     ws_n = ow.ops.attention_decode_workspace_size(qh, length, D)
     ws = ow.DeviceBuffer.empty(ws_n)
+    two = ow.DeviceBuffer.empty(qh * D)
+    ow.ops.attention_decode(dq, dk, dv, two, qh, kv_rep, D, length, cap, workspace=ws)
+    check(two.to_host().reshape(qh, D), ref, bound[:, 0])
     counters = ow.DeviceBuffer.from_host(np.zeros(ow.ops.attention_decode_counters_size(qh, kv_rep), np.int32))
     fused = ow.DeviceBuffer.empty(qh * D)
     ow.ops.attention_decode_fused(dq, dk, dv, fused, qh, kv_rep, D, length, cap, ws, ws_n, counters)
-    assert np.array_equal(fused.to_host().view(np.uint32), out.to_host().view(np.uint32))
+    assert np.array_equal(fused.to_host().view(np.uint32), two.to_host().view(np.uint32))
+
+
+def decode_f64(q, k, v, qh, kv_rep, D, length, cap):
+    """Float64 decode attention of q head h over kv head h // kv_rep, and the bar's magnitude
+    sum_j p_j |v_j| per output."""
+    q = q.reshape(qh, D).astype(np.float64)
+    out, bound = np.empty((qh, D)), np.empty((qh, D))
+    for h in range(qh):
+        base = (h // kv_rep) * cap * D
+        kh = k[base:base + length * D].reshape(length, D).astype(np.float64)
+        vh = v[base:base + length * D].reshape(length, D).astype(np.float64)
+        s = kh @ q[h] / np.sqrt(D)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        out[h], bound[h] = p @ vh, p @ np.abs(vh)
+    return out, bound
+
+
+def offset_upload(ow, arr):
+    """arr placed one float into its device buffer: 4-byte aligned, not 16 (the view keeps the buffer alive)."""
+    buf = upload(ow, np.concatenate([np.float32([7.0]), np.ascontiguousarray(arr, np.float32)]))
+    return buf.offset(1, arr.size)
+
+
+@pytest.mark.parametrize("qh,kv_rep,D", [(4, 4, 1), (6, 2, 5), (8, 4, 63), (64, 32, 64), (5, 2, 64), (3, 8, 17),
+                                         (32, 4, 64), (16, 1, 33)])
+@pytest.mark.parametrize("length", [1, 31, 33, 257, 2048])
+def test_decode_reference_contract(ow, orc, qh, kv_rep, D, length):
+    """ops::attention_decode under the reference's own contract (include/ops/attention_decode.cuh:98-109):
+    head_dim 1, 5, 17, 33 and 63; q, both caches and the output one float into their allocations (4-byte
+    aligned only); kv_rep 32; head counts that kv_rep does not divide (q head h reads kv head h // kv_rep of
+    ceil(qh / kv_rep)); against the oracle's restatement of the reference kernel and float64."""
+    cap = length + 3
+    kvh = -(-qh // kv_rep)
+    q = orc.fill_normal(qh * D, SEED, 50, 0.0, 1.0)
+    k = orc.fill_normal(kvh * cap * D, SEED, 51, 0.0, 1.0)
+    v = orc.fill_normal(kvh * cap * D, SEED, 52, 0.0, 1.0)
+    dq, dk, dv = offset_upload(ow, q), offset_upload(ow, k), offset_upload(ow, v)
+    out = offset_upload(ow, np.full(qh * D, np.nan, np.float32))
+    print(f"[decode contract] qh={qh} kv_rep={kv_rep} D={D} len={length}", flush=True)
+    ow.ops.attention_decode(dq, dk, dv, out, qh, kv_rep, D, length, cap)
+    got = out.to_host().reshape(qh, D)
+    ref = orc.attention_decode(q, k, v, qh, kv_rep, D, length, cap)
+    want, bound = decode_f64(q, k, v, qh, kv_rep, D, length, cap)
+    check(got, ref, bound)
+    check(got, want, bound)
+
+
+def test_decode_reference_contract_full_length(ow, orc):
+    """The 8192-key limit at config 4's head shape, with unaligned buffers."""
+    qh, kv_rep, D, length = 32, 4, 64, 8192
+    kvh = qh // kv_rep
+    q = orc.fill_normal(qh * D, SEED, 53, 0.0, 1.0)
+    k = orc.fill_normal(kvh * length * D, SEED, 54, 0.0, 1.0)
+    v = orc.fill_normal(kvh * length * D, SEED, 55, 0.0, 1.0)
+    dq, dk, dv = offset_upload(ow, q), offset_upload(ow, k), offset_upload(ow, v)
+    out = ow.DeviceBuffer.empty(qh * D)
+    ow.ops.attention_decode(dq, dk, dv, out, qh, kv_rep, D, length, length)
+    want, bound = decode_f64(q, k, v, qh, kv_rep, D, length, length)
+    check(out.to_host().reshape(qh, D), want, bound)
+
+
+def test_decode_reference_contract_rejects(ow):
+    """The reference's rejections and nothing more: head_dim 65, len past max_seq or past 8192, zero heads."""
+    buf = ow.DeviceBuffer.empty(64 * 64)
+    for args in [(4, 4, 65, 1, 8), (4, 4, 64, 9, 8), (4, 4, 1, 8193, 9000), (0, 4, 64, 1, 8), (4, 0, 64, 1, 8),
+                 (4, 4, 0, 1, 8), (4, 4, 64, 0, 8)]:
+        qh, kv_rep, D, length, cap = args
+        with pytest.raises(ow.OpworksError):
+            ow.ops.attention_decode(buf, buf, buf, buf, qh, kv_rep, D, length, cap)
+
+
+def test_decode_reference_contract_in_graph(ow, orc):
+    """ops::attention_decode captured into a HIP graph in global mode (so an allocation or synchronization
+    inside the op would fail the capture), then replayed three times, each after new q, K and V contents were
+    uploaded into the captured buffers, with an eager call on the same buffers between replays: every replay
+    against the oracle and bit-identical to the eager call."""
+    qh, kv_rep, D, length, cap = 32, 4, 64, 1000, 1024
+    kvh = qh // kv_rep
+    dq = ow.DeviceBuffer.empty(qh * D)
+    dk = ow.DeviceBuffer.empty(kvh * cap * D)
+    dv = ow.DeviceBuffer.empty(kvh * cap * D)
+    out = ow.DeviceBuffer.empty(qh * D)
+    eager = ow.DeviceBuffer.empty(qh * D)
+    stream = ow.Stream()
+    graph = ow.Graph.capture(stream, lambda: ow.ops.attention_decode(dq, dk, dv, out, qh, kv_rep, D, length, cap,
+                                                                     stream=stream))
+    for r in range(3):
+        q = orc.fill_normal(qh * D, SEED, 60 + 3 * r, 0.0, 1.0)
+        k = orc.fill_normal(kvh * cap * D, SEED, 61 + 3 * r, 0.0, 1.0)
+        v = orc.fill_normal(kvh * cap * D, SEED, 62 + 3 * r, 0.0, 1.0)
+        dq.copy_from_host(q)
+        dk.copy_from_host(k)
+        dv.copy_from_host(v)
+        graph.launch(stream)
+        stream.synchronize()
+        got = out.to_host().reshape(qh, D)
+        ow.ops.attention_decode(dq, dk, dv, eager, qh, kv_rep, D, length, cap)
+        assert np.array_equal(eager.to_host().view(np.uint32), out.to_host().view(np.uint32))
+        ref = orc.attention_decode(q, k, v, qh, kv_rep, D, length, cap)
+        _, bound = decode_f64(q, k, v, qh, kv_rep, D, length, cap)
+        check(got, ref, bound)
 
 
 # 1025 and 1600 keys: 17 and 25 chunks, past 16 records per head, so two chunks per workgroup with the

@@ -67,3 +67,33 @@ def test_noalloc_reduce_on_a_stream_and_limits(ow, orc):
     assert "536870912" in ow.lib().opw_last_error().decode()
     assert fn(d_in.ptr, out.ptr, 10, 7, None) == -1
     assert fn(d_in.ptr, out.ptr, -1, 0, None) == -1
+
+
+@pytest.mark.parametrize("op", [0, 1])
+def test_noalloc_reduce_in_a_captured_graph(ow, orc, op):
+    """Captured into a HIP graph (global mode: an allocation inside the call would fail the capture) after a
+    first call outside capture has looked up the device's scratch address, then replayed three times, each
+    after new input contents were uploaded into the captured buffer, with eager workspace-form calls between
+    the replays: every replay bit-identical to opw_reduce_f32 with a caller workspace."""
+    fn = noalloc(ow.lib())
+    n = (1 << 20) + 333
+    d_in = ow.DeviceBuffer.from_host(orc.fill_normal(n, SEED, 70, 0.0, 1.0))
+    out = ow.DeviceBuffer.empty(1)
+    assert fn(d_in.ptr, out.ptr, n, op, None) == 0, ow.lib().opw_last_error()
+    stream = ow.Stream()
+    stream.synchronize()
+
+    def body():
+        assert fn(d_in.ptr, out.ptr, n, op, stream.handle) == 0, ow.lib().opw_last_error()
+
+    graph = ow.Graph.capture(stream, body)
+    for r in range(3):
+        host = orc.fill_normal(n, SEED, 71 + r, 0.0, 1.0)
+        d_in.copy_from_host(host)
+        graph.launch(stream)
+        stream.synchronize()
+        got = np.float32(out.to_host()[0])
+        want = np.float32(with_workspace(ow, d_in, n, op))
+        assert got.view(np.uint32) == want.view(np.uint32), (op, r, got, want)
+        if op == 1:
+            assert got == np.max(host)
