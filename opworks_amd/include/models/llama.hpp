@@ -273,8 +273,16 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         OPWORKS_HIP_CHECK(hipMemcpyAsync(s.h_state, s.state(), sizeof(llama::StepState), hipMemcpyDeviceToHost,
                                          s.stream));
         synchronize(s.stream);
-        s.cache.length += n;
         s.last_prefill_rows = 0;
+        if (s.h_state->chain == 0) {
+            // a step produced no valid token and stopped the chain: the steps up to and including it
+            // appended their tokens (the later queued steps recomputed it in place)
+            const int failed = s.h_state->pos - pos0;
+            s.cache.length = s.h_state->pos + 1;
+            throw std::runtime_error("decode_greedy: step " + std::to_string(failed) + " produced no token id (argmax " +
+                                     std::to_string(s.h_state->next) + ": no finite winner among the logits)");
+        }
+        s.cache.length += n;
     }
 
     // One decode step launched eagerly with an event before every kernel and
@@ -550,7 +558,7 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         launch_async(s.stream, llama::lm_head_kernel<kV, WT>, records, llama::kBlock, la);
         launch_async(s.stream, llama::argmax_records_kernel, llama::kArgmaxGroups, 256, s.workspace.lm_best_val.data(),
                      s.workspace.lm_best_idx.data(), records, s.workspace.lm_part_val.data(), s.workspace.lm_part_idx.data(),
-                     s.workspace.lm_counter.data(), s.state(), s.workspace.gen.data());
+                     s.workspace.lm_counter.data(), s.state(), s.workspace.gen.data(), cfg_.vocab_size);
     }
 
     // Calls f(IntTag<H / 256>, IntTag<I / 1024>); bf16 rows need whole 8-weight

@@ -477,11 +477,16 @@ __global__ __launch_bounds__(kBlock) void lm_head_kernel(LmHeadArgs<WT> a) {
 // The merge is order-independent (largest value, then lowest index), so the
 // result does not depend on which workgroup arrives last. (One 1024-lane
 // workgroup over the 32064 records of the fp32 LM head took 8.1 us.)
+// A chained step whose logits hold no winner (every logit NaN: index 0x7fffffff) or any index
+// outside [0, vocab) records it in gen[pos] and stops the chain instead of advancing: the token
+// and position stay those of the step just run, so the steps still queued behind it recompute
+// that step in place (same inputs, same cache row) and no kernel reads an embedding row past
+// the table. The host sees chain == 0 with that index in `next`.
 constexpr int kArgmaxGroups = 64;
 __global__ __launch_bounds__(256) static void argmax_records_kernel(const float *__restrict__ best_val,
                                                                     const int *__restrict__ best_idx, int count,
                                                                     float *part_val, int *part_idx, int *counter,
-                                                                    StepState *state, int *gen) {
+                                                                    StepState *state, int *gen, int vocab) {
     __shared__ float sv[256 / kWaveSize];
     __shared__ int si[256 / kWaveSize];
     __shared__ int last;
@@ -533,8 +538,12 @@ __global__ __launch_bounds__(256) static void argmax_records_kernel(const float 
         state->next = ix;
         if (state->chain) { // greedy chaining: the next launch decodes this token at pos + 1
             gen[state->pos] = ix;
-            state->token = ix;
-            state->pos += 1;
+            if (ix >= 0 && ix < vocab) {
+                state->token = ix;
+                state->pos += 1;
+            } else {
+                state->chain = 0;
+            }
         }
     }
 }

@@ -630,6 +630,45 @@ static void lin_range(void *p, int64_t lo, int64_t hi) {
     free(buf);
 }
 
+/* The bf16 tensor-core projection (ops::linear_mma_bf16, include/ops/linear_mma.cuh:19-115) on
+ * inputs already rounded to bf16: every product of two bf16 values is exact in fp32, and the
+ * WMMA fragments accumulate them inside the tensor core in an order the code does not fix. This
+ * restatement sums the exact products in double (its error far below an fp32 ulp) and rounds once
+ * to fp32: the correctly rounded dot product but for rare near-halfway cases, the value any
+ * accumulation order approximates. A k-ascending fp32 chain would add its own ~sqrt(K)-ulp
+ * rounding walk to the difference from the GPU. */
+static void lin_exact_range(void *p, int64_t lo, int64_t hi) {
+    struct lin_ctx *c = (struct lin_ctx *)p;
+    double *buf = (double *)malloc(sizeof(double) * (size_t)c->in * LIN_BLOCK);
+    double acc[LIN_BLOCK];
+    for (int64_t blk = lo; blk < hi; ++blk) {
+        const int o0 = (int)blk * LIN_BLOCK;
+        const int nb = c->out - o0 < LIN_BLOCK ? c->out - o0 : LIN_BLOCK;
+        for (int j = 0; j < LIN_BLOCK; ++j)
+            for (int n = 0; n < c->in; ++n)
+                buf[(int64_t)n * LIN_BLOCK + j] = j < nb ? (double)c->W[(int64_t)(o0 + j) * c->in + n] : 0.0;
+        for (int r = 0; r < c->rows; ++r) {
+            const float *x = c->X + (int64_t)r * c->in;
+            for (int j = 0; j < LIN_BLOCK; ++j)
+                acc[j] = 0.0;
+            for (int n = 0; n < c->in; ++n) {
+                const double a = x[n];
+                const double *b = buf + (int64_t)n * LIN_BLOCK;
+                for (int j = 0; j < LIN_BLOCK; ++j)
+                    acc[j] += a * b[j];
+            }
+            for (int j = 0; j < nb; ++j)
+                c->Y[(int64_t)r * c->out + o0 + j] = (float)acc[j];
+        }
+    }
+    free(buf);
+}
+
+void orc_linear_exact(const float *X, const float *W, float *Y, int rows, int in, int out) {
+    struct lin_ctx c = {X, W, Y, rows, in, out};
+    parallel_for((out + LIN_BLOCK - 1) / LIN_BLOCK, lin_exact_range, &c);
+}
+
 /* ops::linear (include/ops/linear.cuh:130-153): the GEMV order for one row,
  * the tiled order otherwise. */
 void orc_linear(const float *X, const float *W, float *Y, int rows, int in, int out) {
@@ -825,7 +864,7 @@ static void llama_project(const orc_llama *m, const float *X, const float *W, fl
     if (m->bf16 && rows >= 16) {
         float *xr = alloc_f((int64_t)rows * in);
         orc_round_bf16(X, xr, NULL, (int64_t)rows * in);
-        orc_linear(xr, W, Y, rows, in, out);
+        orc_linear_exact(xr, W, Y, rows, in, out);
         free(xr);
     } else {
         orc_linear(X, W, Y, rows, in, out);

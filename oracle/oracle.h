@@ -31,6 +31,9 @@
  *  orc_attention_decode  equals the explicit path's last row (same maths,
  *                        other order) and the float64 reference
  *  orc_linear            agrees with orc_mat_mul_rows (same chain) / orc_gemv
+ *  orc_linear_exact      within 1 ulp of the exact sum (math.fsum of the float64
+ *                        products, rounded once) on bf16-valued inputs, and
+ *                        bit-equal to it for all but a rare near-halfway few
  *  orc_rope_inv_freq     closed form without scaling; llama3 bands by hand;
  *                        the reference's own model_config.cuh via oracle/_ref
  *  orc_rope              position 0 is the identity; pair norms preserved
@@ -51,7 +54,7 @@
  *  orc_gather/scatter    numpy fancy indexing; scatter of a permutation is its
  *                        inverse gather; out-of-range indices by hand
  *  orc_llama_set_bf16    weights equal their bf16 rounding (bit patterns);
- *                        the >= 16-row projection equals the fp32 one on
+ *                        the >= 16-row projection equals orc_linear_exact on
  *                        bf16-rounded inputs; float64 forward of a tiny model
  */
 #ifndef OPWORKS_ORACLE_H
@@ -109,6 +112,8 @@ void orc_attention_decode(const float *q, const float *k, const float *v, float 
 
 /* Llama forward (include/models/llama.cuh:216-285) on seeded random weights */
 void orc_linear(const float *X, const float *W, float *Y, int rows, int in, int out);
+/* the bf16 tensor-core projection: products summed in double, rounded once to fp32 */
+void orc_linear_exact(const float *X, const float *W, float *Y, int rows, int in, int out);
 void orc_rope_inv_freq(int head_dim, float theta, int llama3, float factor, float low, float high, int orig,
                        float *out);
 void orc_rope(float *x, const float *inv_freq, int rows, int heads, int head_dim, int pos_start);

@@ -42,6 +42,7 @@ _SIGS = {
                                       POINTER(c_int), c_int]),
     "orc_attention_decode": (None, [_F, _F, _F, _F, c_int, c_int, c_int, c_int, c_int]),
     "orc_linear": (None, [_F, _F, _F, c_int, c_int, c_int]),
+    "orc_linear_exact": (None, [_F, _F, _F, c_int, c_int, c_int]),
     "orc_rope_inv_freq": (None, [c_int, c_float, c_int, c_float, c_float, c_float, c_int, _F]),
     "orc_rope": (None, [_F, _F, c_int, c_int, c_int, c_int]),
     "orc_argmax": (c_int, [_F, c_int]),
@@ -223,6 +224,13 @@ def linear(X, W, rows, in_f, out_f):
     X, W = f32(X), f32(W)
     Y = np.empty(rows * out_f, np.float32)
     lib().orc_linear(fp(X), fp(W), fp(Y), rows, in_f, out_f)
+    return Y.reshape(rows, out_f)
+
+
+def linear_exact(X, W, rows, in_f, out_f):
+    X, W = f32(X), f32(W)
+    Y = np.empty(rows * out_f, np.float32)
+    lib().orc_linear_exact(fp(X), fp(W), fp(Y), rows, in_f, out_f)
     return Y.reshape(rows, out_f)
 
 

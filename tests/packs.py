@@ -33,10 +33,11 @@ def write_pack(path, tensors: dict, aliases: dict | None = None, extra: dict | N
             f.write(b)
 
 
-def pack_from_oracle(path, model, cfg: dict, dtype: str = "float32"):
+def pack_from_oracle(path, model, cfg: dict, dtype: str = "float32", overrides: dict | None = None):
     """Writes the oracle model's seeded weights as an HF-named pack (tied LM head alias);
     dtype "bfloat16" stores every tensor as bf16 bits (the oracle's weights must
-    already be bf16 values, e.g. a bf16 oracle model)."""
+    already be bf16 values, e.g. a bf16 oracle model). `overrides` replaces tensors
+    by HF name before they are written."""
     H, I, V = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"]
     qh, kvh = cfg["num_attention_heads"], cfg["num_key_value_heads"]
     D = cfg.get("head_dim", H // qh)
@@ -53,6 +54,9 @@ def pack_from_oracle(path, model, cfg: dict, dtype: str = "float32"):
         t[p + "mlp.down_proj.weight"] = model.weight(8, l, H * I).reshape(H, I)
         t[p + "input_layernorm.weight"] = model.weight(9, l, H)
         t[p + "post_attention_layernorm.weight"] = model.weight(10, l, H)
+    for k, v in (overrides or {}).items():
+        assert k in t and np.shape(v) == np.shape(t[k]), k
+        t[k] = v
     if dtype == "bfloat16":
         for k, v in t.items():
             bits = np.ascontiguousarray(v, np.float32).view(np.uint32)

@@ -19,6 +19,11 @@ MID_BF = dict(MID, torch_dtype="bfloat16")
 BAR = 1e-2
 
 
+def cosine(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(a @ b / np.sqrt((a @ a) * (b @ b)))
+
+
 @pytest.fixture(scope="module")
 def small_bf(ow):
     from opworks_amd.llama import LlamaModel
@@ -141,4 +146,60 @@ def test_config5_bf16_llama_3_2_1b(ow):
     cpu = orc.Llama(cfg, 1234, 0.02, "ones")
     worst, n_same = greedy_bf16(gpu, cpu, prompt(128, cfg["vocab_size"], 1234), 24, cap=256)
     print(f"config5 bf16: {n_same} identical tokens, worst logits nrmse {worst:.2e}")
+    assert worst <= BAR
+
+
+@pytest.mark.slow
+def test_config5_bf16_llama_3_2_1b_benched_configuration(ow):
+    """The bf16 path at the configuration bench.py measures and the reference publishes its bf16 figures
+    at (README.md:320-326): Llama-3.2-1B architecture, bf16 weights N(0, 0.02), gamma = 1, a 512-token
+    prompt (the prefill projections take the bf16 MFMA GEMM, gate/up its direct-load form) and 128
+    greedy tokens (decode steps to position 639), against the oracle's bf16 forward.
+
+    Decode steps: logits within NRMSE 1e-2 and cosine 0.999 (the reference's bf16 tolerances,
+    tests/model/model_test_body.cuh:205-206) at every step; ids identical except at near ties (top-1/top-2
+    margin < 1e-2, the reference's margin analysis, :238-256), after which both continue from the oracle's
+    token (teacher forcing, as that analysis replays the reference's prefix), so all 127 steps are checked.
+
+    Prefill logits: rounding a 512-row prompt's projection inputs to bf16 makes any two correct
+    evaluations drift apart by about 1e-2, because an fp32-level difference anywhere moves some values
+    across a bf16 rounding boundary (one bf16 ulp = 0.4%) and 16 layers carry those flips to the
+    logits. The test measures that floor on the same prompt as the distance between the oracle and a
+    float64 forward with the same rounding points, and requires the GPU to be within 1.25 times it of
+    the oracle (and cosine >= 0.999). Measured: oracle vs float64 1.06e-2, GPU vs oracle 1.18e-2;
+    decode steps 1.1e-3 to 1.3e-3."""
+    from opworks_amd.llama import LLAMA_3_2_1B, LlamaModel
+    from tests import oracle as orc
+    from tests.test_oracle_llama import _np_forward
+    orc.set_threads(16)
+    cfg = dict(LLAMA_3_2_1B, torch_dtype="bfloat16")
+    gpu = LlamaModel.load_random(cfg, 1234, 0.02, "ones")
+    cpu = orc.Llama(cfg, 1234, 0.02, "ones")
+    ids = prompt(512, cfg["vocab_size"], 1234)
+    s = gpu.session(1024)
+    cpu.reset(1024)
+    tok = s.prefill(ids)
+    ctok, clog = cpu.prefill(ids)
+    got = s.last_logits()
+    floor = nrmse(clog, _np_forward(cpu, cfg, ids, round_x=True))
+    pre = nrmse(got, clog)
+    print(f"config5 bf16 prompt 512: prefill nrmse {pre:.3e}, floor (oracle vs float64) {floor:.3e}, "
+          f"cosine {cosine(got, clog):.6f}", flush=True)
+    assert pre <= max(BAR, 1.25 * floor) and cosine(got, clog) >= 0.999
+    worst, n_same, ties = 0.0, 0, 0
+    for _ in range(128):
+        if tok == ctok:
+            n_same += 1
+        else:  # a near tie; both continue from the oracle's token (teacher forcing)
+            assert margin(clog) < BAR, f"divergence with margin {margin(clog)}"
+            ties += 1
+        if n_same + ties == 128:
+            break
+        tok = s.decode_step(ctok)
+        ctok, clog = cpu.decode(ctok)
+        got = s.last_logits()
+        worst = max(worst, nrmse(got, clog))
+        assert cosine(got, clog) >= 0.999
+    print(f"config5 bf16 prompt 512: {n_same} of 128 ids identical, {ties} near ties, worst decode-step logits "
+          f"nrmse {worst:.2e}", flush=True)
     assert worst <= BAR

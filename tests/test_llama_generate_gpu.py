@@ -101,3 +101,46 @@ def test_sampled_generation_is_seeded(small_pair):
     c = s.generate(ids, 16, temperature=0.8, top_p=0.9, seed=4)
     assert a == b and len(a) == 16
     assert a != c or len(set(a)) == 1
+
+
+def test_greedy_chain_stops_at_a_step_without_a_winner(ow, tmp_path):
+    """Regression: chained greedy generation must not feed an argmax without a winner back in as a token.
+    Token Z's embedding row is +inf in column 0 and zero elsewhere: its tied LM-head logit is +inf whenever
+    the normalised final hidden state is positive there, so Z wins a step; fed back in, Z's row normalises
+    to NaN, so the next step's logits are all NaN and its argmax is 0x7fffffff (the reference's all-NaN
+    result, include/ops/argmax.cuh:8-14). The host loop of decode_step calls returns that index as the
+    reference's decode_step does; a chained generation that reaches that step stops there and raises
+    instead of reading embedding row 0x7fffffff, and a generation that ends at Z matches the host loop."""
+    from opworks_amd.llama import LlamaModel
+    from tests import oracle as orc
+    from tests.packs import pack_from_oracle
+    cfg = TINY
+    V, H = cfg["vocab_size"], cfg["hidden_size"]
+    cpu = orc.Llama(cfg, SEED + 7, 0.02, "uniform")
+    Z = 300
+    embed = cpu.weight(0, 0, V * H).reshape(V, H)
+    embed[Z] = 0.0
+    embed[Z, 0] = np.inf
+    path = tmp_path / "inf_row.pack"
+    pack_from_oracle(str(path), cpu, cfg, overrides={"model.embed_tokens.weight": embed})
+    gpu = LlamaModel.load(str(path))
+    ids = prompt(12, V, 99)
+    s = gpu.session(128)
+    toks = [s.prefill(ids)]
+    while toks[-1] != Z and len(toks) < 40:
+        toks.append(s.decode_step(toks[-1]))
+    assert toks[-1] == Z, toks
+    k = len(toks) - 1  # index of Z among the generated tokens
+    assert s.decode_step(Z) == 0x7FFFFFFF
+    with pytest.raises(ow.OpworksError, match="outside the vocabulary"):
+        s.decode_step(0x7FFFFFFF)
+    print(f"[greedy guard] Z generated at step {k}", flush=True)
+    g = gpu.session(128)
+    got, _, _ = g.generate_greedy(ids, k + 1)
+    assert [int(t) for t in got] == toks
+    g2 = gpu.session(128)
+    with pytest.raises(ow.OpworksError, match="produced no token id"):
+        g2.generate_greedy(ids, k + 6)
+    g2.reset()
+    again, _, _ = g2.generate_greedy(ids, k + 1)
+    assert [int(t) for t in again] == toks

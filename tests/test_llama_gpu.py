@@ -276,11 +276,11 @@ def test_pack_load_matches_random_init(tiny, tmp_path, ow):
     assert a.prefill(ids) == b.prefill(ids)
     assert np.array_equal(a.last_logits(), b.last_logits())
     assert b.is_eos(7) and b.is_eos(9)
-    with pytest.raises(ow.OpworksError, match="bad magic"):
+    with pytest.raises(ow.OpworksError, match="not an OPWPACK1 file"):
         bad = tmp_path / "bad.pack"
         bad.write_bytes(b"NOTAPACK" + b"\0" * 64)
         LlamaModel.load(str(bad))
-    with pytest.raises(ow.OpworksError, match="cannot open"):
+    with pytest.raises(ow.OpworksError, match="cannot be opened"):
         LlamaModel.load(str(tmp_path / "missing.pack"))
 
 

@@ -229,3 +229,22 @@ def test_oracle_causal_scale_mask_shape(orc):
         assert np.all(out[r][~visible] == -np.inf)
     sq = orc.causal_scale(np.ones(16, np.float32), 4, 4, 1.0).reshape(4, 4)
     assert np.array_equal(np.isfinite(sq), np.tril(np.ones((4, 4), bool)))
+
+
+def test_oracle_linear_exact_is_the_rounded_exact_sum(orc):
+    """orc_linear_exact, the bf16 tensor-core projection's restatement (include/ops/linear_mma.cuh:19-115):
+    on bf16-valued inputs every product is exact, and each output must be their exact sum (math.fsum)
+    rounded once to fp32: never more than 1 ulp away and bit-equal for nearly all outputs. A dropped
+    term, a transposed weight or an fp32 accumulation chain (orc_linear) fails it."""
+    import math
+    rng = np.random.default_rng(11)
+    rows, K, N = 3, 2048, 70  # N past one 64-column block
+    X = _bf16_np(rng.normal(0, 1, (rows, K))).astype(np.float32)
+    W = _bf16_np(rng.normal(0, 0.02, (N, K))).astype(np.float32)
+    got = orc.linear_exact(X, W, rows, K, N)
+    exact = np.array([[math.fsum((X[r].astype(np.float64) * W[j].astype(np.float64)).tolist()) for j in range(N)]
+                      for r in range(rows)], np.float32)
+    ulps = np.abs(got.view(np.int32).astype(np.int64) - exact.view(np.int32).astype(np.int64))
+    assert ulps.max() <= 1 and (ulps == 0).mean() >= 0.99, (ulps.max(), (ulps == 0).mean())
+    chain = orc.linear(X, W, rows, K, N)
+    assert (chain != got).mean() > 0.2  # the fp32 chain is a different function
