@@ -380,7 +380,7 @@ def wl_llama(stream, steps, warmup, bf16=False, prompt_len=512, new_tokens=256, 
     cfg = dict(LLAMA_3_2_1B, torch_dtype="bfloat16") if bf16 else dict(LLAMA_3_2_1B)
     wb = 2 if bf16 else 4  # bytes per weight
     model = LlamaModel.load_random(cfg, SEED, 0.02, "ones")
-    sess = model.session(1024)
+    sess = model.session(max(1024, prompt_len + new_tokens))
     rng = np.random.default_rng(SEED)
     prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], prompt_len)]
     runs = []
@@ -443,6 +443,8 @@ def wl_llama(stream, steps, warmup, bf16=False, prompt_len=512, new_tokens=256, 
     if published:  # the reference's own figure for this exact configuration (other hardware)
         out["published"] = published
         out["vs_published"] = round(tok_s / published["decode_tok_s"], 2)
+        if "ttft_ms" in published:
+            out["ttft_vs_published"] = round(published["ttft_ms"] / pre, 2)
     return out
 
 
@@ -505,7 +507,20 @@ WORKLOADS = {"map": wl_map, "reduce": wl_reduce, "softmax": wl_softmax, "rmsnorm
              "llama_bf16": lambda st, k, w: wl_llama(
                  st, k, w, bf16=True, prompt_len=512, new_tokens=128,
                  published={"decode_tok_s": 215, "ttft_ms": 103.5, "hardware": "RTX 4080 SUPER",
-                            "source": "README.md:320-326"})}
+                            "source": "README.md:320-326"}),
+             # the reference's long-prompt rows of the same table (bf16, 128 new tokens)
+             "llama_bf16_p1024": lambda st, k, w: wl_llama(
+                 st, min(k, 10), min(w, 2), bf16=True, prompt_len=1024, new_tokens=128,
+                 published={"decode_tok_s": 198, "ttft_ms": 183.9, "hardware": "RTX 4080 SUPER",
+                            "source": "README.md:324"}),
+             "llama_bf16_p4096": lambda st, k, w: wl_llama(
+                 st, min(k, 6), min(w, 2), bf16=True, prompt_len=4096, new_tokens=128,
+                 published={"decode_tok_s": 134, "ttft_ms": 711.3, "hardware": "RTX 4080 SUPER",
+                            "source": "README.md:325"}),
+             "llama_bf16_p8000": lambda st, k, w: wl_llama(
+                 st, min(k, 4), min(w, 1), bf16=True, prompt_len=8000, new_tokens=128,
+                 published={"decode_tok_s": 95, "ttft_ms": 1874.3, "hardware": "RTX 4080 SUPER",
+                            "source": "README.md:326"})}
 HEADLINE = "llama"
 
 

@@ -696,17 +696,20 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
                 return;
             }
         }
-        if constexpr (kBf16 && kStore == detail::GemmStore::swiglu) {
-            // gate/up: A rounded to bf16 (nearest-even, as the GEMM's own staging rounds it) by a
-            // pass of its own, then the GEMM with both operands loaded straight into LDS: the same
-            // products and sums, at T = 512 77 -> 63.5 us per layer.
-            auto &xb = s.workspace.normed_bf16;
+        if constexpr (kBf16) {
+            // From 16 rows the input is rounded to bf16 (nearest-even, the rounding the reference's
+            // tensor-core GEMM applies as it stages X, include/ops/linear_mma.cuh:49) by a pass of its
+            // own, then the GEMM loads both operands straight into LDS: the same products and sums
+            // as rounding while staging (gate/up at T = 512: 77 -> 63.5 us per layer), on tiles
+            // sized to the row count (gemm_bf16_launch_direct).
+            auto &xb = s.workspace.x_bf16;
             if (int64_t(M) * K <= xb.size()) {
                 auto *bits = reinterpret_cast<uint16_t *>(xb.data());
                 launch_async(st, detail::convert_f32_bf16_kernel, detail::stream_grid(int64_t(M) * K), 256, A, bits,
                              int64_t(M) * K);
-                detail::gemm_bf16_launch<uint16_t, IdentityEpilogue, kStore>(bits, Wb, nullptr, C, M, N, K,
-                                                                             IdentityEpilogue{}, st);
+                detail::gemm_bf16_launch_direct<IdentityEpilogue, kStore>(bits, Wb, nullptr, C, M, N, K,
+                                                                         IdentityEpilogue{}, s.workspace.splitk.data(),
+                                                                         s.workspace.splitk.size(), st);
                 return;
             }
         }
@@ -732,22 +735,55 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
                      s.workspace.tokens.data(), s.workspace.hidden.data(), n, H);
         if (hook)
             hook(-1);
+        // bf16 weights from 16 rows: every projection input is written as bf16 bits by the kernel
+        // that produces it (RMSNorm, the head merge, the gate/up SwiGLU store), the rounding the
+        // reference's tensor-core GEMM applies to X as it loads it (include/ops/linear_mma.cuh:49),
+        // and the GEMMs load both operands straight into LDS. At T = 512 this removed 64 rounding
+        // passes (6 us each) and halved those inputs' bytes.
+        const bool xb = kBf16 && n >= 16 && s.workspace.x_bf16.size() >= int64_t(n) * std::max(H, qh * D);
+        auto *xbits = reinterpret_cast<uint16_t *>(s.workspace.x_bf16.data());
+        auto *act_bits = reinterpret_cast<uint16_t *>(s.workspace.act.data()); // [T][I] bf16 in the fp32 buffer
+        using detail::GemmStore;
+        using detail::IdentityEpilogue;
+        auto direct = [&](auto store_tag, const uint16_t *A, const WT *W, float *C, int N, int K) {
+            detail::gemm_bf16_launch_direct<IdentityEpilogue, decltype(store_tag)::value>(
+                A, reinterpret_cast<const uint16_t *>(W), nullptr, C, n, N, K, IdentityEpilogue{},
+                s.workspace.splitk.data(), s.workspace.splitk.size(), st);
+        };
+        using StoreTag = std::integral_constant<GemmStore, GemmStore::store>;
+        using ResidualTag = std::integral_constant<GemmStore, GemmStore::residual>;
+        using SwigluBf16Tag = std::integral_constant<GemmStore, GemmStore::swiglu_bf16>;
         for (int l = 0; l < cfg_.num_layers; ++l) {
             const LayerWeights<WT> &lw = w_.layers[static_cast<size_t>(l)];
-            ops::rms_norm(s.workspace.hidden.data(), lw.input_norm.data(), s.workspace.normed.data(), n, H, cfg_.rms_norm_eps, st);
-            project(s, s.workspace.normed.data(), lw.qkv_proj.data(), s.workspace.qkv.data(), n, qkvw, H, st);
+            if (xb) {
+                detail::rms_norm_to_bf16(s.workspace.hidden.data(), lw.input_norm.data(), xbits, n, H, cfg_.rms_norm_eps, st);
+                direct(StoreTag{}, xbits, lw.qkv_proj.data(), s.workspace.qkv.data(), qkvw, H);
+            } else {
+                ops::rms_norm(s.workspace.hidden.data(), lw.input_norm.data(), s.workspace.normed.data(), n, H, cfg_.rms_norm_eps, st);
+                project(s, s.workspace.normed.data(), lw.qkv_proj.data(), s.workspace.qkv.data(), n, qkvw, H, st);
+            }
             launch_async(st, llama::rope_split_kernel, detail::stream_grid(int64_t(n) * (qh + 2 * kvh) * (D / 2)),
                          256, s.workspace.qkv.data(), w_.rope_inv_freq.data(), s.workspace.q_heads.data(), layer_k(s, l), layer_v(s, l), n, qh,
                          kvh, D, s.cache.max_seq_len, 0);
             ops::attention_prefill(s.workspace.q_heads.data(), layer_k(s, l), layer_v(s, l), s.workspace.attn_heads.data(), n, n, 0, qh,
                                    cfg_.kv_rep(), D, s.cache.max_seq_len, st);
-            launch_async(st, llama::merge_heads_kernel, detail::stream_grid(int64_t(n) * qh * D), 256,
-                         s.workspace.attn_heads.data(), s.workspace.attn_out.data(), n, qh, D);
-            project<detail::GemmStore::residual>(s, s.workspace.attn_out.data(), lw.o_proj.data(), s.workspace.hidden.data(), n, H, qh * D,
-                                                 st);
-            ops::rms_norm(s.workspace.hidden.data(), lw.post_norm.data(), s.workspace.normed.data(), n, H, cfg_.rms_norm_eps, st);
-            project<detail::GemmStore::swiglu>(s, s.workspace.normed.data(), lw.gate_up_proj.data(), s.workspace.act.data(), n, 2 * I, H, st);
-            project<detail::GemmStore::residual>(s, s.workspace.act.data(), lw.down_proj.data(), s.workspace.hidden.data(), n, H, I, st);
+            if (xb) {
+                launch_async(st, llama::merge_heads_kernel<uint16_t>, detail::stream_grid(int64_t(n) * qh * D), 256,
+                             s.workspace.attn_heads.data(), xbits, n, qh, D);
+                direct(ResidualTag{}, xbits, lw.o_proj.data(), s.workspace.hidden.data(), H, qh * D);
+                detail::rms_norm_to_bf16(s.workspace.hidden.data(), lw.post_norm.data(), xbits, n, H, cfg_.rms_norm_eps, st);
+                direct(SwigluBf16Tag{}, xbits, lw.gate_up_proj.data(), reinterpret_cast<float *>(act_bits), 2 * I, H);
+                direct(ResidualTag{}, act_bits, lw.down_proj.data(), s.workspace.hidden.data(), H, I);
+            } else {
+                launch_async(st, llama::merge_heads_kernel<float>, detail::stream_grid(int64_t(n) * qh * D), 256,
+                             s.workspace.attn_heads.data(), s.workspace.attn_out.data(), n, qh, D);
+                project<GemmStore::residual>(s, s.workspace.attn_out.data(), lw.o_proj.data(), s.workspace.hidden.data(), n, H,
+                                             qh * D, st);
+                ops::rms_norm(s.workspace.hidden.data(), lw.post_norm.data(), s.workspace.normed.data(), n, H, cfg_.rms_norm_eps, st);
+                project<GemmStore::swiglu>(s, s.workspace.normed.data(), lw.gate_up_proj.data(), s.workspace.act.data(), n, 2 * I, H,
+                                           st);
+                project<GemmStore::residual>(s, s.workspace.act.data(), lw.down_proj.data(), s.workspace.hidden.data(), n, H, I, st);
+            }
             if (hook)
                 hook(l);
         }

@@ -617,14 +617,20 @@ __global__ __launch_bounds__(256) static void rope_split_kernel(const float *__r
     }
 }
 
-// attn_heads [qh][T][D] -> packed rows [T][qh * D]
-__global__ __launch_bounds__(256) static void merge_heads_kernel(const float *__restrict__ in, float *__restrict__ out,
-                                                                 int T, int qh, int D) {
+// attn_heads [qh][T][D] -> packed rows [T][qh * D]; OT = uint16_t rounds each value to bf16
+// (nearest-even) as it is stored, the input of a bf16 o_proj GEMM.
+template <typename OT = float>
+__global__ __launch_bounds__(256) void merge_heads_kernel(const float *__restrict__ in, OT *__restrict__ out, int T,
+                                                          int qh, int D) {
     OPWORKS_GRID_LOOP(i, int64_t(T) * qh * D) {
         const int d = static_cast<int>(i % D);
         const int h = static_cast<int>((i / D) % qh);
         const int t = static_cast<int>(i / (int64_t(D) * qh));
-        out[i] = in[(int64_t(h) * T + t) * D + d];
+        const float v = in[(int64_t(h) * T + t) * D + d];
+        if constexpr (std::is_same_v<OT, float>)
+            out[i] = v;
+        else
+            out[i] = float_to_bf16_rne(v);
     }
 }
 

@@ -52,12 +52,24 @@ constexpr int kBfBM = 256, kBfBN = 256;
 constexpr int kBfBK = 32; // K granularity of split-K planning (the smaller of the two K tiles)
 constexpr int kBfThreads = 512;
 
+// Workgroup tile shapes. Big: 256 x 256 outputs, 8 waves in 2 x 4 (128 x 64 each), one
+// workgroup per CU. Small: 128 x 128, 4 waves in 2 x 2 (64 x 64 each), 64 KB of LDS so two
+// workgroups share a CU; for short-M products (prefill projections at a few hundred rows), where
+// 256 x 256 tiles leave CUs idle or force deep split-K. The small shape exists on the direct
+// path only (bf16 A, 16-byte aligned operands).
+struct BfBig {
+    static constexpr int BM = 256, BN = 256, kThreads = 512, WM = 2, WN = 4;
+};
+struct BfSmall {
+    static constexpr int BM = 128, BN = 128, kThreads = 256, WM = 2, WN = 2;
+};
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return static_cast<uint32_t>(float_to_bf16_rne(lo)) | (static_cast<uint32_t>(float_to_bf16_rne(hi)) << 16);
 }
 
-template <typename TA, bool kVec, typename Epi, GemmStore kStore = GemmStore::store>
-__global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__restrict__ A,
+template <typename TA, bool kVec, typename Epi, GemmStore kStore = GemmStore::store, typename Shape = BfBig>
+__global__ __launch_bounds__(Shape::kThreads) void gemm_bf16_mfma_kernel(const TA *__restrict__ A,
                                                                     const uint16_t *__restrict__ W,
                                                                     const float *__restrict__ bias,
                                                                     float *__restrict__ C, int M, int N, int K,
@@ -69,6 +81,10 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     // on the vector path with bf16 A. With fp32 A, which is rounded on the way in registers,
     // and on the scalar path both are staged through registers.
     constexpr bool kDirect = kVec && !kF32A;
+    constexpr int kBM = Shape::BM, kBN = Shape::BN, kT = Shape::kThreads;
+    constexpr int kWTM = kBM / Shape::WM, kWTN = kBN / Shape::WN; // outputs per wave
+    static_assert(std::is_same_v<Shape, BfBig> || kDirect, "the small tile runs on the direct path only");
+    static_assert(kBM == kBN, "square workgroup tiles: both operands stage the same rows per thread");
     // LDS rows: a direct load writes 1 KB of consecutive bytes, so its rows are unpadded, with
     // chunk c of row r in slot c ^ ((r >> 1) & 7). The LDS serves 256 bytes a cycle, 16 lanes of
     // a 16-byte read, and the reads of 16 consecutive rows at one k then fall on 16 different
@@ -77,17 +93,17 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     // read offset a compile-time constant (the swizzle took the fp32-A kernel past 256 registers).
     constexpr int kRowE = kDirect ? BK : BK + 8;       // bf16 elements per LDS row
     constexpr int kCPR = BK / 8;                       // 16-byte chunks (8 k) per tile row
-    constexpr int kPer = kBfBM * kCPR / kBfThreads;    // chunks per thread per operand
-    constexpr int kStage = (kBfBM + kBfBN) * kRowE;    // uint16 elements per stage
+    constexpr int kPer = kBM * kCPR / kT;              // chunks per thread per operand
+    constexpr int kStage = (kBM + kBN) * kRowE;        // uint16 elements per stage
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kStage];
 
-    const int tiles_m = (M + kBfBM - 1) / kBfBM, tiles_n = (N + kBfBN - 1) / kBfBN;
+    const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
     int tm, tn;
     gemm_tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * kBfBM, n0 = tn * kBfBN;
+    const int m0 = tm * kBM, n0 = tn * kBN;
     const int tid = threadIdx.x, lane = tid % kWaveSize;
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWaveSize); // uniform: LDS targets in scalar registers
-    const int wm = wave / 4, wn = wave % 4; // 2 x 4 waves
+    const int wm = wave / Shape::WN, wn = wave % Shape::WN;
     const int l32 = lane % 32, half = lane / 32;
     const int l16 = lane % 16, quad = lane / 16;
     // The compiler does not count direct loads as writes to the array: without a store it may
@@ -99,8 +115,8 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
         return row * kRowE + ((kDirect ? chunk ^ ((row >> 1) & 7) : chunk) << 3);
     };
 
-    // Register staging: chunk tid + kBfThreads * i of each operand tile (256 rows x BK k),
-    // row (tid + kBfThreads * i) / kCPR. The vector path loads unconditionally from clamped
+    // Register staging: chunk tid + kT * i of each operand tile (kBM rows x BK k),
+    // row (tid + kT * i) / kCPR. The vector path loads unconditionally from clamped
     // addresses into raw registers (fp32 A is rounded to bf16 only when staged): a load under
     // a branch makes the compiler wait for every load in flight before the next one. Rows past
     // M or N then hold copies of the last row, which only feed outputs that are not stored; the
@@ -109,8 +125,8 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     constexpr int kAParts = kF32A ? 2 : 1;
     AStage ra[kPer][kAParts];
     u32x4 rb[kPer];
-    auto chunk_row = [&](int i) { return (tid + kBfThreads * i) / kCPR; };
-    auto chunk_k = [&](int i) { return ((tid + kBfThreads * i) % kCPR) * 8; };
+    auto chunk_row = [&](int i) { return (tid + kT * i) / kCPR; };
+    auto chunk_k = [&](int i) { return ((tid + kT * i) % kCPR) * 8; };
     auto load_chunk_bf16 = [&](const uint16_t *src, int row, int rows_total, int k) -> u32x4 {
         uint16_t e[8];
 #pragma unroll
@@ -156,7 +172,7 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     };
     auto lds_store = [&](int buf, int kt, bool zero_tail, bool with_a, bool with_b) {
         uint16_t *As = lds + buf * kStage;
-        uint16_t *Bs = As + kBfBM * kRowE;
+        uint16_t *Bs = As + kBM * kRowE;
         const int k0 = kt * BK;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
@@ -182,17 +198,17 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
         }
     };
     // Direct loads of tile kt (full K tiles of the vector path): the wave's instruction i
-    // writes the 1 KB block of rows 8 * wave + 64 * i .. + 7, lane l at byte 16 l, i.e. row
-    // r = block + l / 8, slot l % 8, which holds chunk (l % 8) ^ ((r >> 1) & 7) of that row;
-    // (r >> 1) & 7 = (4 (wave & 1) + l / 16) & 7 for every i.
+    // writes the 1 KB block of rows 8 * wave + 8 * waves * i .. + 7, lane l at byte 16 l, i.e.
+    // row r = block + l / 8, slot l % 8, which holds chunk (l % 8) ^ ((r >> 1) & 7) of that row;
+    // (r >> 1) & 7 = (4 (wave & 1) + l / 16) & 7 for every i (8 * waves is a multiple of 16).
     const int d_row = lane >> 3, d_chunk = (lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7);
     auto direct_load = [&](int buf, int kt) {
         const int k0 = kt * BK + 8 * d_chunk;
         uint16_t *As = lds + buf * kStage;
-        uint16_t *Bs = As + kBfBM * kRowE;
+        uint16_t *Bs = As + kBM * kRowE;
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const int block = 8 * wave + 64 * i, r = block + d_row;
+            const int block = 8 * wave + (kT / 8) * i, r = block + d_row;
             const int ar = m0 + r < M ? m0 + r : M - 1, br = n0 + r < N ? n0 + r : N - 1;
             load_lds16(A + int64_t(ar) * K + k0, As + block * kRowE);
             load_lds16(W + int64_t(br) * K + k0, Bs + block * kRowE);
@@ -201,7 +217,7 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
 
     // Accumulators: 16x16 tiles (4 registers each) on the direct path, 32x32 tiles (16) otherwise.
     constexpr int kTile = kDirect ? 16 : 32;
-    constexpr int FM = 128 / kTile, FN = 64 / kTile;
+    constexpr int FM = kWTM / kTile, FN = kWTN / kTile;
     using Acc = std::conditional_t<kDirect, f32x4, f32x16>;
     Acc acc[FM][FN];
 #pragma unroll
@@ -215,16 +231,16 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     bf16x8 fa[2][FM], fb[2][FN];
     auto read16 = [&](int buf, int s, int p) {
         const uint16_t *As = lds + buf * kStage;
-        const uint16_t *Bs = As + kBfBM * kRowE;
+        const uint16_t *Bs = As + kBM * kRowE;
         const int ch = 4 * s + quad;
 #pragma unroll
         for (int bm = 0; bm < FM; ++bm)
             fa[p][bm] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                                       As + swz(wm * 128 + bm * 16 + l16, ch)));
+                                                       As + swz(wm * kWTM + bm * 16 + l16, ch)));
 #pragma unroll
         for (int bn = 0; bn < FN; ++bn)
             fb[p][bn] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                                       Bs + swz(wn * 64 + bn * 16 + l16, ch)));
+                                                       Bs + swz(wn * kWTN + bn * 16 + l16, ch)));
     };
     auto mfma16 = [&](int p) {
         if constexpr (kDirect) {
@@ -253,7 +269,7 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     // (against staging after the last step: 990-999 -> 1019-1025 TFLOP/s).
     auto compute = [&](int buf, auto &&stage_next) {
         const uint16_t *As = lds + buf * kStage;
-        const uint16_t *Bs = As + kBfBM * kRowE;
+        const uint16_t *Bs = As + kBM * kRowE;
         constexpr int kSteps = BK / 16;
         bf16x8 a[2][4], b[2][2];
         auto read = [&](int s, bf16x8 (&fa)[4], bf16x8 (&fb)[2]) {
@@ -261,11 +277,11 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
 #pragma unroll
             for (int bm = 0; bm < 4; ++bm)
                 fa[bm] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                                        As + swz(wm * 128 + bm * 32 + l32, ch)));
+                                                        As + swz(wm * kWTM + bm * 32 + l32, ch)));
 #pragma unroll
             for (int bn = 0; bn < 2; ++bn)
                 fb[bn] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4 *>(
-                                                        Bs + swz(wn * 64 + bn * 32 + l32, ch)));
+                                                        Bs + swz(wn * kWTN + bn * 32 + l32, ch)));
         };
         read(0, a[0], b[0]);
 #pragma unroll
@@ -387,20 +403,20 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
         if (kStore != GemmStore::partial && bias != nullptr) { // one uniform test for every column
 #pragma unroll
             for (int bn = 0; bn < FN; ++bn) {
-                const int col = n0 + wn * 64 + bn * kTile + (kDirect ? l16 : l32);
+                const int col = n0 + wn * kWTN + bn * kTile + (kDirect ? l16 : l32);
                 bv[bn] = (!checked || col < N) ? bias[col] : 0.f;
             }
         }
         auto row_of = [&](int bm, int r) {
-            return kDirect ? m0 + wm * 128 + bm * 16 + 4 * quad + r
-                           : m0 + wm * 128 + bm * 32 + 8 * (r / 4) + 4 * half + (r % 4);
+            return kDirect ? m0 + wm * kWTM + bm * 16 + 4 * quad + r
+                           : m0 + wm * kWTM + bm * 32 + 8 * (r / 4) + 4 * half + (r % 4);
         };
         // residual loads per batch of 16 values: four 16x16 tiles or one 32x32 tile (larger batches
         // pushed both paths into spills)
         constexpr int kBatch = kDirect ? 4 : 1;
 #pragma unroll
         for (int bn = 0; bn < FN; ++bn) {
-            const int col = n0 + wn * 64 + bn * kTile + (kDirect ? l16 : l32);
+            const int col = n0 + wn * kWTN + bn * kTile + (kDirect ? l16 : l32);
             const bool col_ok = !checked || col < N;
 #pragma unroll
             for (int bm0 = 0; bm0 < FM; bm0 += kBatch) {
@@ -427,10 +443,16 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
                             continue;
                         }
                         const float v = epi(acc[bm][bn][r] + bv[bn]);
-                        if constexpr (kStore == GemmStore::swiglu) {
+                        if constexpr (kStore == GemmStore::swiglu || kStore == GemmStore::swiglu_bf16) {
                             const float partner = __shfl_xor(v, 1); // lane l ^ 1 holds column col ^ 1
-                            if ((col & 1) == 0 && (!checked || (row < M && col + 1 < N)))
-                                C[int64_t(row) * (N / 2) + col / 2] = v / (1.f + expf(-v)) * partner;
+                            if ((col & 1) == 0 && (!checked || (row < M && col + 1 < N))) {
+                                const float y = v / (1.f + expf(-v)) * partner;
+                                if constexpr (kStore == GemmStore::swiglu)
+                                    C[int64_t(row) * (N / 2) + col / 2] = y;
+                                else
+                                    reinterpret_cast<uint16_t *>(C)[int64_t(row) * (N / 2) + col / 2] =
+                                        float_to_bf16_rne(y);
+                            }
                         } else if constexpr (kStore == GemmStore::residual) {
                             if (ok)
                                 C[int64_t(row) * N + col] = prev[i][r] + v;
@@ -445,7 +467,7 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
     };
     // The register-staged paths keep the checked form only: a second copy pushed them into spills.
     if constexpr (kDirect) {
-        if (m0 + kBfBM <= M && n0 + kBfBN <= N)
+        if (m0 + kBM <= M && n0 + kBN <= N)
             store_tile(std::false_type{});
         else
             store_tile(std::true_type{});
@@ -459,7 +481,8 @@ __global__ __launch_bounds__(kBfThreads) void gemm_bf16_mfma_kernel(const TA *__
 template <typename TA, typename Epi, GemmStore kStore = GemmStore::store>
 void gemm_bf16_launch(const TA *A, const uint16_t *W, const float *bias, float *C, int M, int N, int K, Epi epi,
                       hipStream_t stream, int splits = 1) {
-    require(kStore != GemmStore::swiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
+    require((kStore != GemmStore::swiglu && kStore != GemmStore::swiglu_bf16) || N % 2 == 0,
+            "swiglu epilogue needs an even number of columns");
     const int tiles = static_cast<int>(blocks_for64(M, kBfBM) * blocks_for64(N, kBfBN));
     const dim3 grid(tiles, splits);
     const bool vec = aligned16(A) && aligned16(W) && K % 8 == 0;
@@ -471,7 +494,8 @@ void gemm_bf16_launch(const TA *A, const uint16_t *W, const float *bias, float *
                      epi);
 }
 
-// Floats of split-K workspace any launch planned by splitk_factor(tiles, ., 256) needs.
+// Floats of split-K workspace any launch planned by splitk_factor(tiles, ., 256) needs (the
+// small-tile plans below stay within it: splits x tiles <= 512 tiles of a quarter the size).
 constexpr int64_t kSplitKWorkspaceBf16 = int64_t(256) * kBfBM * kBfBN;
 
 // Split-K form of gemm_bf16_launch for store / residual outputs (see
@@ -490,6 +514,46 @@ void gemm_bf16_launch_splitk(const TA *A, const uint16_t *W, const float *bias, 
                                                                splits);
     launch_async(stream, splitk_reduce_kernel<Epi, kStore>, stream_grid(int64_t(M) * N / 4), 256, ws, splits, bias, C,
                  M, N, epi);
+}
+
+// bf16 A on the direct path (both operands straight into LDS), for any M: 256 x 256 tiles when
+// they fill the GPU's 256 CUs, else 128 x 128 tiles, and for store / residual outputs K split
+// across workgroups toward two per CU, at least 8 K tiles of 64 per split, the partial tiles
+// summed in split order by splitk_reduce_kernel. At M = 512 (a 512-token prefill) the 256 x 256
+// tiles gave gate/up 128 workgroups and qkv, o_proj and down 8-way splits on 16-24 tiles.
+template <typename Epi, GemmStore kStore>
+void gemm_bf16_launch_direct(const uint16_t *A, const uint16_t *W, const float *bias, float *C, int M, int N, int K,
+                             Epi epi, float *ws, int64_t ws_floats, hipStream_t stream) {
+    const bool vec = aligned16(A) && aligned16(W) && K % 8 == 0;
+    const int big_tiles = static_cast<int>(blocks_for64(M, kBfBM) * blocks_for64(N, kBfBN));
+    constexpr bool kSwiglu = kStore == GemmStore::swiglu || kStore == GemmStore::swiglu_bf16;
+    require(!kSwiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
+    if (!vec || big_tiles >= 256) {
+        if constexpr (kSwiglu)
+            gemm_bf16_launch<uint16_t, Epi, kStore>(A, W, bias, C, M, N, K, epi, stream);
+        else
+            gemm_bf16_launch_splitk<uint16_t, Epi, kStore>(A, W, bias, C, M, N, K, epi, ws, ws_floats, stream);
+        return;
+    }
+    using S = BfSmall;
+    const int tiles = static_cast<int>(blocks_for64(M, S::BM) * blocks_for64(N, S::BN));
+    int splits = 1;
+    if constexpr (!kSwiglu) {
+        splits = splitk_factor(tiles, static_cast<int>(blocks_for64(K, 64)), 512);
+        if (N % 4 != 0 || !ws || int64_t(splits) * M * N > ws_floats || !aligned16(C) || (bias && !aligned16(bias)))
+            splits = 1;
+    }
+    if (splits == 1) {
+        launch_async(stream, gemm_bf16_mfma_kernel<uint16_t, true, Epi, kStore, S>, dim3(tiles, 1), S::kThreads, A, W,
+                     bias, C, M, N, K, epi);
+        return;
+    }
+    launch_async(stream, gemm_bf16_mfma_kernel<uint16_t, true, IdentityEpilogue, GemmStore::partial, S>,
+                 dim3(tiles, splits), S::kThreads, A, W, static_cast<const float *>(nullptr), ws, M, N, K,
+                 IdentityEpilogue{});
+    if constexpr (!kSwiglu)
+        launch_async(stream, splitk_reduce_kernel<Epi, kStore>, stream_grid(int64_t(M) * N / 4), 256, ws, splits, bias,
+                     C, M, N, epi);
 }
 
 } // namespace opworks::detail

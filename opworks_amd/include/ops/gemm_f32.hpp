@@ -83,7 +83,10 @@ struct IdentityEpilogue {
 //  partial  raw accumulators of K split gridDim.y into C[blockIdx.y][M][N]
 //           (split-K; splitk_reduce_kernel sums the splits in order and
 //           applies bias, epilogue and the final store)
-enum class GemmStore { store, residual, swiglu, partial };
+//  swiglu_bf16  (bf16 GEMM only) swiglu, each product rounded to bf16 bits
+//           (nearest-even) into C read as a uint16_t [M][N / 2] array: the
+//           input of the next bf16 GEMM, which would round it on load anyway
+enum class GemmStore { store, residual, swiglu, partial, swiglu_bf16 };
 
 // Maps the dispatch-order workgroup id to a (tile_m, tile_n) pair: a band of
 // consecutive tiles per XCD (dispatch is round-robin over XCDs), then

@@ -7,6 +7,8 @@
 //    with X given either as fp32 or as bf16;
 //  * ops::convert_f32_to_bf16: nearest-even rounding of an fp32 array.
 
+#include <type_traits>
+
 #include "../core/bf16.hpp"
 #include "../core/hip_utils.hpp"
 #include "gemm_bf16.hpp"
@@ -31,6 +33,18 @@ inline void linear_bf16_validate(const TA *X, const uint16_t *W, float *Y, int r
     require(in_features > 0, "linear_mma_bf16 requires a positive reduction dim");
 }
 
+// fp32 X: the register-staged GEMM (rounded as staged); bf16 X: the direct-load GEMM on tiles
+// sized to the row count (no workspace, so no split-K).
+template <typename TA, typename Epi>
+inline void linear_bf16_launch(const TA *X, const uint16_t *W, const float *bias, float *Y, int rows, int in_features,
+                               int out_features, Epi epi, hipStream_t stream) {
+    if constexpr (std::is_same_v<TA, uint16_t>)
+        gemm_bf16_launch_direct<Epi, GemmStore::store>(X, W, bias, Y, rows, out_features, in_features, epi, nullptr, 0,
+                                                       stream);
+    else
+        gemm_bf16_launch(X, W, bias, Y, rows, out_features, in_features, epi, stream);
+}
+
 template <typename TA>
 inline void linear_bf16_act(const TA *X, const uint16_t *W, const float *bias, float *Y, int rows, int in_features,
                             int out_features, ops::Activation act, hipStream_t stream) {
@@ -39,13 +53,13 @@ inline void linear_bf16_act(const TA *X, const uint16_t *W, const float *bias, f
         return;
     switch (act) {
     case ops::Activation::none:
-        gemm_bf16_launch(X, W, bias, Y, rows, out_features, in_features, ops::PassThrough{}, stream);
+        linear_bf16_launch(X, W, bias, Y, rows, in_features, out_features, ops::PassThrough{}, stream);
         break;
     case ops::Activation::relu:
-        gemm_bf16_launch(X, W, bias, Y, rows, out_features, in_features, ops::ReluEpilogue{}, stream);
+        linear_bf16_launch(X, W, bias, Y, rows, in_features, out_features, ops::ReluEpilogue{}, stream);
         break;
     case ops::Activation::gelu:
-        gemm_bf16_launch(X, W, bias, Y, rows, out_features, in_features, ops::GeluEpilogue{}, stream);
+        linear_bf16_launch(X, W, bias, Y, rows, in_features, out_features, ops::GeluEpilogue{}, stream);
         break;
     default: throw std::invalid_argument("unknown activation");
     }

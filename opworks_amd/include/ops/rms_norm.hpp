@@ -3,14 +3,17 @@
 // ops::rms_norm — row-wise RMSNorm (reference: include/ops/rms_norm.cuh:9-40).
 // Per row: ss = sum(x^2); inv = rsqrtf(ss/cols + eps); out = x * inv * weight.
 
+#include "../core/bf16.hpp"
 #include "rowwise_kernels.hpp"
 
 namespace opworks::detail {
 
-template <int kW, int kV, bool kExact>
+// OT = float, or uint16_t: the output rounded to bf16 (nearest-even) as it is stored, for a
+// bf16 GEMM that would round it on load anyway (the same bits, half the bytes, no extra pass).
+template <int kW, int kV, bool kExact, typename OT = float>
 __global__ __launch_bounds__(RowShape<kW>::kBlock) void rms_norm_reg_kernel(const float *__restrict__ x,
                                                                              const float *__restrict__ weight,
-                                                                             float *__restrict__ out, int rows,
+                                                                             OT *__restrict__ out, int rows,
                                                                              int cols, float eps) {
     const RowPos p = row_position<kW>(rows);
     const int n4 = cols / 4;
@@ -29,7 +32,6 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void rms_norm_reg_kernel(cons
     }
     const float inv = rsqrtf(row_combine<kW>(wave::sum(local), p, wave::Add{}) / cols + eps);
     const f32x4 *w4 = reinterpret_cast<const f32x4 *>(weight);
-    f32x4 *dst = reinterpret_cast<f32x4 *>(out + p.row * cols);
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
         const int q = pack_index<kW>(p, k);
@@ -39,7 +41,13 @@ __global__ __launch_bounds__(RowShape<kW>::kBlock) void rms_norm_reg_kernel(cons
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 r[j] = v[k][j] * inv * w[j];
-            __builtin_nontemporal_store(r, dst + q);
+            if constexpr (std::is_same_v<OT, float>) {
+                __builtin_nontemporal_store(r, reinterpret_cast<f32x4 *>(out + p.row * cols) + q);
+            } else {
+                const uint2 b = make_uint2(uint32_t(float_to_bf16_rne(r[0])) | (uint32_t(float_to_bf16_rne(r[1])) << 16),
+                                           uint32_t(float_to_bf16_rne(r[2])) | (uint32_t(float_to_bf16_rne(r[3])) << 16));
+                reinterpret_cast<uint2 *>(out + p.row * cols)[q] = b;
+            }
         }
     }
 }
@@ -87,3 +95,25 @@ inline void rms_norm(const float *x, const float *weight, float *out, int rows, 
 }
 
 } // namespace opworks::ops
+
+namespace opworks::detail {
+
+// RMSNorm whose output is rounded to bf16 bits as it is stored (the input of a bf16 GEMM).
+// Needs the register plan (16-byte aligned rows, cols a multiple of 4, at most 32768).
+inline void rms_norm_to_bf16(const float *x, const float *weight, uint16_t *out, int rows, int cols, float eps,
+                             hipStream_t stream) {
+    validate_matrix(rows, cols);
+    if (rows == 0)
+        return;
+    require(x && weight && out && eps > 0.f, "rms_norm_to_bf16: bad arguments");
+    const RowPlan plan = plan_row(cols, aligned16(x) && aligned16(weight) && aligned16(out));
+    require(plan.waves != 0, "rms_norm_to_bf16 needs aligned rows of a multiple of 4 columns");
+    dispatch_row_plan(plan, [&](auto w, auto v) {
+        constexpr int kW = decltype(w)::value, kV = decltype(v)::value;
+        auto *kernel = row_plan_exact<kW, kV>(cols) ? rms_norm_reg_kernel<kW, kV, true, uint16_t>
+                                                     : rms_norm_reg_kernel<kW, kV, false, uint16_t>;
+        launch_async(stream, kernel, row_grid<kW>(rows), RowShape<kW>::kBlock, x, weight, out, rows, cols, eps);
+    });
+}
+
+} // namespace opworks::detail

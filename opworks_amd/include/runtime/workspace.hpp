@@ -11,6 +11,7 @@
 // and arrival counters, the LM head's per-workgroup argmax records, the
 // device step state and the tokens a chained greedy decode produces.
 
+#include <algorithm>
 #include <cstdint>
 
 #include "../core/typed_device_buffer.hpp"
@@ -26,7 +27,7 @@ struct WorkspaceSizes {
     int state_ints = 0;        // device step state
     int argmax_groups = 0;     // workgroups of the records' reduction
     int attn_counter_ints = 0; // decode attention arrival counters (one cache line per kv head)
-    bool bf16_inputs = false;  // bf16-weight model: a bf16 copy of the gate/up GEMM input
+    bool bf16_inputs = false;  // bf16-weight model: a bf16 copy of each prefill projection's input
 };
 
 struct Workspace {
@@ -40,7 +41,7 @@ struct Workspace {
     TypedDeviceBuffer<float> attn_out;   // [T, qh D]
     TypedDeviceBuffer<float> act;        // [T, I] silu(gate) * up
     TypedDeviceBuffer<float> splitk;     // split-K partial tiles
-    TypedDeviceBuffer<bf16> normed_bf16; // [T, H] normed rounded to bf16 (bf16-weight models)
+    TypedDeviceBuffer<bf16> x_bf16;      // [T, max(H, I, qh D)] projection input rounded to bf16 (bf16-weight models)
     // decode step: one row
     TypedDeviceBuffer<float> step_hidden;   // [H] residual stream
     TypedDeviceBuffer<float> step_q;        // [qh D] post-RoPE query
@@ -73,7 +74,7 @@ struct Workspace {
         if (T >= 2) { // only a multi-row prefill runs the GEMMs
             splitk = TypedDeviceBuffer<float>(s.splitk_floats);
             if (s.bf16_inputs)
-                normed_bf16 = TypedDeviceBuffer<bf16>(T * H);
+                x_bf16 = TypedDeviceBuffer<bf16>(T * std::max(std::max(H, I), qw));
         }
         step_hidden = TypedDeviceBuffer<float>(H);
         step_q = TypedDeviceBuffer<float>(qw);
