@@ -678,8 +678,11 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
     // inputs against the widened bf16 weights, as the reference's linear_dispatch does.
     // Outputs with too few tiles to fill the GPU (o_proj, down, qkv at a few
     // hundred rows) split K across workgroups into the session's workspace.
-    template <detail::GemmStore kStore = detail::GemmStore::store>
-    void project(Session &s, const float *A, const WT *W, float *C, int M, int N, int K, hipStream_t st) const {
+    // `reduce` (optional, split-K outputs): run in place of the split-K reduction kernel, see
+    // gemm_f32_launch_splitk. Returns true when K was split (and `reduce`, if given, ran).
+    template <detail::GemmStore kStore = detail::GemmStore::store, typename Reduce = std::nullptr_t>
+    bool project(Session &s, const float *A, const WT *W, float *C, int M, int N, int K, hipStream_t st,
+                 Reduce reduce = nullptr) const {
         using detail::IdentityEpilogue;
         constexpr bool kSplittable = kStore != detail::GemmStore::swiglu;
         const auto *Wb = reinterpret_cast<const uint16_t *>(W);
@@ -688,12 +691,12 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
             // linear_dispatch does below 16 rows (include/models/llama.cuh:190-199)
             if (M < 16) {
                 if constexpr (kSplittable)
-                    detail::gemm_f32_launch_splitk<detail::BLayout::nk, IdentityEpilogue, kStore, uint16_t>(
-                        A, Wb, nullptr, C, M, N, K, IdentityEpilogue{}, s.workspace.splitk.data(), s.workspace.splitk.size(), st);
-                else
-                    detail::gemm_f32_launch<detail::BLayout::nk, IdentityEpilogue, kStore, uint16_t>(
-                        A, Wb, nullptr, C, M, N, K, IdentityEpilogue{}, st);
-                return;
+                    return detail::gemm_f32_launch_splitk<detail::BLayout::nk, IdentityEpilogue, kStore, uint16_t>(
+                        A, Wb, nullptr, C, M, N, K, IdentityEpilogue{}, s.workspace.splitk.data(), s.workspace.splitk.size(), st,
+                        reduce);
+                detail::gemm_f32_launch<detail::BLayout::nk, IdentityEpilogue, kStore, uint16_t>(
+                    A, Wb, nullptr, C, M, N, K, IdentityEpilogue{}, st);
+                return false;
             }
         }
         if constexpr (kBf16) {
@@ -707,24 +710,26 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
                 auto *bits = reinterpret_cast<uint16_t *>(xb.data());
                 launch_async(st, detail::convert_f32_bf16_kernel, detail::stream_grid(int64_t(M) * K), 256, A, bits,
                              int64_t(M) * K);
-                detail::gemm_bf16_launch_direct<IdentityEpilogue, kStore>(bits, Wb, nullptr, C, M, N, K,
-                                                                         IdentityEpilogue{}, s.workspace.splitk.data(),
-                                                                         s.workspace.splitk.size(), st);
-                return;
+                return detail::gemm_bf16_launch_direct<IdentityEpilogue, kStore>(
+                    bits, Wb, nullptr, C, M, N, K, IdentityEpilogue{}, s.workspace.splitk.data(), s.workspace.splitk.size(),
+                    st, reduce);
             }
         }
-        if constexpr (kBf16 && kSplittable)
+        if constexpr (kBf16 && kSplittable) { // (no hook: the reduction kernel stores, the caller norms)
             detail::gemm_bf16_launch_splitk<float, IdentityEpilogue, kStore>(
                 A, Wb, nullptr, C, M, N, K, IdentityEpilogue{}, s.workspace.splitk.data(), s.workspace.splitk.size(), st);
-        else if constexpr (kBf16)
+        } else if constexpr (kBf16) {
             detail::gemm_bf16_launch<float, IdentityEpilogue, kStore>(A, Wb, nullptr, C, M, N, K, IdentityEpilogue{},
                                                                       st);
-        else if constexpr (kSplittable)
-            detail::gemm_f32_launch_splitk<detail::BLayout::nk, IdentityEpilogue, kStore>(
-                A, W, nullptr, C, M, N, K, IdentityEpilogue{}, s.workspace.splitk.data(), s.workspace.splitk.size(), st);
-        else
+        } else if constexpr (kSplittable) {
+            return detail::gemm_f32_launch_splitk<detail::BLayout::nk, IdentityEpilogue, kStore>(
+                A, W, nullptr, C, M, N, K, IdentityEpilogue{}, s.workspace.splitk.data(), s.workspace.splitk.size(), st,
+                reduce);
+        } else {
             detail::gemm_f32_launch<detail::BLayout::nk, IdentityEpilogue, kStore>(A, W, nullptr, C, M, N, K,
                                                                                   IdentityEpilogue{}, st);
+        }
+        return false;
     }
 
     void enqueue_prefill(Session &s, int n, const std::function<void(int)> &hook) {
@@ -753,37 +758,69 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         using StoreTag = std::integral_constant<GemmStore, GemmStore::store>;
         using ResidualTag = std::integral_constant<GemmStore, GemmStore::residual>;
         using SwigluBf16Tag = std::integral_constant<GemmStore, GemmStore::swiglu_bf16>;
+        float *hidden = s.workspace.hidden.data(), *normed = s.workspace.normed.data();
+        const float eps = cfg_.rms_norm_eps;
+        auto norm = [&](const float *gamma) {
+            if (xb)
+                detail::rms_norm_to_bf16(hidden, gamma, xbits, n, H, eps, st);
+            else
+                ops::rms_norm(hidden, gamma, normed, n, H, eps, st);
+        };
+        // A residual projection (o_proj, down) whose output RMSNorm(hidden) * gamma feeds the next
+        // projection: when K is split, the norm runs inside the split-K reduction (one row pass and
+        // one launch fewer); returns whether it did. A_f32 / A_bits: the fp32 or bf16 input.
+        auto residual_then_norm = [&](const float *A_f32, const uint16_t *A_bits, const WT *W, int K,
+                                      const float *gamma) -> bool {
+            const bool fusable = gamma && detail::splitk_residual_rms_norm_ok(
+                                              n, H, hidden, gamma, xb ? static_cast<const void *>(xbits) : normed);
+            auto reduce = [&](float *ws, int splits) {
+                if (xb)
+                    detail::splitk_residual_rms_norm<uint16_t>(ws, splits, hidden, gamma, xbits, n, H, eps, st);
+                else
+                    detail::splitk_residual_rms_norm<float>(ws, splits, hidden, gamma, normed, n, H, eps, st);
+            };
+            if (!fusable) {
+                if (xb)
+                    direct(ResidualTag{}, A_bits, W, hidden, H, K);
+                else
+                    project<GemmStore::residual>(s, A_f32, W, hidden, n, H, K, st);
+                return false;
+            }
+            if (xb)
+                return detail::gemm_bf16_launch_direct<IdentityEpilogue, GemmStore::residual>(
+                    A_bits, reinterpret_cast<const uint16_t *>(W), nullptr, hidden, n, H, K, IdentityEpilogue{},
+                    s.workspace.splitk.data(), s.workspace.splitk.size(), st, reduce);
+            return project<GemmStore::residual>(s, A_f32, W, hidden, n, H, K, st, reduce);
+        };
+        bool input_normed = false; // layer l's input norm ran in layer l - 1's down reduction
         for (int l = 0; l < cfg_.num_layers; ++l) {
             const LayerWeights<WT> &lw = w_.layers[static_cast<size_t>(l)];
-            if (xb) {
-                detail::rms_norm_to_bf16(s.workspace.hidden.data(), lw.input_norm.data(), xbits, n, H, cfg_.rms_norm_eps, st);
+            if (!input_normed)
+                norm(lw.input_norm.data());
+            if (xb)
                 direct(StoreTag{}, xbits, lw.qkv_proj.data(), s.workspace.qkv.data(), qkvw, H);
-            } else {
-                ops::rms_norm(s.workspace.hidden.data(), lw.input_norm.data(), s.workspace.normed.data(), n, H, cfg_.rms_norm_eps, st);
-                project(s, s.workspace.normed.data(), lw.qkv_proj.data(), s.workspace.qkv.data(), n, qkvw, H, st);
-            }
+            else
+                project(s, normed, lw.qkv_proj.data(), s.workspace.qkv.data(), n, qkvw, H, st);
             launch_async(st, llama::rope_split_kernel, detail::stream_grid(int64_t(n) * (qh + 2 * kvh) * (D / 2)),
                          256, s.workspace.qkv.data(), w_.rope_inv_freq.data(), s.workspace.q_heads.data(), layer_k(s, l), layer_v(s, l), n, qh,
                          kvh, D, s.cache.max_seq_len, 0);
             ops::attention_prefill(s.workspace.q_heads.data(), layer_k(s, l), layer_v(s, l), s.workspace.attn_heads.data(), n, n, 0, qh,
                                    cfg_.kv_rep(), D, s.cache.max_seq_len, st);
-            if (xb) {
+            if (xb)
                 launch_async(st, llama::merge_heads_kernel<uint16_t>, detail::stream_grid(int64_t(n) * qh * D), 256,
                              s.workspace.attn_heads.data(), xbits, n, qh, D);
-                direct(ResidualTag{}, xbits, lw.o_proj.data(), s.workspace.hidden.data(), H, qh * D);
-                detail::rms_norm_to_bf16(s.workspace.hidden.data(), lw.post_norm.data(), xbits, n, H, cfg_.rms_norm_eps, st);
-                direct(SwigluBf16Tag{}, xbits, lw.gate_up_proj.data(), reinterpret_cast<float *>(act_bits), 2 * I, H);
-                direct(ResidualTag{}, act_bits, lw.down_proj.data(), s.workspace.hidden.data(), H, I);
-            } else {
+            else
                 launch_async(st, llama::merge_heads_kernel<float>, detail::stream_grid(int64_t(n) * qh * D), 256,
                              s.workspace.attn_heads.data(), s.workspace.attn_out.data(), n, qh, D);
-                project<GemmStore::residual>(s, s.workspace.attn_out.data(), lw.o_proj.data(), s.workspace.hidden.data(), n, H,
-                                             qh * D, st);
-                ops::rms_norm(s.workspace.hidden.data(), lw.post_norm.data(), s.workspace.normed.data(), n, H, cfg_.rms_norm_eps, st);
-                project<GemmStore::swiglu>(s, s.workspace.normed.data(), lw.gate_up_proj.data(), s.workspace.act.data(), n, 2 * I, H,
-                                           st);
-                project<GemmStore::residual>(s, s.workspace.act.data(), lw.down_proj.data(), s.workspace.hidden.data(), n, H, I, st);
-            }
+            if (!residual_then_norm(s.workspace.attn_out.data(), xbits, lw.o_proj.data(), qh * D, lw.post_norm.data()))
+                norm(lw.post_norm.data());
+            if (xb)
+                direct(SwigluBf16Tag{}, xbits, lw.gate_up_proj.data(), reinterpret_cast<float *>(act_bits), 2 * I, H);
+            else
+                project<GemmStore::swiglu>(s, normed, lw.gate_up_proj.data(), s.workspace.act.data(), n, 2 * I, H, st);
+            const float *next_gamma =
+                l + 1 < cfg_.num_layers ? w_.layers[static_cast<size_t>(l) + 1].input_norm.data() : nullptr;
+            input_normed = residual_then_norm(s.workspace.act.data(), act_bits, lw.down_proj.data(), I, next_gamma);
             if (hook)
                 hook(l);
         }

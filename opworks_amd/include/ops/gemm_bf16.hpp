@@ -34,6 +34,7 @@
 // On 4096^3 uniformly random bf16 operands the 16x16x32 and 32x32x16 forms gave
 // bit-identical outputs (measured on gfx950); the tests hold both to the oracle.
 
+#include <cstddef>
 #include <cstdint>
 #include <type_traits>
 
@@ -521,9 +522,11 @@ void gemm_bf16_launch_splitk(const TA *A, const uint16_t *W, const float *bias, 
 // across workgroups toward two per CU, at least 8 K tiles of 64 per split, the partial tiles
 // summed in split order by splitk_reduce_kernel. At M = 512 (a 512-token prefill) the 256 x 256
 // tiles gave gate/up 128 workgroups and qkv, o_proj and down 8-way splits on 16-24 tiles.
-template <typename Epi, GemmStore kStore>
-void gemm_bf16_launch_direct(const uint16_t *A, const uint16_t *W, const float *bias, float *C, int M, int N, int K,
-                             Epi epi, float *ws, int64_t ws_floats, hipStream_t stream) {
+// `reduce` as in gemm_f32_launch_splitk: called as reduce(ws, splits) in place of the reduction
+// kernel when K is split (small tiles only). Returns true when it was.
+template <typename Epi, GemmStore kStore, typename Reduce = std::nullptr_t>
+bool gemm_bf16_launch_direct(const uint16_t *A, const uint16_t *W, const float *bias, float *C, int M, int N, int K,
+                             Epi epi, float *ws, int64_t ws_floats, hipStream_t stream, Reduce reduce = nullptr) {
     const bool vec = aligned16(A) && aligned16(W) && K % 8 == 0;
     const int big_tiles = static_cast<int>(blocks_for64(M, kBfBM) * blocks_for64(N, kBfBN));
     constexpr bool kSwiglu = kStore == GemmStore::swiglu || kStore == GemmStore::swiglu_bf16;
@@ -533,7 +536,7 @@ void gemm_bf16_launch_direct(const uint16_t *A, const uint16_t *W, const float *
             gemm_bf16_launch<uint16_t, Epi, kStore>(A, W, bias, C, M, N, K, epi, stream);
         else
             gemm_bf16_launch_splitk<uint16_t, Epi, kStore>(A, W, bias, C, M, N, K, epi, ws, ws_floats, stream);
-        return;
+        return false;
     }
     using S = BfSmall;
     const int tiles = static_cast<int>(blocks_for64(M, S::BM) * blocks_for64(N, S::BN));
@@ -546,14 +549,19 @@ void gemm_bf16_launch_direct(const uint16_t *A, const uint16_t *W, const float *
     if (splits == 1) {
         launch_async(stream, gemm_bf16_mfma_kernel<uint16_t, true, Epi, kStore, S>, dim3(tiles, 1), S::kThreads, A, W,
                      bias, C, M, N, K, epi);
-        return;
+        return false;
     }
     launch_async(stream, gemm_bf16_mfma_kernel<uint16_t, true, IdentityEpilogue, GemmStore::partial, S>,
                  dim3(tiles, splits), S::kThreads, A, W, static_cast<const float *>(nullptr), ws, M, N, K,
                  IdentityEpilogue{});
-    if constexpr (!kSwiglu)
-        launch_async(stream, splitk_reduce_kernel<Epi, kStore>, stream_grid(int64_t(M) * N / 4), 256, ws, splits, bias,
-                     C, M, N, epi);
+    if constexpr (!kSwiglu) {
+        if constexpr (std::is_same_v<Reduce, std::nullptr_t>)
+            launch_async(stream, splitk_reduce_kernel<Epi, kStore>, stream_grid(int64_t(M) * N / 4), 256, ws, splits,
+                         bias, C, M, N, epi);
+        else
+            reduce(ws, splits);
+    }
+    return true;
 }
 
 } // namespace opworks::detail

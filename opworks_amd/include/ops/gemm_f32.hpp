@@ -39,6 +39,7 @@
 // Accumulation is fp32 on the matrix core; the result differs from a
 // k-ascending fmaf chain only by summation order.
 
+#include <cstddef>
 #include <cstdint>
 #include <type_traits>
 
@@ -508,9 +509,11 @@ constexpr int64_t kSplitKWorkspaceF32 = int64_t(512) * GemmSmall::BM * GemmSmall
 // C (store or residual) = epi(A B + bias) with K split across `splits`
 // workgroup rows when the output alone has too few tiles to fill the GPU;
 // the partial tiles go to `ws` (splits * M * N floats) and are summed in order.
-template <BLayout kB, typename Epi, GemmStore kStore, typename TB = float>
-void gemm_f32_launch_splitk(const float *A, const TB *B, const float *bias, float *C, int M, int N, int K, Epi epi,
-                            float *ws, int64_t ws_floats, hipStream_t stream) {
+// `reduce` (optional): when K is split, called as reduce(ws, splits) in place of the reduction
+// kernel, so a caller can fuse what follows the store into it. Returns true when K was split.
+template <BLayout kB, typename Epi, GemmStore kStore, typename TB = float, typename Reduce = std::nullptr_t>
+bool gemm_f32_launch_splitk(const float *A, const TB *B, const float *bias, float *C, int M, int N, int K, Epi epi,
+                            float *ws, int64_t ws_floats, hipStream_t stream, Reduce reduce = nullptr) {
     // Partials on GemmMid tiles up to 256 workgroups when M fills its 256-row tiles and that splits
     // K at all, else on GemmSmall tiles up to 512 (prefill at 512 rows: qkv 86.2 -> 81.8 us, down
     // 152.5 -> 148.4 us, o_proj unchanged). Either plan needs at most 256 * 256 * 128 =
@@ -527,7 +530,7 @@ void gemm_f32_launch_splitk(const float *A, const TB *B, const float *bias, floa
     if (splits == 1 || N % 4 != 0 || !ws || int64_t(splits) * M * N > ws_floats || !aligned16(C) ||
         (bias && !aligned16(bias))) {
         gemm_f32_launch<kB, Epi, kStore, TB>(A, B, bias, C, M, N, K, epi, stream);
-        return;
+        return false;
     }
     if (mid_splits > 1)
         gemm_f32_launch_shape<GemmMid, kB, IdentityEpilogue, GemmStore::partial, TB>(
@@ -535,8 +538,12 @@ void gemm_f32_launch_splitk(const float *A, const TB *B, const float *bias, floa
     else
         gemm_f32_launch_shape<GemmSmall, kB, IdentityEpilogue, GemmStore::partial, TB>(
             A, B, nullptr, ws, M, N, K, IdentityEpilogue{}, stream, splits);
-    launch_async(stream, splitk_reduce_kernel<Epi, kStore>, stream_grid(int64_t(M) * N / 4), 256, ws, splits, bias, C,
-                 M, N, epi);
+    if constexpr (std::is_same_v<Reduce, std::nullptr_t>)
+        launch_async(stream, splitk_reduce_kernel<Epi, kStore>, stream_grid(int64_t(M) * N / 4), 256, ws, splits, bias,
+                     C, M, N, epi);
+    else
+        reduce(ws, splits);
+    return true;
 }
 
 } // namespace opworks::detail

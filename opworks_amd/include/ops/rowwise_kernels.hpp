@@ -125,6 +125,19 @@ inline RowPlan plan_row(int cols, bool packed) {
     return {16, 8};
 }
 
+// The plan for `rows` rows: a short matrix (fewer than 2048 row waves, 8 per CU) spreads each
+// row over more waves with fewer packs each, down to 2 packs per lane, so the GPU has enough
+// waves in flight: 512 x 2048 (a 512-token prefill's RMSNorm) runs 4 waves of 2 packs per row
+// instead of 1 wave of 8. Only the row ops whose dispatch carries these shapes use it.
+inline RowPlan plan_row_for_rows(int rows, int cols, bool packed) {
+    RowPlan p = plan_row(cols, packed);
+    while (p.waves != 0 && p.packs >= 4 && p.waves <= 4 && int64_t(rows) * p.waves < 2048) {
+        p.waves *= 2;
+        p.packs /= 2;
+    }
+    return p;
+}
+
 // Calls fn(W{}, V{}) with std::integral_constant tags of the plan's
 // instantiation (C++17 generic lambdas read them back as constants).
 template <int N> using IntTag = std::integral_constant<int, N>;
@@ -140,6 +153,19 @@ template <typename Fn> inline void dispatch_row_plan(const RowPlan &plan, Fn &&f
     case 808: fn(IntTag<8>{}, IntTag<8>{}); break;
     case 1608: fn(IntTag<16>{}, IntTag<8>{}); break;
     default: throw std::invalid_argument("row plan has no kernel instantiation");
+    }
+}
+
+// dispatch_row_plan plus the shapes plan_row_for_rows can add.
+template <typename Fn> inline void dispatch_row_plan_for_rows(const RowPlan &plan, Fn &&fn) {
+    switch (plan.waves * 100 + plan.packs) {
+    case 202: fn(IntTag<2>{}, IntTag<2>{}); break;
+    case 204: fn(IntTag<2>{}, IntTag<4>{}); break;
+    case 402: fn(IntTag<4>{}, IntTag<2>{}); break;
+    case 404: fn(IntTag<4>{}, IntTag<4>{}); break;
+    case 802: fn(IntTag<8>{}, IntTag<2>{}); break;
+    case 804: fn(IntTag<8>{}, IntTag<4>{}); break;
+    default: dispatch_row_plan(plan, fn);
     }
 }
 

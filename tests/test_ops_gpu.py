@@ -172,7 +172,8 @@ def test_layer_norm_known_answer(ow):
     assert framework_close(out.to_host(), [(i % 5 - 2) * 2 / math.sqrt(2 + 1e-5) + 1 for i in range(10)])
 
 
-@pytest.mark.parametrize("rows,cols", ROW_SHAPES + [(8192, 2048)])
+# (512, 2048), (1500, 2048): prefill shapes whose rows are spread over 4 and 2 waves
+@pytest.mark.parametrize("rows,cols", ROW_SHAPES + [(8192, 2048), (512, 2048), (1500, 2048)])
 def test_rms_norm_matches_oracle(ow, orc, rows, cols):
     x = _rows_input(orc, rows, cols, 1.0, 44)
     w = orc.fill_uniform(cols, SEED, 45, 0.5, 1.5)
