@@ -124,7 +124,7 @@ def roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) 
 
 
 TRAFFIC_FILES = (ROOT / "profiles" / "llama_decode_traffic.md", ROOT / "profiles" / "stream_ops_traffic.md",
-                 ROOT / "profiles" / "scan_transpose_gather_traffic.md")
+                 ROOT / "profiles" / "scan_transpose_gather_traffic.md", ROOT / "profiles" / "gemm_attention_traffic.md")
 
 
 def profiled_traffic(stage: str):
@@ -285,7 +285,8 @@ def wl_gemm(stream, steps, warmup):
     flop = 2.0 * n ** 3
     tf = flop / ms / 1e9
     return {"workload": "gemm_f32_relu_bias_4096^3", "unit": "TFLOP/s", "value": tf, "ms": ms, "flop": flop,
-            "kernel": "gemm_f32_mfma_kernel<kn>", "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma")}
+            "kernel": "gemm_f32_mfma_kernel<kn>",
+            "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma", traffic=profiled_traffic("gemm"))}
 
 
 def wl_gemm_bf16(stream, steps, warmup):
@@ -304,7 +305,8 @@ def wl_gemm_bf16(stream, steps, warmup):
     flop = 2.0 * n ** 3
     tf = flop / ms / 1e9
     return {"workload": "gemm_bf16_relu_bias_4096^3", "unit": "TFLOP/s", "value": tf, "ms": ms, "flop": flop,
-            "kernel": "gemm_bf16_mfma_kernel<bf16>", "roofline": roofline(tf, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma")}
+            "kernel": "gemm_bf16_mfma_kernel<bf16>",
+            "roofline": roofline(tf, BF16_PEAK_TFLOPS, "TFLOP/s", "mfma", traffic=profiled_traffic("gemm_bf16"))}
 
 
 def wl_linear(stream, steps, warmup):
@@ -318,7 +320,8 @@ def wl_linear(stream, steps, warmup):
     flop = 2.0 * n ** 3
     tf = flop / ms / 1e9
     return {"workload": "linear_f32_4096^3_hf_weights", "unit": "TFLOP/s", "value": tf, "ms": ms, "flop": flop,
-            "kernel": "gemm_f32_mfma_kernel<nk>", "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma")}
+            "kernel": "gemm_f32_mfma_kernel<nk>",
+            "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma", traffic=profiled_traffic("linear"))}
 
 
 def wl_attention(stream, steps, warmup):
@@ -336,7 +339,7 @@ def wl_attention(stream, steps, warmup):
     tf = flop / ms / 1e9
     return {"workload": "attention_prefill_causal_gqa_32q8kv_d64_t2048", "unit": "TFLOP/s", "value": tf, "ms": ms,
             "flop": flop, "kernel": "attention_prefill_kernel<4,4,2>",
-            "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma")}
+            "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma", traffic=profiled_traffic("attention"))}
 
 
 def wl_attention_decode(stream, steps, warmup):
@@ -367,7 +370,7 @@ def wl_attention_decode(stream, steps, warmup):
     return {"workload": "attention_decode_32q8kv_d64_len2048", "unit": "GB/s", "value": gbs, "ms": ms,
             "bytes": nbytes, "kernel": "attention_decode_partial_kernel (fused merge)",
             "two_launch_ms": ms_two, "two_launch_kernels": "attention_decode_partial_kernel+combine",
-            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm")}
+            "roofline": roofline(gbs, HBM_PEAK_GBS, "GB/s", "hbm", traffic=profiled_traffic("attention_decode"))}
 
 
 def wl_llama(stream, steps, warmup, bf16=False, prompt_len=512, new_tokens=256, published=None):
@@ -433,8 +436,11 @@ def wl_llama(stream, steps, warmup, bf16=False, prompt_len=512, new_tokens=256, 
            "ms": pre + dec, "ttft_ms": round(pre, 3), "decode_ms_per_token": round(dec / (new_tokens - 1), 4),
            "kernel": f"swiglu_gemv_kernel<8{', bf16' if bf16 else ''}> (gate/up)",
            "roofline": roofline(gu_gbs, HBM_PEAK_GBS, "GB/s", "hbm",
-                                traffic=None if bf16 else profiled_traffic("gate_up")),
-           "decode_step_roofline": roofline(step_gbs, HBM_PEAK_GBS, "GB/s", "hbm"),
+                                traffic=profiled_traffic("bf16_gate_up" if bf16 else "gate_up")),
+           # the whole step's counted bytes exist for the configuration they were measured on
+           "decode_step_roofline": roofline(step_gbs, HBM_PEAK_GBS, "GB/s", "hbm",
+                                            traffic=profiled_traffic("bf16_decode_step")
+                                            if bf16 and (prompt_len, new_tokens) == (512, 128) else None),
            "decode_step_loop_tok_s": round(loop_tok_s, 2),
            "decode_step_loop_method": "reference scripts/llama/benchmark.py:53-68: one opw_llama_decode_step "
                                       "call per token from the host, median of the runs",
