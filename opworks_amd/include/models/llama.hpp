@@ -54,13 +54,16 @@ struct SessionHandles {
     hipStream_t stream = nullptr;
     hipGraph_t graph = nullptr;          // the decode step, captured on first use
     hipGraphExec_t graph_exec = nullptr;
+    hipGraph_t group_graph = nullptr;    // kDecodeGroup chained decode steps in one graph
+    hipGraphExec_t group_exec = nullptr;
     llama::StepState *h_state = nullptr; // pinned host copy of the device step state
     std::vector<hipEvent_t> step_events; // chained decode: completion of the steps in flight
 
     SessionHandles() = default;
     SessionHandles(SessionHandles &&o) noexcept
         : stream(std::exchange(o.stream, nullptr)), graph(std::exchange(o.graph, nullptr)),
-          graph_exec(std::exchange(o.graph_exec, nullptr)), h_state(std::exchange(o.h_state, nullptr)),
+          graph_exec(std::exchange(o.graph_exec, nullptr)), group_graph(std::exchange(o.group_graph, nullptr)),
+          group_exec(std::exchange(o.group_exec, nullptr)), h_state(std::exchange(o.h_state, nullptr)),
           step_events(std::move(o.step_events)) {
         o.step_events.clear();
     }
@@ -70,6 +73,8 @@ struct SessionHandles {
             stream = std::exchange(o.stream, nullptr);
             graph = std::exchange(o.graph, nullptr);
             graph_exec = std::exchange(o.graph_exec, nullptr);
+            group_graph = std::exchange(o.group_graph, nullptr);
+            group_exec = std::exchange(o.group_exec, nullptr);
             h_state = std::exchange(o.h_state, nullptr);
             step_events = std::move(o.step_events);
             o.step_events.clear();
@@ -84,6 +89,10 @@ struct SessionHandles {
         for (hipEvent_t e : step_events)
             (void)hipEventDestroy(e);
         step_events.clear();
+        if (group_exec)
+            (void)hipGraphExecDestroy(group_exec);
+        if (group_graph)
+            (void)hipGraphDestroy(group_graph);
         if (graph_exec)
             (void)hipGraphExecDestroy(graph_exec);
         if (graph)
@@ -92,6 +101,8 @@ struct SessionHandles {
             (void)hipHostFree(h_state);
         if (stream)
             (void)hipStreamDestroy(stream);
+        group_exec = nullptr;
+        group_graph = nullptr;
         graph_exec = nullptr;
         graph = nullptr;
         h_state = nullptr;
@@ -253,20 +264,26 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
                                          s.stream));
         // At most 16 steps are queued ahead of the GPU: enough that it never waits for the host,
         // few enough that eager mode (82 kernels per step) keeps a short queue. An event closes
-        // every group of 4 steps; a group starts once the group 4 before it has completed.
-        constexpr int kGroup = 4, kGroups = 4;
+        // every group of kDecodeGroup steps; a group starts once the group 4 before it has
+        // completed. A whole group is one launch of a graph holding its steps.
+        constexpr int kGroup = kDecodeGroup, kGroups = 2;
         while (static_cast<int>(s.step_events.size()) < kGroups) {
             hipEvent_t e;
             OPWORKS_HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
             s.step_events.push_back(e);
         }
-        for (int i = 0; i < n; ++i) {
+        for (int i = 0; i < n;) {
             const int g = i / kGroup;
-            if (i % kGroup == 0 && g >= kGroups)
+            if (g >= kGroups)
                 OPWORKS_HIP_CHECK(hipEventSynchronize(s.step_events[g % kGroups]));
-            launch_decode(s);
-            if (i % kGroup == kGroup - 1)
-                OPWORKS_HIP_CHECK(hipEventRecord(s.step_events[g % kGroups], s.stream));
+            const int steps = n - i < kGroup ? n - i : kGroup;
+            if (steps == kGroup)
+                launch_decode_group(s);
+            else
+                for (int k = 0; k < steps; ++k)
+                    launch_decode(s);
+            i += steps;
+            OPWORKS_HIP_CHECK(hipEventRecord(s.step_events[g % kGroups], s.stream));
         }
         OPWORKS_HIP_CHECK(hipMemcpyAsync(out, s.workspace.gen.data() + pos0, sizeof(int32_t) * static_cast<size_t>(n),
                                          hipMemcpyDeviceToHost, s.stream));
@@ -613,10 +630,27 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         OPWORKS_HIP_CHECK(hipGraphLaunch(s.graph_exec, s.stream));
     }
 
-    void capture_decode_graph(Session &s) const {
+    // kDecodeGroup chained greedy steps (device state with chain = 1): one graph launch, with
+    // no gap between the steps' graphs (about 8 us per step in separate launches).
+    static constexpr int kDecodeGroup = 16;
+    void launch_decode_group(Session &s) const {
+        if (!use_graph()) {
+            for (int k = 0; k < kDecodeGroup; ++k)
+                enqueue_decode(s);
+            return;
+        }
+        if (!s.group_exec)
+            capture_graph(s, kDecodeGroup, s.group_graph, s.group_exec);
+        OPWORKS_HIP_CHECK(hipGraphLaunch(s.group_exec, s.stream));
+    }
+
+    void capture_decode_graph(Session &s) const { capture_graph(s, 1, s.graph, s.graph_exec); }
+
+    void capture_graph(Session &s, int steps, hipGraph_t &graph, hipGraphExec_t &exec) const {
         OPWORKS_HIP_CHECK(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
         try {
-            enqueue_decode(s);
+            for (int k = 0; k < steps; ++k)
+                enqueue_decode(s);
         } catch (...) {
             hipGraph_t g = nullptr;
             (void)hipStreamEndCapture(s.stream, &g);
@@ -624,8 +658,8 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
                 (void)hipGraphDestroy(g);
             throw;
         }
-        OPWORKS_HIP_CHECK(hipStreamEndCapture(s.stream, &s.graph));
-        OPWORKS_HIP_CHECK(hipGraphInstantiate(&s.graph_exec, s.graph, nullptr, nullptr, 0));
+        OPWORKS_HIP_CHECK(hipStreamEndCapture(s.stream, &graph));
+        OPWORKS_HIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
     }
 
     // ---- prefill -------------------------------------------------------------
