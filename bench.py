@@ -232,21 +232,28 @@ import json, sys, torch
 kind, n, calls, seed = sys.argv[1], int(sys.argv[2]), int(sys.argv[3]), int(sys.argv[4])
 dev = torch.device("cuda", 0)
 g = torch.Generator(device=dev).manual_seed(seed)
-dt = torch.bfloat16 if kind == "bf16" else torch.float32  # kinds: f32 (A @ B), f32nk and bf16 (A @ W^T)
+# kinds: f32 (A @ B), f32nk (X @ W^T), bf16 (A @ W^T, bf16 result), bf16f32 (A @ W^T, fp32 result)
+dt = torch.bfloat16 if kind.startswith("bf16") else torch.float32
 a = (torch.randn(n, n, device=dev, generator=g) / 64).to(dt)
 b = (torch.randn(n, n, device=dev, generator=g) / 64).to(dt)
 rhs = b if kind == "f32" else b.t()
-out = torch.empty(n, n, device=dev, dtype=dt)
+out = torch.empty(n, n, device=dev, dtype=torch.float32 if kind == "bf16f32" else dt)
+if kind == "bf16f32":
+    def call():
+        torch.mm(a, rhs, torch.float32, out=out)
+else:
+    def call():
+        torch.matmul(a, rhs, out=out)
 import time
 t_end = time.perf_counter() + 0.3  # back-to-back calls past the clock ramp, as this library's workloads get
 while time.perf_counter() < t_end:
     for _ in range(10):
-        torch.matmul(a, rhs, out=out)
+        call()
     torch.cuda.synchronize()
 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 e0.record()
 for _ in range(calls):
-    torch.matmul(a, rhs, out=out)
+    call()
 e1.record()
 torch.cuda.synchronize()
 print(json.dumps({"ms": e0.elapsed_time(e1) / calls, "torch": torch.__version__}))
@@ -257,7 +264,8 @@ def library_reference(kind, n=4096, calls=50):
     """The vendor library on the same problem, for comparison only (opt-in, --library-reference):
     torch.matmul (hipBLASLt on ROCm) on n^3 N(0, 1/64) operands, `calls` back-to-back calls
     between two events after 0.3 s of untimed ones (the clock ramp). kind "f32": fp32 A @ B; "bf16": bf16 A @ W^T with
-    a bf16 result (half the output bytes of this library's fp32 result); "f32nk": fp32 X @ W^T."""
+    a bf16 result (half the output bytes of this library's fp32 result); "bf16f32": bf16 A @ W^T with an fp32
+    result (torch.mm's out_dtype, this library's problem); "f32nk": fp32 X @ W^T."""
     import subprocess
 
     proc = subprocess.run([sys.executable, "-c", LIBRARY_REFERENCE_CHILD, kind, str(n), str(calls), str(SEED)],
@@ -266,7 +274,8 @@ def library_reference(kind, n=4096, calls=50):
         return {"impl": "torch.matmul", "error": proc.stderr.strip().splitlines()[-1:]}
     r = json.loads(proc.stdout.strip().splitlines()[-1])
     ms = r["ms"]
-    desc = {"f32": "fp32, A @ B", "f32nk": "fp32, X @ W^T", "bf16": "bf16 in/out, A @ W^T"}[kind]
+    desc = {"f32": "fp32, A @ B", "f32nk": "fp32, X @ W^T", "bf16": "bf16 in/out, A @ W^T",
+            "bf16f32": "bf16 in, fp32 out, A @ W^T"}[kind]
     return {"impl": f"torch {r['torch']} matmul ({desc})",
             "ms": round(ms, 5), "value": round(2.0 * n ** 3 / ms / 1e9, 2), "unit": "TFLOP/s"}
 
@@ -734,14 +743,15 @@ def main() -> int:
         print(f"[bench] {name}: {results[name]['value']:.1f} {results[name]['unit']} "
               f"({results[name]['ms']:.4f} ms/step)", file=sys.stderr, flush=True)
     if args.library_reference:  # after every workload of this library, so it cannot disturb them
-        for name, kind in (("gemm", "f32"), ("gemm_bf16", "bf16"), ("linear", "f32nk")):
+        for name, kind, key in (("gemm", "f32", "library_reference"), ("gemm_bf16", "bf16f32", "library_reference"),
+                                ("gemm_bf16", "bf16", "library_reference_bf16_out"),
+                                ("linear", "f32nk", "library_reference")):
             if name in results:
                 ref = library_reference(kind)
                 if "value" in ref:
                     ref["ratio"] = round(results[name]["value"] / ref["value"], 4)  # this library / the vendor's
-                results[name]["library_reference"] = ref
-                print(f"[bench] {name} library reference: {ref.get('value', ref.get('error'))}", file=sys.stderr,
-                      flush=True)
+                results[name][key] = ref
+                print(f"[bench] {name} {key}: {ref.get('value', ref.get('error'))}", file=sys.stderr, flush=True)
     if not args.no_cpu:  # the oracle on this host beside every GPU figure (bounded samples)
         for name in names:
             if name != headline and name in CPU_SAMPLES:
