@@ -136,6 +136,20 @@ int opw_convert_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, void *st
  * requires S >= T, q_offset == S - T, head_dim in {16,32,48,64}, cap >= S) */
 int opw_attention_prefill_f32(const float *q_heads, const float *kcache, const float *vcache, float *out, int T, int S,
                               int q_offset, int num_q_heads, int kv_rep, int head_dim, int cap, void *stream);
+/* Workspace form of opw_attention_prefill_f32 (no counterpart in the reference; same results to
+ * rounding). The query-tile groups with the most K/V tiles (more than split_threshold; negative
+ * picks it from the shape and the CU count) run as two workgroups over the halves of their K/V
+ * range, and the one that finishes last merges them: a one-round causal grid otherwise ends with
+ * one workgroup running the longest range alone on its CU. rec needs no initialisation; counters
+ * must be zero before the first call, and every call leaves them at zero. Calls that share a
+ * workspace must not overlap. Smaller memory than opw_attention_prefill_workspace_size reports
+ * splits fewer groups (none: the plain kernel). */
+int opw_attention_prefill_workspace_size(int T, int S, int q_offset, int num_q_heads, int kv_rep, int head_dim,
+                                         int split_threshold, int64_t *rec_floats, int64_t *counter_ints);
+int opw_attention_prefill_ws_f32(const float *q_heads, const float *kcache, const float *vcache, float *out, int T,
+                                 int S, int q_offset, int num_q_heads, int kv_rep, int head_dim, int cap, float *rec,
+                                 int64_t rec_floats, int *counters, int64_t counter_ints, int split_threshold,
+                                 void *stream);
 /* One query per head against `len` cache entries (reference: ops::attention_decode,
  * include/ops/attention_decode.cuh:98-109; q/out [num_q_heads][head_dim], len <= 8192). The
  * reference's contract: one launch, nothing allocated (graph-capturable), head_dim in [1, 64], q and

@@ -83,6 +83,11 @@ _SIGNATURES = {
     "opw_convert_f32_to_bf16": (c_int, [c_void_p, c_void_p, c_int64, c_void_p]),
     "opw_attention_prefill_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                           c_int, c_int, c_void_p]),
+    "opw_attention_prefill_workspace_size": (c_int, [c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                                     ctypes.POINTER(c_int64), ctypes.POINTER(c_int64)]),
+    "opw_attention_prefill_ws_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
+                                             c_int, c_int, c_int, c_void_p, c_int64, c_void_p, c_int64, c_int,
+                                             c_void_p]),
     "opw_attention_decode_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                          c_void_p]),
     "opw_attention_decode_workspace_size": (c_int, [c_int, c_int, c_int]),
@@ -415,6 +420,21 @@ class _Ops:
                           kv_rep: int, head_dim: int, cap: int, stream=None) -> None:
         check(lib().opw_attention_prefill_f32(_p(q), _p(k), _p(v), _p(out), T, S, q_offset, num_q_heads, kv_rep,
                                               head_dim, cap, _stream(stream)))
+
+    # Workspace form: the heaviest query-tile groups split their K/V range over two workgroups.
+    def attention_prefill_workspace_size(self, T: int, S: int, q_offset: int, num_q_heads: int, kv_rep: int,
+                                         head_dim: int, split_threshold: int = -1) -> tuple:
+        rec, ctr = c_int64(0), c_int64(0)
+        check(lib().opw_attention_prefill_workspace_size(T, S, q_offset, num_q_heads, kv_rep, head_dim,
+                                                         split_threshold, ctypes.byref(rec), ctypes.byref(ctr)))
+        return rec.value, ctr.value
+
+    def attention_prefill_ws(self, q: Ptr, k: Ptr, v: Ptr, out: Ptr, T: int, S: int, q_offset: int, num_q_heads: int,
+                             kv_rep: int, head_dim: int, cap: int, rec: Ptr, rec_floats: int, counters: Ptr,
+                             counter_ints: int, split_threshold: int = -1, stream=None) -> None:
+        check(lib().opw_attention_prefill_ws_f32(_p(q), _p(k), _p(v), _p(out), T, S, q_offset, num_q_heads, kv_rep,
+                                                 head_dim, cap, _p(rec), rec_floats, _p(counters), counter_ints,
+                                                 split_threshold, _stream(stream)))
 
     def attention_decode(self, q: Ptr, k: Ptr, v: Ptr, out: Ptr, num_q_heads: int, kv_rep: int, head_dim: int,
                          length: int, max_seq: int, workspace: Ptr = None, workspace_size: int = 0,

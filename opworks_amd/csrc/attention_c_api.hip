@@ -18,6 +18,28 @@ int opw_attention_prefill_f32(const float *q_heads, const float *kcache, const f
     });
 }
 
+int opw_attention_prefill_workspace_size(int T, int S, int q_offset, int num_q_heads, int kv_rep, int head_dim,
+                                         int split_threshold, int64_t *rec_floats, int64_t *counter_ints) {
+    return guard([&] {
+        opworks::detail::require(rec_floats && counter_ints, "attention_prefill_workspace_size: null output");
+        opworks::ops::attention_prefill_workspace_size(T, S, q_offset, num_q_heads, kv_rep, head_dim, split_threshold,
+                                                       rec_floats, counter_ints);
+        return 0;
+    });
+}
+
+int opw_attention_prefill_ws_f32(const float *q_heads, const float *kcache, const float *vcache, float *out, int T,
+                                 int S, int q_offset, int num_q_heads, int kv_rep, int head_dim, int cap, float *rec,
+                                 int64_t rec_floats, int *counters, int64_t counter_ints, int split_threshold,
+                                 void *stream) {
+    return guard([&] {
+        opworks::ops::attention_prefill_ws(q_heads, kcache, vcache, out, T, S, q_offset, num_q_heads, kv_rep, head_dim,
+                                           cap, rec, rec_floats, counters, counter_ints, split_threshold,
+                                           static_cast<hipStream_t>(stream));
+        return 0;
+    });
+}
+
 int opw_attention_decode_f32(const float *q, const float *kcache, const float *vcache, float *out, int num_q_heads,
                              int kv_rep, int head_dim, int len, int max_seq, void *stream) {
     return guard([&] {

@@ -121,6 +121,9 @@ struct LlamaSession : detail::SessionHandles {
     Workspace workspace;
     int last_prefill_rows = 0;
 
+    // Records of the prefill attention's split groups held per session (64 MiB).
+    static constexpr int64_t kPrefillSplitCap = int64_t(1) << 24;
+
     // Sizes of the kernels' per-session scratch at max_seq_len.
     static WorkspaceSizes workspace_sizes(const ModelConfig &cfg, int max_seq_len, bool bf16_weights) {
         WorkspaceSizes ws;
@@ -131,6 +134,18 @@ struct LlamaSession : detail::SessionHandles {
         ws.state_ints = sizeof(llama::StepState) / sizeof(int32_t);
         ws.argmax_groups = llama::kArgmaxGroups;
         ws.attn_counter_ints = cfg.num_kv_heads * detail::kAttnCounterStride;
+        // the prefill attention's split records for the largest need over the prompt lengths this
+        // session can take, at most kPrefillSplitCap floats (past it fewer groups split)
+        if (max_seq_len >= 2 && cfg.head_dim % 16 == 0 && cfg.head_dim <= detail::kAttnMaxD) {
+            for (int n = 16; n < max_seq_len + 16; n += 16) {
+                const int t = n < max_seq_len ? n : max_seq_len;
+                int64_t rec = 0, ctr = 0;
+                ops::attention_prefill_workspace_size(t, t, 0, cfg.num_q_heads, cfg.kv_rep(), cfg.head_dim, -1, &rec,
+                                                      &ctr);
+                ws.prefill_split_floats = std::max(ws.prefill_split_floats, std::min(rec, kPrefillSplitCap));
+                ws.prefill_split_ints = std::max(ws.prefill_split_ints, ctr);
+            }
+        }
         return ws;
     }
 
@@ -139,6 +154,9 @@ struct LlamaSession : detail::SessionHandles {
         OPWORKS_HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
         OPWORKS_HIP_CHECK(hipMemsetAsync(workspace.state.data(), 0, workspace.state.bytes(), stream));
         OPWORKS_HIP_CHECK(hipMemsetAsync(workspace.attn_counters.data(), 0, workspace.attn_counters.bytes(), stream));
+        if (workspace.attn_split_counters.size() > 0)
+            OPWORKS_HIP_CHECK(hipMemsetAsync(workspace.attn_split_counters.data(), 0,
+                                             workspace.attn_split_counters.bytes(), stream));
         OPWORKS_HIP_CHECK(hipMemsetAsync(workspace.lm_counter.data(), 0, workspace.lm_counter.bytes(), stream));
         OPWORKS_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&h_state), sizeof(llama::StepState)));
         *h_state = llama::StepState{0, 0, -1, 0};
@@ -838,8 +856,11 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
             launch_async(st, llama::rope_split_kernel, detail::stream_grid(int64_t(n) * (qh + 2 * kvh) * (D / 2)),
                          256, s.workspace.qkv.data(), w_.rope_inv_freq.data(), s.workspace.q_heads.data(), layer_k(s, l), layer_v(s, l), n, qh,
                          kvh, D, s.cache.max_seq_len, 0);
-            ops::attention_prefill(s.workspace.q_heads.data(), layer_k(s, l), layer_v(s, l), s.workspace.attn_heads.data(), n, n, 0, qh,
-                                   cfg_.kv_rep(), D, s.cache.max_seq_len, st);
+            ops::attention_prefill_ws(s.workspace.q_heads.data(), layer_k(s, l), layer_v(s, l),
+                                      s.workspace.attn_heads.data(), n, n, 0, qh, cfg_.kv_rep(), D, s.cache.max_seq_len,
+                                      s.workspace.attn_split.data(), s.workspace.attn_split.size(),
+                                      s.workspace.attn_split_counters.data(), s.workspace.attn_split_counters.size(),
+                                      -1, st);
             if (xb)
                 launch_async(st, llama::merge_heads_kernel<uint16_t>, detail::stream_grid(int64_t(n) * qh * D), 256,
                              s.workspace.attn_heads.data(), xbits, n, qh, D);

@@ -36,8 +36,10 @@
 // combine kernel merges the chunks. The valid length can be read from device
 // memory, so one graph serves every decode position.
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <type_traits>
 
 #include "../core/hip_utils.hpp"
 #include "../core/wave.hpp"
@@ -51,6 +53,29 @@ constexpr int kAttnKTile = 32;     // keys per staged K/V tile (two 16-key MFMA 
 constexpr int kAttnMaxD = 64;
 constexpr int kAttnMaxRep = 16;    // q heads per kv head (waves per decode workgroup)
 constexpr float kLog2e = 1.4426950408889634f;
+
+// ints from one kv head's arrival counter to the next (256 B): every counter sits on a cache
+// line of its own, so the chunk workgroups of different kv heads never queue behind each
+// other's atomics on one line (at 2048 keys: 8.35 against 10.4 us per fused call).
+constexpr int kAttnCounterStride = 64;
+
+// s_waitcnt operand of gfx9 for vmcnt(0) with expcnt and lgkmcnt left at their maxima
+// (vmcnt bits [3:0] and [15:14] = 0, expcnt [6:4] = 7, lgkmcnt [11:8] = 15): waits until
+// every vector memory access of the wave, stores included, has completed.
+constexpr int kWaitVmcnt0 = 0x0F70;
+
+template <bool kCoherent> __device__ __forceinline__ float record_load(const float *p) {
+    if constexpr (kCoherent)
+        return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        return *p;
+}
+template <bool kCoherent> __device__ __forceinline__ void record_store(float *p, float v) {
+    if constexpr (kCoherent)
+        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *p = v;
+}
 
 // c(x[l], x[l ^ 16]) then c(., .[l ^ 32]): the combine over the four 16-lane
 // rows of a wave, by gfx950's v_permlane16_swap / v_permlane32_swap (a VGPR
@@ -90,15 +115,96 @@ __device__ __forceinline__ int prefill_tile_of_rank(int rank, int ntq, int pass_
     return ntq - 1 - pos;
 }
 
+// ---- split of the heaviest query-tile groups (workspace form) --------------
+// A causal grid's last query tiles carry the longest K/V ranges. Measured per CU, a CU whose
+// heavier workgroup ran 56-64 K/V tiles finished 6-8% after the others: once its lighter
+// workgroup is done, one 8-wave workgroup runs the long chain alone. In the workspace form the
+// groups with more than `thr` K/V tiles run as two workgroups, one per half of the range, and the
+// one that finishes last merges the halves. Units go out in descending order of work (a half
+// counts n/2 tiles), so the big units start first and the small ones fill the slots that free up.
+struct PrefillGeom {
+    int kTiles, ntq, S, q_offset;
+    // K/V tiles of query-tile group g: its last query tile's causal range
+    __host__ __device__ int tiles(int g) const {
+        const int last = g * kTiles + kTiles - 1 < ntq - 1 ? g * kTiles + kTiles - 1 : ntq - 1;
+        const int end = q_offset + last * kAttnQTile + kAttnQTile;
+        return ((end < S ? end : S) + kAttnKTile - 1) / kAttnKTile;
+    }
+    // First tile of the second half: half the range, and no later than the group's first query
+    // position, so every query row of the group sees the second half's first key.
+    __host__ __device__ int split_point(int g) const {
+        const int half = tiles(g) / 2, first = (q_offset + g * kTiles * kAttnQTile) / kAttnKTile;
+        return half < first ? half : first;
+    }
+    __host__ __device__ bool is_split(int g, int thr) const { return tiles(g) > thr && split_point(g) >= 1; }
+    // The split groups are a suffix of the group indices (tiles and split point never decrease
+    // with g): the first of them, or ngroups if none.
+    __host__ __device__ int first_split(int ngroups, int thr) const {
+        int lo = 0, hi = ngroups;
+        while (lo < hi) {
+            const int mid = (lo + hi) / 2;
+            if (is_split(mid, thr))
+                hi = mid;
+            else
+                lo = mid + 1;
+        }
+        return lo;
+    }
+};
+
+struct PrefillUnit {
+    int g;        // query-tile group
+    int half;     // -1: the whole K/V range; 0 or 1: a half
+    int kt_begin, kt_end;
+    int slot;     // split groups only: g - first split group
+};
+
+// Unit of dispatch rank r: the halves (key n tiles each, groups from the last down, half 0 first)
+// merged with the unsplit groups (key 2n, from gs - 1 down) in descending key order, ties to the
+// halves. The number i of halves among the first r units comes from a binary search along the
+// merge path.
+__device__ __forceinline__ PrefillUnit prefill_unit_of_rank(int r, int ngroups, int thr, const PrefillGeom &geo) {
+    const int gs = geo.first_split(ngroups, thr);
+    const int na = 2 * (ngroups - gs), nb = gs;
+    auto key_a = [&](int i) { return geo.tiles(ngroups - 1 - i / 2); };
+    auto key_b = [&](int j) { return 2 * geo.tiles(gs - 1 - j); };
+    int lo = r - nb > 0 ? r - nb : 0, hi = r < na ? r : na;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (mid == 0 || r - mid == nb || key_a(mid - 1) >= key_b(r - mid))
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const int i = lo, j = r - i;
+    if (i < na && (j == nb || key_a(i) >= key_b(j))) {
+        const int g = ngroups - 1 - i / 2, half = i % 2, h = geo.split_point(g);
+        return {g, half, half ? h : 0, half ? geo.tiles(g) : h, g - gs};
+    }
+    const int g = gs - 1 - j;
+    return {g, -1, 0, geo.tiles(g), 0};
+}
+
+// Merge state of the split units: per (split group, kv head x slice) workgroup pair, two records
+// of kRec x threads floats ([value][thread], coalesced) and one arrival counter on a 256-byte line
+// of its own, zero between launches (the merging workgroup resets it).
+struct PrefillSplit {
+    float *rec;
+    int *counters;
+    int thr;       // groups with more K/V tiles than this split (when their split point is >= 1)
+    int alternate; // nonzero: units go out in passes of alternating direction, not in descending order
+};
+
 // amdgpu_waves_per_eu: with four or more waves per workgroup the register budget is 128
 // (four resident waves per SIMD, as many as the LDS allows); the bound also makes the
-// compiler keep the MFMA accumulators in VGPRs rather than AGPRs.
-template <int kDT, int kWaves, int kTiles>
+// compiler keep the MFMA accumulators in VGPRs rather than AGPRs. kSplit: the workspace form
+// (units from prefill_unit_of_rank, halves merged through `sp`).
+template <int kDT, int kWaves, int kTiles, bool kSplit = false>
 __global__ __launch_bounds__(kTiles *kWaves *kWaveSize)
 __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) void attention_prefill_kernel(
     const float *__restrict__ q_heads, const float *__restrict__ kcache, const float *__restrict__ vcache,
     float *__restrict__ out, int T, int S, int q_offset, int kv_rep, int num_kv_heads, int cap, float qscale,
-    int pass_width) {
+    int pass_width, PrefillSplit sp) {
     using Shape = PrefillShape<kDT, kWaves, kTiles>;
     constexpr int D = Shape::kD, kLd = Shape::kLd, kQ = Shape::kQ;
     extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -107,7 +213,24 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
     const int per_tile = num_kv_heads * slices;
     const int ntq = (T + kAttnQTile - 1) / kAttnQTile;
     const int ngroups = (ntq + kTiles - 1) / kTiles; // query-tile groups
-    const int grp = prefill_tile_of_rank(static_cast<int>(blockIdx.x) / per_tile, ngroups, pass_width);
+    const int rank = static_cast<int>(blockIdx.x) / per_tile;
+    int grp, kt_begin = 0, kt_end = -1, half = -1, slot = 0; // kt_end < 0: the group's whole range
+    if constexpr (kSplit) {
+        const PrefillGeom geo{kTiles, ntq, S, q_offset};
+        int pos = rank;
+        if (sp.alternate) {
+            const int nunits = ngroups + (ngroups - geo.first_split(ngroups, sp.thr));
+            pos = nunits - 1 - prefill_tile_of_rank(rank, nunits, pass_width);
+        }
+        const PrefillUnit u = prefill_unit_of_rank(pos, ngroups, sp.thr, geo);
+        grp = u.g;
+        half = u.half;
+        kt_begin = u.kt_begin;
+        kt_end = u.kt_end;
+        slot = u.slot;
+    } else {
+        grp = prefill_tile_of_rank(rank, ngroups, pass_width);
+    }
     const int kvh = (static_cast<int>(blockIdx.x) % per_tile) / slices;
     const int slice = static_cast<int>(blockIdx.x) % slices;
     const int wave = threadIdx.x / kWaveSize, lane = threadIdx.x % kWaveSize;
@@ -145,7 +268,7 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
     const int my_ntiles = tile_ok ? (kv_end + kAttnKTile - 1) / kAttnKTile : 0;
     const int q0_last = (grp * kTiles + kTiles - 1 < ntq ? grp * kTiles + kTiles - 1 : ntq - 1) * kAttnQTile;
     const int kv_end_last = (q_offset + q0_last + kAttnQTile) < S ? (q_offset + q0_last + kAttnQTile) : S;
-    const int ntiles = (kv_end_last + kAttnKTile - 1) / kAttnKTile;
+    const int ntiles = kt_end >= 0 ? kt_end : (kv_end_last + kAttnKTile - 1) / kAttnKTile;
 
     // K/V tile staging through registers: chunk c = tid + i * threads is row c / (D/4).
     // Loads are unconditional (rows past S read row S-1 and are zeroed when staged, chunks
@@ -195,11 +318,11 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
         oacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = kNegInf, l_part = 0.f; // l_part: this lane's share of the row sum
 
-    fetch(0);
-    commit(0, 0);
+    fetch(kt_begin);
+    commit(0, kt_begin);
     __syncthreads();
-    for (int kt = 0; kt < ntiles; ++kt) {
-        const int buf = kt & 1;
+    for (int kt = kt_begin; kt < ntiles; ++kt) {
+        const int buf = (kt - kt_begin) & 1;
         fetch(kt + 1); // in flight during this tile's MFMAs (all zeros past the last tile)
         __builtin_amdgcn_sched_barrier(0); // keep the loads at the top
         const float *Ks = lds + buf * kStage;
@@ -289,7 +412,56 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
     }
 
     // oacc[t][r] = O^T[16t + 4g + r][q]: four consecutive head-dim values of row q.
-    const float l = column_combine(l_part, wave::Add{});
+    float l = column_combine(l_part, wave::Add{});
+    if constexpr (kSplit) {
+        if (half >= 0) {
+            // Both halves write their (m, l, O) records with agent-coherent stores (through the
+            // XCD's L2), wait for them, and count in; the second to arrive merges in the fixed
+            // order half 0, half 1 and resets the counter. No workgroup waits on another.
+            constexpr int kRec = 2 + 4 * kDT, kThr = Shape::kThreads;
+            const int pair = slot * per_tile + static_cast<int>(blockIdx.x) % per_tile;
+            float *mine = sp.rec + (int64_t(pair) * 2 + half) * kRec * kThr + threadIdx.x;
+            const float *other = sp.rec + (int64_t(pair) * 2 + (1 - half)) * kRec * kThr + threadIdx.x;
+            record_store<true>(mine, m_run);
+            record_store<true>(mine + kThr, l);
+#pragma unroll
+            for (int t = 0; t < kDT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    record_store<true>(mine + (2 + 4 * t + r) * kThr, oacc[t][r]);
+            __shared__ int last;
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); // the record stores have completed
+            __syncthreads();
+            int *counter = sp.counters + int64_t(pair) * kAttnCounterStride;
+            if (threadIdx.x == 0)
+                last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
+            __syncthreads();
+            if (!last)
+                return;
+            const float m_o = record_load<true>(other), l_o = record_load<true>(other + kThr);
+            f32x4 o_o[kDT];
+#pragma unroll
+            for (int t = 0; t < kDT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    o_o[t][r] = record_load<true>(other + (2 + 4 * t + r) * kThr);
+            const float m0 = half == 0 ? m_run : m_o, m1 = half == 0 ? m_o : m_run;
+            const float l0 = half == 0 ? l : l_o, l1 = half == 0 ? l_o : l;
+            const float M = fmaxf(m0, m1);
+            const float c0 = m0 == kNegInf ? 0.f : __builtin_amdgcn_exp2f(m0 - M);
+            const float c1 = m1 == kNegInf ? 0.f : __builtin_amdgcn_exp2f(m1 - M);
+            l = l0 * c0 + l1 * c1;
+#pragma unroll
+            for (int t = 0; t < kDT; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float a0 = half == 0 ? oacc[t][r] : o_o[t][r], a1 = half == 0 ? o_o[t][r] : oacc[t][r];
+                    oacc[t][r] = a0 * c0 + a1 * c1;
+                }
+            if (threadIdx.x == 0)
+                __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
     const float inv = l > 0.f ? 1.f / l : 0.f;
     if (head_ok && tile_ok && q < T) {
         float *orow = out + (int64_t(h) * T + q) * D;
@@ -304,54 +476,148 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
     }
 }
 
+// Caller memory of the workspace form: the split units' records and their arrival counters
+// (zero before the first call; every call leaves them at zero). thr < 0 picks the split
+// threshold automatically.
+struct PrefillWorkspaceArgs {
+    float *rec = nullptr;
+    int64_t rec_floats = 0;
+    int *counters = nullptr;
+    int64_t counter_ints = 0;
+    int thr = -1;
+};
+
+// Workspace form on the host: the threshold, how many groups split, and what that needs.
+struct PrefillSplitPlan {
+    int thr = 0, nsplit = 0;
+    int alternate = 0; // units in alternating passes (one-tile grids) or in descending order
+    int64_t rec_floats = 0, counter_ints = 0;
+};
+
+// Automatic threshold, from a sweep of thresholds and orders at 32 q / 8 kv heads, D = 64:
+//  * one-tile grids (at most 3 workgroups per CU): every group past 2 K/V tiles splits and the
+//    units go out in alternating passes, so a CU holds heavy and light halves (T = 512:
+//    25.9 -> 20.8 us; T = 1024: 49.6 -> 47.7 us);
+//  * two-tile grids of one round (T = 2048, config 4: 512 workgroups, two per CU) do not split:
+//    the alternating passes already pair each heavy group with a light one on its CU, and every
+//    split form measured slower (155 against 162-175 us);
+//  * two-tile grids of several rounds split past 2 tiles in descending order, so the long halves
+//    start first (T = 4096: 603 -> 570 us).
+// The threshold then rises until the records and counters fit the caller's memory.
+template <int kDT, int kWaves, int kTiles>
+inline PrefillSplitPlan prefill_split_plan(int T, int S, int q_offset, int kv_rep, int kvh, int thr_req,
+                                           int64_t rec_cap, int64_t counter_cap) {
+    using Shape = PrefillShape<kDT, kWaves, kTiles>;
+    const int per_tile = kvh * ((kv_rep + kWaves - 1) / kWaves);
+    const int ntq = static_cast<int>(blocks_for64(T, kAttnQTile));
+    const int ngroups = (ntq + kTiles - 1) / kTiles;
+    const PrefillGeom geo{kTiles, ntq, S, q_offset};
+    PrefillSplitPlan p;
+    p.alternate = kTiles == 1;
+    if (thr_req >= 0) {
+        p.thr = thr_req;
+    } else {
+        // resident workgroups per CU: 4 waves per SIMD at kWaves >= 4 (128 registers), else 2
+        const int per_cu = std::max(1, (kWaves >= 4 ? 16 : 8) / (kTiles * kWaves));
+        const int64_t one_round = int64_t(cu_count()) * per_cu;
+        p.thr = kTiles == 2 && int64_t(ngroups) * per_tile <= one_round ? INT32_MAX : 2;
+    }
+    const int64_t rec_per_group = int64_t(per_tile) * 2 * (2 + 4 * kDT) * Shape::kThreads;
+    const int64_t ctr_per_group = int64_t(per_tile) * kAttnCounterStride;
+    for (;;) {
+        const int gs = geo.first_split(ngroups, p.thr);
+        p.nsplit = ngroups - gs;
+        p.rec_floats = p.nsplit * rec_per_group;
+        p.counter_ints = p.nsplit * ctr_per_group;
+        if (p.nsplit == 0 || (p.rec_floats <= rec_cap && p.counter_ints <= counter_cap))
+            return p;
+        p.thr = geo.tiles(gs); // that group no longer splits
+    }
+}
+
 template <int kDT, int kWaves, int kTiles>
 inline void attention_prefill_launch(const float *q, const float *k, const float *v, float *out, int T, int S,
-                                     int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream) {
+                                     int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream,
+                                     const PrefillWorkspaceArgs *ws) {
     using Shape = PrefillShape<kDT, kWaves, kTiles>;
     const int slices = (kv_rep + kWaves - 1) / kWaves;
     const int per_tile = kvh * slices;
     const int64_t ngroups = blocks_for64(blocks_for64(T, kAttnQTile), kTiles);
     require(ngroups * per_tile <= INT32_MAX, "attention_prefill: grid too large");
     const int pass_width = cu_count() / per_tile > 0 ? cu_count() / per_tile : 1;
+    if (ws) {
+        const PrefillSplitPlan p = prefill_split_plan<kDT, kWaves, kTiles>(T, S, q_offset, kv_rep, kvh, ws->thr,
+                                                                           ws->rec_floats, ws->counter_ints);
+        if (p.nsplit > 0) {
+            require((ngroups + p.nsplit) * per_tile <= INT32_MAX, "attention_prefill: grid too large");
+            launch_async_lds(stream, sizeof(float) * Shape::kLdsFloats,
+                             attention_prefill_kernel<kDT, kWaves, kTiles, true>,
+                             static_cast<int>((ngroups + p.nsplit) * per_tile), Shape::kThreads, q, k, v, out, T, S,
+                             q_offset, kv_rep, kvh, cap, scale * kLog2e, pass_width,
+                             PrefillSplit{ws->rec, ws->counters, p.thr, p.alternate});
+            return;
+        }
+    }
     launch_async_lds(stream, sizeof(float) * Shape::kLdsFloats, attention_prefill_kernel<kDT, kWaves, kTiles>,
                      static_cast<int>(ngroups * per_tile), Shape::kThreads, q, k, v, out, T, S, q_offset, kv_rep, kvh,
-                     cap, scale * kLog2e, pass_width);
+                     cap, scale * kLog2e, pass_width, PrefillSplit{nullptr, nullptr, 0, 0});
 }
 
 // Two query tiles per workgroup when the one-tile grid would fill every CU's four
 // workgroup slots (measured on near-uniform work: 76 -> 79.5% of the MFMA peak); one
 // otherwise, so short prompts still spread over all CUs.
+template <int kDT, int kWaves> inline bool prefill_two_tiles(int T, int kv_rep, int kvh) {
+    const int64_t wgs = blocks_for64(T, kAttnQTile) * kvh * ((kv_rep + kWaves - 1) / kWaves);
+    return wgs >= 4 * int64_t(cu_count());
+}
+
 template <int kDT, int kWaves>
 inline void attention_prefill_tiles(const float *q, const float *k, const float *v, float *out, int T, int S,
-                                    int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream) {
-    const int64_t wgs = blocks_for64(T, kAttnQTile) * kvh * ((kv_rep + kWaves - 1) / kWaves);
-    if (wgs >= 4 * int64_t(cu_count()))
-        attention_prefill_launch<kDT, kWaves, 2>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
+                                    int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream,
+                                    const PrefillWorkspaceArgs *ws) {
+    if (prefill_two_tiles<kDT, kWaves>(T, kv_rep, kvh))
+        attention_prefill_launch<kDT, kWaves, 2>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
     else
-        attention_prefill_launch<kDT, kWaves, 1>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_launch<kDT, kWaves, 1>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
 }
 
 template <int kDT>
 inline void attention_prefill_dispatch(const float *q, const float *k, const float *v, float *out, int T, int S,
-                                       int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream) {
+                                       int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream,
+                                       const PrefillWorkspaceArgs *ws = nullptr) {
     if (kv_rep == 1)
-        attention_prefill_tiles<kDT, 1>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_tiles<kDT, 1>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
     else if (kv_rep == 2)
-        attention_prefill_tiles<kDT, 2>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_tiles<kDT, 2>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
     else if (kv_rep <= 4)
-        attention_prefill_tiles<kDT, 4>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_tiles<kDT, 4>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
     else
-        attention_prefill_tiles<kDT, 8>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream);
+        attention_prefill_tiles<kDT, 8>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
+}
+
+// What the workspace form needs for this shape at threshold thr (< 0: automatic), unbounded.
+template <int kDT>
+inline PrefillSplitPlan prefill_split_need(int T, int S, int q_offset, int kv_rep, int kvh, int thr) {
+    constexpr int64_t kNoCap = INT64_MAX;
+    auto by_waves = [&](auto waves) {
+        constexpr int kW = decltype(waves)::value;
+        return prefill_two_tiles<kDT, kW>(T, kv_rep, kvh)
+                   ? prefill_split_plan<kDT, kW, 2>(T, S, q_offset, kv_rep, kvh, thr, kNoCap, kNoCap)
+                   : prefill_split_plan<kDT, kW, 1>(T, S, q_offset, kv_rep, kvh, thr, kNoCap, kNoCap);
+    };
+    if (kv_rep == 1)
+        return by_waves(std::integral_constant<int, 1>{});
+    if (kv_rep == 2)
+        return by_waves(std::integral_constant<int, 2>{});
+    if (kv_rep <= 4)
+        return by_waves(std::integral_constant<int, 4>{});
+    return by_waves(std::integral_constant<int, 8>{});
 }
 
 // ---------------------------------------------------------------- decode
 constexpr int kAttnChunk = 64;       // keys per decode workgroup
 constexpr int kAttnDecodeMaxLen = 8192;
 constexpr int kAttnMaxChunks = kAttnDecodeMaxLen / kAttnChunk;
-// ints from one kv head's arrival counter to the next (256 B): every counter sits on a cache
-// line of its own, so the chunk workgroups of different kv heads never queue behind each
-// other's atomics on one line (at 2048 keys: 8.35 against 10.4 us per fused call).
-constexpr int kAttnCounterStride = 64;
 
 // Partial record per (q head, chunk): [0] max, [1] sum, [2..2+D) unnormalised output.
 inline int attention_decode_workspace_floats(int num_q_heads, int max_len, int head_dim) {
@@ -396,23 +662,6 @@ __device__ __forceinline__ int decode_records(const DecodeAttnArgs &a, int nchun
     return (nchunks + a.chunks_per_record - 1) / a.chunks_per_record;
 }
 
-// s_waitcnt operand of gfx9 for vmcnt(0) with expcnt and lgkmcnt left at their maxima
-// (vmcnt bits [3:0] and [15:14] = 0, expcnt [6:4] = 7, lgkmcnt [11:8] = 15): waits until
-// every vector memory access of the wave, stores included, has completed.
-constexpr int kWaitVmcnt0 = 0x0F70;
-
-template <bool kCoherent> __device__ __forceinline__ float record_load(const float *p) {
-    if constexpr (kCoherent)
-        return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-        return *p;
-}
-template <bool kCoherent> __device__ __forceinline__ void record_store(float *p, float v) {
-    if constexpr (kCoherent)
-        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else
-        *p = v;
-}
 
 // One wave merges q head h's records in chunk order: M = max m_c,
 // L = sum l_c e^(m_c - M), out = sum acc_c e^(m_c - M) / L, 16 chunk rows per
@@ -986,6 +1235,55 @@ inline void attention_prefill(const float *q_heads, const float *kcache, const f
     case 2: detail::attention_prefill_dispatch<2>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream); break;
     case 3: detail::attention_prefill_dispatch<3>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream); break;
     default: detail::attention_prefill_dispatch<4>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream); break;
+    }
+}
+
+// Floats and ints the workspace form needs for this shape (thr < 0: the automatic
+// threshold), so the caller can size its memory; both 0 when nothing would split.
+inline void attention_prefill_workspace_size(int T, int S, int q_offset, int num_q_heads, int kv_rep, int head_dim,
+                                             int thr, int64_t *rec_floats, int64_t *counter_ints) {
+    detail::require(T > 0 && S >= T && q_offset == S - T, "attention_prefill: bad shape/offset");
+    detail::require(num_q_heads > 0 && kv_rep > 0 && num_q_heads % kv_rep == 0, "attention_prefill: bad head shape");
+    detail::require(head_dim > 0 && head_dim <= detail::kAttnMaxD && head_dim % 16 == 0,
+                    "attention_prefill supports head_dim in {16,32,48,64}");
+    const int kvh = num_q_heads / kv_rep;
+    detail::PrefillSplitPlan p;
+    switch (head_dim / 16) {
+    case 1: p = detail::prefill_split_need<1>(T, S, q_offset, kv_rep, kvh, thr); break;
+    case 2: p = detail::prefill_split_need<2>(T, S, q_offset, kv_rep, kvh, thr); break;
+    case 3: p = detail::prefill_split_need<3>(T, S, q_offset, kv_rep, kvh, thr); break;
+    default: p = detail::prefill_split_need<4>(T, S, q_offset, kv_rep, kvh, thr); break;
+    }
+    *rec_floats = p.rec_floats;
+    *counter_ints = p.counter_ints;
+}
+
+// Workspace form of attention_prefill, same results to rounding: the query-tile groups with the
+// longest K/V ranges run as two workgroups over the halves of the range, merged by the one that
+// finishes last, so no CU ends the grid running one long causal range alone. `rec` (rec_floats) needs no
+// initialisation; `counters` (counter_ints) must be zero before the first call, and every call
+// leaves them at zero. Calls that share a workspace must not overlap. When the memory holds less
+// than attention_prefill_workspace_size asks, fewer groups split (none: the plain kernel).
+inline void attention_prefill_ws(const float *q_heads, const float *kcache, const float *vcache, float *out, int T,
+                                 int S, int q_offset, int num_q_heads, int kv_rep, int head_dim, int cap, float *rec,
+                                 int64_t rec_floats, int *counters, int64_t counter_ints, int thr = -1,
+                                 hipStream_t stream = nullptr) {
+    detail::require(T > 0 && S >= T && q_offset == S - T, "attention_prefill: bad shape/offset");
+    detail::require(num_q_heads > 0 && kv_rep > 0 && num_q_heads % kv_rep == 0, "attention_prefill: bad head shape");
+    detail::require(head_dim > 0 && head_dim <= detail::kAttnMaxD && head_dim % 16 == 0,
+                    "attention_prefill supports head_dim in {16,32,48,64}");
+    detail::require(cap >= S, "attention_prefill: length exceeds cache capacity");
+    detail::require(q_heads && kcache && vcache && out, "attention_prefill requires non-null pointers");
+    detail::require(rec_floats >= 0 && counter_ints >= 0 && (rec || rec_floats == 0) && (counters || counter_ints == 0),
+                    "attention_prefill_ws: bad workspace");
+    const float scale = 1.f / std::sqrt(static_cast<float>(head_dim));
+    const int kvh = num_q_heads / kv_rep;
+    const detail::PrefillWorkspaceArgs ws{rec, rec_floats, counters, counter_ints, thr};
+    switch (head_dim / 16) {
+    case 1: detail::attention_prefill_dispatch<1>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, &ws); break;
+    case 2: detail::attention_prefill_dispatch<2>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, &ws); break;
+    case 3: detail::attention_prefill_dispatch<3>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, &ws); break;
+    default: detail::attention_prefill_dispatch<4>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, &ws); break;
     }
 }
 

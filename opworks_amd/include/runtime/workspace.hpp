@@ -6,8 +6,9 @@
 // reference keep its name (tokens, hidden, normed, q_heads, attn_heads,
 // attn_out, logits); the others serve this build's fused kernels: the fused
 // [q;k;v] projection output, the SwiGLU product, split-K partial tiles, the
-// bf16 copy of the gate/up GEMM input (bf16-weight models), the
-// one-row buffers of the decode step, the decode attention's chunk records
+// bf16 copy of the gate/up GEMM input (bf16-weight models), the prefill
+// attention's split records and counters, the one-row buffers of the decode
+// step, the decode attention's chunk records
 // and arrival counters, the LM head's per-workgroup argmax records, the
 // device step state and the tokens a chained greedy decode produces.
 
@@ -27,6 +28,8 @@ struct WorkspaceSizes {
     int state_ints = 0;        // device step state
     int argmax_groups = 0;     // workgroups of the records' reduction
     int attn_counter_ints = 0; // decode attention arrival counters (one cache line per kv head)
+    int64_t prefill_split_floats = 0; // prefill attention: records of the split query-tile groups
+    int64_t prefill_split_ints = 0;   // and their arrival counters
     bool bf16_inputs = false;  // bf16-weight model: a bf16 copy of each prefill projection's input
 };
 
@@ -42,6 +45,8 @@ struct Workspace {
     TypedDeviceBuffer<float> act;        // [T, I] silu(gate) * up
     TypedDeviceBuffer<float> splitk;     // split-K partial tiles
     TypedDeviceBuffer<bf16> x_bf16;      // [T, max(H, I, qh D)] projection input rounded to bf16 (bf16-weight models)
+    TypedDeviceBuffer<float> attn_split;          // prefill attention: records of split query-tile groups
+    TypedDeviceBuffer<int32_t> attn_split_counters; // their arrivals, zero between launches
     // decode step: one row
     TypedDeviceBuffer<float> step_hidden;   // [H] residual stream
     TypedDeviceBuffer<float> step_q;        // [qh D] post-RoPE query
@@ -75,6 +80,10 @@ struct Workspace {
             splitk = TypedDeviceBuffer<float>(s.splitk_floats);
             if (s.bf16_inputs)
                 x_bf16 = TypedDeviceBuffer<bf16>(T * std::max(std::max(H, I), qw));
+            if (s.prefill_split_floats > 0 && s.prefill_split_ints > 0) {
+                attn_split = TypedDeviceBuffer<float>(s.prefill_split_floats);
+                attn_split_counters = TypedDeviceBuffer<int32_t>(s.prefill_split_ints);
+            }
         }
         step_hidden = TypedDeviceBuffer<float>(H);
         step_q = TypedDeviceBuffer<float>(qw);
