@@ -28,6 +28,9 @@
 // keys) at half the MFMA work of a 32-query tile and give four resident
 // workgroups per CU; tiles are dispatched heaviest first in alternating passes
 // (prefill_tile_of_rank) so each CU's share of KV tiles is about equal.
+// Two-tile grids (long prompts) run the same products on bf16 MFMAs with every
+// operand split into three bf16 parts ("bf16x6", fp32 accuracy): K and V are
+// split once when staged, Q once per workgroup, P once per tile.
 //
 // ---- decode (split-KV) ---------------------------------------------------
 // One workgroup = one kv head x one chunk of kAttnChunk keys: the chunk's K/V
@@ -93,15 +96,68 @@ template <typename Combine> __device__ __forceinline__ float column_combine(floa
 // adjacent query tiles per workgroup, one wave per (tile, head): with 2 every
 // staged K/V tile feeds twice as many MFMA chains (used when the grid still
 // fills every CU's four workgroup slots).
-template <int kDT, int kWaves, int kTiles> struct PrefillShape {
+template <int kDT, int kWaves, int kTiles, bool kX6 = false> struct PrefillShape {
     static constexpr int kD = 16 * kDT;                        // head_dim
     static constexpr int kLd = kD + 4;                         // LDS row stride of K and V (floats)
-    static constexpr int kLdsFloats = 4 * kAttnKTile * kLd;    // K and V, double buffered
     static constexpr int kThreads = kTiles * kWaves * kWaveSize;
     static constexpr int kChunks = kAttnKTile * kD / 4;        // 16-byte chunks per K (or V) tile
     static constexpr int kPerThread = (kChunks + kThreads - 1) / kThreads;
     static constexpr int kQ = kD / 4;                          // Q values per lane = QK^T MFMA steps per block
+    // kX6 stage: K as three bf16 parts [part][key][kRowK] and V transposed as three parts
+    // [part][dim][kRowV], each row padded by 16 bytes
+    static constexpr int kRowK = kD + 8, kRowV = kAttnKTile + 8;              // bf16 elements
+    static constexpr int kStageX6 = 3 * kAttnKTile * kRowK + 3 * kD * kRowV;  // bf16 elements per stage
+    static constexpr int kLdsBytes = kX6 ? 2 * 2 * kStageX6 : 4 * 4 * kAttnKTile * kLd; // double buffered
 };
+
+// ---- fp32 products on bf16 MFMAs ("bf16x6") --------------------------------
+// An fp32 value splits exactly into three bf16 parts, x = x0 + x1 + x2 (each round to nearest
+// of the remaining residual; 3 x 8 significand bits cover fp32's 24). A product keeps the six
+// terms with i + j <= 2, x_i y_j, each exact in fp32, accumulated by the MFMA in fp32; the
+// dropped terms are below 2^-24 of |x y|. Dot products then carry fp32's error (checked in
+// float64 against fp32 sums of length 64: the same worst case, 6.7e-8 of sum |x y|), at 16
+// cycles per 16x16x32 bf16 MFMA against 32 per 16x16x4 fp32 one: per 16x16x64 block, 12 x 16
+// against 16 x 32 cycles.
+using bf16x8v = __bf16 __attribute__((ext_vector_type(8)));
+using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+
+using bf16x2v = __bf16 __attribute__((ext_vector_type(2)));
+
+// (a, b) -> packed bf16 words, a in the low half, rounded to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+    const bf16x2v v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+    return __builtin_bit_cast(uint32_t, v);
+}
+// (a, b) -> three packed words w0, w1, w2 with a == lo(w0) + lo(w1) + lo(w2), b likewise in the
+// high halves; each residual is exact in fp32
+__device__ __forceinline__ void split3x2(float a, float b, uint32_t &w0, uint32_t &w1, uint32_t &w2) {
+    w0 = cvt_pk_bf16(a, b);
+    a -= __uint_as_float(w0 << 16);
+    b -= __uint_as_float(w0 & 0xffff0000u);
+    w1 = cvt_pk_bf16(a, b);
+    a -= __uint_as_float(w1 << 16);
+    b -= __uint_as_float(w1 & 0xffff0000u);
+    w2 = cvt_pk_bf16(a, b);
+}
+// eight floats -> their three bf16x8 parts
+__device__ __forceinline__ void split3x8(const float (&x)[8], bf16x8v (&part)[3]) {
+    uint32_t w[3][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        split3x2(x[2 * j], x[2 * j + 1], w[0][j], w[1][j], w[2][j]);
+#pragma unroll
+    for (int p = 0; p < 3; ++p)
+        part[p] = __builtin_bit_cast(bf16x8v, u32x4{w[p][0], w[p][1], w[p][2], w[p][3]});
+}
+// acc += term `term` of a b with both operands as three parts; terms 0..5 in turn add the six
+// products, smallest first: a2 b0, a1 b1, a0 b2, a1 b0, a0 b1, a0 b0
+__device__ __forceinline__ f32x4 mfma_x6_term(int term, const bf16x8v (&a)[3], const bf16x8v (&b)[3], f32x4 acc) {
+    constexpr int ia[6] = {2, 1, 0, 1, 0, 0}, ib[6] = {0, 1, 2, 0, 1, 0};
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ia[term]], b[ib[term]], acc, 0, 0, 0);
+}
+// Key slot of V^T rows: lane group g's eight keys of a 32-key tile (16 (j / 4) + 4 g + j % 4,
+// the keys its S^T registers hold) sit at slots 8 g + j, so one 16-byte read fetches them.
+__device__ __forceinline__ int x6_key_slot(int key) { return 8 * ((key % 16) / 4) + 4 * (key / 16) + key % 4; }
 
 // Dispatch order of query tiles. Work per tile grows with its index (causal),
 // and the grid is the query tiles x kv heads (x head slices). Ranks go out in
@@ -198,16 +254,19 @@ struct PrefillSplit {
 // amdgpu_waves_per_eu: with four or more waves per workgroup the register budget is 128
 // (four resident waves per SIMD, as many as the LDS allows); the bound also makes the
 // compiler keep the MFMA accumulators in VGPRs rather than AGPRs. kSplit: the workspace form
-// (units from prefill_unit_of_rank, halves merged through `sp`).
-template <int kDT, int kWaves, int kTiles, bool kSplit = false>
+// (units from prefill_unit_of_rank, halves merged through `sp`). kX6: QK^T and P V on bf16
+// MFMAs with every operand in three parts (the bf16x6 products above; head_dim 32 or 64).
+template <int kDT, int kWaves, int kTiles, bool kSplit = false, bool kX6 = false>
 __global__ __launch_bounds__(kTiles *kWaves *kWaveSize)
 __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) void attention_prefill_kernel(
     const float *__restrict__ q_heads, const float *__restrict__ kcache, const float *__restrict__ vcache,
     float *__restrict__ out, int T, int S, int q_offset, int kv_rep, int num_kv_heads, int cap, float qscale,
     int pass_width, PrefillSplit sp) {
-    using Shape = PrefillShape<kDT, kWaves, kTiles>;
+    using Shape = PrefillShape<kDT, kWaves, kTiles, kX6>;
     constexpr int D = Shape::kD, kLd = Shape::kLd, kQ = Shape::kQ;
+    static_assert(!kX6 || kDT % 2 == 0, "the bf16x6 path needs head_dim 32 or 64");
     extern __shared__ __attribute__((aligned(16))) float lds[];
+    uint16_t *const lds16 = reinterpret_cast<uint16_t *>(lds);
 
     const int slices = (kv_rep + kWaves - 1) / kWaves; // workgroups per GQA group
     const int per_tile = num_kv_heads * slices;
@@ -251,8 +310,21 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
 
     // Q^T operand: lane (l16, g) keeps Q[q][kQ*g + s] * scale * log2(e), s < kQ, so the
     // scores come out in the base-2 exponent domain. Rows past T read row T-1 and are not stored.
-    float qreg[kQ];
-    {
+    // kX6: lane (l16, g) keeps the three parts of Q[q][32 c + 8 g + j], j < 8, as the B operand of
+    // step c of the 16x16x32 products.
+    float qreg[kX6 ? 1 : kQ];
+    bf16x8v qx[kX6 ? kDT / 2 : 1][3];
+    if constexpr (kX6) {
+        const float *qrow = q_heads + (int64_t(h) * T + (q < T ? q : T - 1)) * D + 8 * g;
+#pragma unroll
+        for (int c = 0; c < kDT / 2; ++c) {
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(qrow + 32 * c);
+            const f32x4 b = *reinterpret_cast<const f32x4 *>(qrow + 32 * c + 4);
+            const float v[8] = {a[0] * qscale, a[1] * qscale, a[2] * qscale, a[3] * qscale,
+                                b[0] * qscale, b[1] * qscale, b[2] * qscale, b[3] * qscale};
+            split3x8(v, qx[c]);
+        }
+    } else {
         const float *qrow = q_heads + (int64_t(h) * T + (q < T ? q : T - 1)) * D + kQ * g;
 #pragma unroll
         for (int c = 0; c < kQ / 4; ++c) {
@@ -292,8 +364,6 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
         }
     };
     auto commit = [&](int buf, int kt) {
-        float *Ks = lds + buf * kStage;
-        float *Vs = Ks + kAttnKTile * kLd;
 #pragma unroll
         for (int i = 0; i < Shape::kPerThread; ++i) {
             const int c = threadIdx.x + i * Shape::kThreads;
@@ -305,9 +375,36 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
                 vv[j] = live ? vst[i][j] : 0.f;
             }
             if (Shape::kChunks % Shape::kThreads == 0 || c < Shape::kChunks) {
-                const int off = (c / kChunksPerRow) * kLd + (c % kChunksPerRow) * 4;
-                *reinterpret_cast<f32x4 *>(Ks + off) = kv;
-                *reinterpret_cast<f32x4 *>(Vs + off) = vv;
+                const int row = c / kChunksPerRow, d = (c % kChunksPerRow) * 4;
+                if constexpr (kX6) {
+                    // K parts row-major; V parts transposed, keys at their x6_key_slot
+                    uint16_t *Kx = lds16 + buf * Shape::kStageX6;
+                    uint16_t *Vx = Kx + 3 * kAttnKTile * Shape::kRowK;
+                    uint32_t kw[2][3], vw[2][3]; // [dim pair][part]
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        split3x2(kv[2 * j], kv[2 * j + 1], kw[j][0], kw[j][1], kw[j][2]);
+                        split3x2(vv[2 * j], vv[2 * j + 1], vw[j][0], vw[j][1], vw[j][2]);
+                    }
+                    const int slot = x6_key_slot(row);
+#pragma unroll
+                    for (int pp = 0; pp < 3; ++pp) {
+                        *reinterpret_cast<uint2 *>(Kx + (pp * kAttnKTile + row) * Shape::kRowK + d) =
+                            make_uint2(kw[0][pp], kw[1][pp]);
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            uint16_t *vcol = Vx + (pp * D + d + 2 * j) * Shape::kRowV + slot;
+                            vcol[0] = static_cast<uint16_t>(vw[j][pp]);
+                            vcol[Shape::kRowV] = static_cast<uint16_t>(vw[j][pp] >> 16);
+                        }
+                    }
+                } else {
+                    float *Ks = lds + buf * kStage;
+                    float *Vs = Ks + kAttnKTile * kLd;
+                    const int off = row * kLd + d;
+                    *reinterpret_cast<f32x4 *>(Ks + off) = kv;
+                    *reinterpret_cast<f32x4 *>(Vs + off) = vv;
+                }
             }
         }
     };
@@ -327,36 +424,61 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
         __builtin_amdgcn_sched_barrier(0); // keep the loads at the top
         const float *Ks = lds + buf * kStage;
         const float *Vs = Ks + kAttnKTile * kLd;
+        const uint16_t *Kx = lds16 + buf * Shape::kStageX6;
+        const uint16_t *Vx = Kx + 3 * kAttnKTile * Shape::kRowK;
 
         if (kt < my_ntiles) { // wave-uniform: the group's shorter tile skips its last K/V tile
-            // Operands first: the K fragments of both 16-key blocks and the V^T operands of the
-            // P V chain, so one LDS latency covers the tile.
-            f32x4 kf[2][kQ / 4];
-#pragma unroll
-            for (int u = 0; u < 2; ++u)
-#pragma unroll
-                for (int c = 0; c < kQ / 4; ++c)
-                    kf[u][c] = *reinterpret_cast<const f32x4 *>(Ks + (16 * u + l16) * kLd + kQ * g + 4 * c);
-            float vf[2][4][kDT];
-#pragma unroll
-            for (int u = 0; u < 2; ++u)
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-#pragma unroll
-                    for (int t = 0; t < kDT; ++t)
-                        vf[u][s][t] = Vs[(16 * u + 4 * g + s) * kLd + 16 * t + l16];
-
-            // S^T[key][q] = sum_d K[key][d] Q[q][d] for the two 16-key blocks u; at step s lane
-            // group g supplies reduction index kQ*g + s to both operands, and sacc[u][r] is key
-            // 16u + 4g + r. The blocks' chains alternate so consecutive MFMAs are independent.
             f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+            float vf[kX6 ? 1 : 2][4][kDT];
+            if constexpr (kX6) {
+                // S^T blocks on 16x16x32 products: lane (l16, g) supplies K[16u + l16][32c + 8g + j]
+                // (A) and Q[q][32c + 8g + j] (B); sacc[u][r] is again key 16u + 4g + r.
 #pragma unroll
-            for (int c = 0; c < kQ / 4; ++c)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int c = 0; c < kDT / 2; ++c) {
+                    bf16x8v kf[2][3];
 #pragma unroll
                     for (int u = 0; u < 2; ++u)
-                        sacc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[u][c][j], qreg[4 * c + j], sacc[u], 0, 0, 0);
+#pragma unroll
+                        for (int pp = 0; pp < 3; ++pp)
+                            kf[u][pp] = __builtin_bit_cast(
+                                bf16x8v, *reinterpret_cast<const u32x4 *>(
+                                             Kx + (pp * kAttnKTile + 16 * u + l16) * Shape::kRowK + 32 * c + 8 * g));
+                    // the two blocks' chains alternate, so consecutive MFMAs are independent
+#pragma unroll
+                    for (int term = 0; term < 6; ++term)
+#pragma unroll
+                        for (int u = 0; u < 2; ++u)
+                            sacc[u] = mfma_x6_term(term, kf[u], qx[c], sacc[u]);
+                }
+            } else {
+                // Operands first: the K fragments of both 16-key blocks and the V^T operands of the
+                // P V chain, so one LDS latency covers the tile.
+                f32x4 kf[2][kQ / 4];
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int c = 0; c < kQ / 4; ++c)
+                        kf[u][c] = *reinterpret_cast<const f32x4 *>(Ks + (16 * u + l16) * kLd + kQ * g + 4 * c);
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int t = 0; t < kDT; ++t)
+                            vf[u][s][t] = Vs[(16 * u + 4 * g + s) * kLd + 16 * t + l16];
+
+                // S^T[key][q] = sum_d K[key][d] Q[q][d] for the two 16-key blocks u; at step s lane
+                // group g supplies reduction index kQ*g + s to both operands, and sacc[u][r] is key
+                // 16u + 4g + r. The blocks' chains alternate so consecutive MFMAs are independent.
+#pragma unroll
+                for (int c = 0; c < kQ / 4; ++c)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int u = 0; u < 2; ++u)
+                            sacc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[u][c][j], qreg[4 * c + j], sacc[u], 0,
+                                                                           0, 0);
+            }
 
             // Causal mask, only on tiles that reach past the tile's first query position (a
             // wave-uniform branch: the mask's VALU work sits on the wave's critical path).
@@ -394,15 +516,41 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     oacc[t][r] *= corr;
-            // O^T[d][q] += sum_key V[key][d] P^T[key][q]: at step s of block u lane group g
-            // supplies key 16u + 4g + s, which is its own S^T register sacc[u][s].
+            if constexpr (kX6) {
+                // O^T[d][q] += V^T P^T over the tile's 32 keys in one 16x16x32 product per head-dim
+                // tile: lane (l16, g) supplies slots 8g + j, i.e. keys 16 (j / 4) + 4g + j % 4, whose
+                // probabilities are its own sacc[j / 4][j % 4].
+                const float pv[8] = {sacc[0][0], sacc[0][1], sacc[0][2], sacc[0][3],
+                                     sacc[1][0], sacc[1][1], sacc[1][2], sacc[1][3]};
+                bf16x8v px[3];
+                split3x8(pv, px);
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+                for (int t0 = 0; t0 < kDT; t0 += 2) {
+                    bf16x8v vx[2][3];
 #pragma unroll
-                for (int s = 0; s < 4; ++s)
+                    for (int t = 0; t < 2; ++t)
 #pragma unroll
-                    for (int t = 0; t < kDT; ++t)
-                        oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[u][s][t], sacc[u][s], oacc[t], 0, 0, 0);
+                        for (int pp = 0; pp < 3; ++pp)
+                            vx[t][pp] = __builtin_bit_cast(
+                                bf16x8v, *reinterpret_cast<const u32x4 *>(
+                                             Vx + (pp * D + 16 * (t0 + t) + l16) * Shape::kRowV + 8 * g));
+#pragma unroll
+                    for (int term = 0; term < 6; ++term)
+#pragma unroll
+                        for (int t = 0; t < 2; ++t)
+                            oacc[t0 + t] = mfma_x6_term(term, vx[t], px, oacc[t0 + t]);
+                }
+            } else {
+                // O^T[d][q] += sum_key V[key][d] P^T[key][q]: at step s of block u lane group g
+                // supplies key 16u + 4g + s, which is its own S^T register sacc[u][s].
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+#pragma unroll
+                    for (int s = 0; s < 4; ++s)
+#pragma unroll
+                        for (int t = 0; t < kDT; ++t)
+                            oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[u][s][t], sacc[u][s], oacc[t], 0, 0, 0);
+            }
         }
         // Stage the next tile into the other buffer (last read before the previous barrier);
         // the fence keeps the staging, which waits for the loads, at the end.
@@ -535,11 +683,11 @@ inline PrefillSplitPlan prefill_split_plan(int T, int S, int q_offset, int kv_re
     }
 }
 
-template <int kDT, int kWaves, int kTiles>
+template <int kDT, int kWaves, int kTiles, bool kX6>
 inline void attention_prefill_launch(const float *q, const float *k, const float *v, float *out, int T, int S,
                                      int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream,
                                      const PrefillWorkspaceArgs *ws) {
-    using Shape = PrefillShape<kDT, kWaves, kTiles>;
+    using Shape = PrefillShape<kDT, kWaves, kTiles, kX6>;
     const int slices = (kv_rep + kWaves - 1) / kWaves;
     const int per_tile = kvh * slices;
     const int64_t ngroups = blocks_for64(blocks_for64(T, kAttnQTile), kTiles);
@@ -550,15 +698,14 @@ inline void attention_prefill_launch(const float *q, const float *k, const float
                                                                            ws->rec_floats, ws->counter_ints);
         if (p.nsplit > 0) {
             require((ngroups + p.nsplit) * per_tile <= INT32_MAX, "attention_prefill: grid too large");
-            launch_async_lds(stream, sizeof(float) * Shape::kLdsFloats,
-                             attention_prefill_kernel<kDT, kWaves, kTiles, true>,
+            launch_async_lds(stream, Shape::kLdsBytes, attention_prefill_kernel<kDT, kWaves, kTiles, true, kX6>,
                              static_cast<int>((ngroups + p.nsplit) * per_tile), Shape::kThreads, q, k, v, out, T, S,
                              q_offset, kv_rep, kvh, cap, scale * kLog2e, pass_width,
                              PrefillSplit{ws->rec, ws->counters, p.thr, p.alternate});
             return;
         }
     }
-    launch_async_lds(stream, sizeof(float) * Shape::kLdsFloats, attention_prefill_kernel<kDT, kWaves, kTiles>,
+    launch_async_lds(stream, Shape::kLdsBytes, attention_prefill_kernel<kDT, kWaves, kTiles, false, kX6>,
                      static_cast<int>(ngroups * per_tile), Shape::kThreads, q, k, v, out, T, S, q_offset, kv_rep, kvh,
                      cap, scale * kLog2e, pass_width, PrefillSplit{nullptr, nullptr, 0, 0});
 }
@@ -575,10 +722,18 @@ template <int kDT, int kWaves>
 inline void attention_prefill_tiles(const float *q, const float *k, const float *v, float *out, int T, int S,
                                     int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream,
                                     const PrefillWorkspaceArgs *ws) {
-    if (prefill_two_tiles<kDT, kWaves>(T, kv_rep, kvh))
-        attention_prefill_launch<kDT, kWaves, 2>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
-    else
-        attention_prefill_launch<kDT, kWaves, 1>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
+    // Two-tile grids take the bf16x6 products when head_dim allows (32 or 64): config 4 154 ->
+    // 136 us, T = 4096 569 -> 443 us, T = 8192 2197 -> 1685 us (workspace form). One-tile grids
+    // keep the fp32 MFMA kernel: the three-part stages take 58 KB of LDS per workgroup, which
+    // halves their resident workgroups (T = 512: 20.8 us against 22.2).
+    if (prefill_two_tiles<kDT, kWaves>(T, kv_rep, kvh)) {
+        if constexpr (kDT % 2 == 0)
+            attention_prefill_launch<kDT, kWaves, 2, true>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
+        else
+            attention_prefill_launch<kDT, kWaves, 2, false>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
+    } else {
+        attention_prefill_launch<kDT, kWaves, 1, false>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
+    }
 }
 
 template <int kDT>
