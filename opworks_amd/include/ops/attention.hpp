@@ -158,6 +158,12 @@ __device__ __forceinline__ f32x4 mfma_x6_term(int term, const bf16x8v (&a)[3], c
 // Key slot of V^T rows: lane group g's eight keys of a 32-key tile (16 (j / 4) + 4 g + j % 4,
 // the keys its S^T registers hold) sit at slots 8 g + j, so one 16-byte read fetches them.
 __device__ __forceinline__ int x6_key_slot(int key) { return 8 * ((key % 16) / 4) + 4 * (key / 16) + key % 4; }
+// Physical V^T row of head-dim d: within each block of 8 rows, d's low three bits XOR the next
+// three. With 80-byte rows (row p starts at 4-bank group 5p mod 8 of 32 banks) the fragment reads
+// (dims 16t + 0..7 and 16t + 8..15, one 16-byte block) hit 8 distinct bank groups, and the
+// staging writes of one 16-lane group (dims 4 l + q, l < 16, one 8-byte piece each) hit each bank
+// pair at most twice, against eight times for rows in dim order.
+__device__ __forceinline__ int x6_vrow(int d) { return (d & ~7) | ((d ^ (d >> 3)) & 7); }
 
 // Dispatch order of query tiles. Work per tile grows with its index (causal),
 // and the grid is the query tiles x kv heads (x head slices). Ranks go out in
@@ -380,23 +386,59 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
                     // K parts row-major; V parts transposed, keys at their x6_key_slot
                     uint16_t *Kx = lds16 + buf * Shape::kStageX6;
                     uint16_t *Vx = Kx + 3 * kAttnKTile * Shape::kRowK;
-                    uint32_t kw[2][3], vw[2][3]; // [dim pair][part]
+                    uint32_t kw[2][3], vw[2][3]; // [value pair][part]
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
+                    for (int j = 0; j < 2; ++j)
                         split3x2(kv[2 * j], kv[2 * j + 1], kw[j][0], kw[j][1], kw[j][2]);
-                        split3x2(vv[2 * j], vv[2 * j + 1], vw[j][0], vw[j][1], vw[j][2]);
-                    }
-                    const int slot = x6_key_slot(row);
 #pragma unroll
-                    for (int pp = 0; pp < 3; ++pp) {
+                    for (int pp = 0; pp < 3; ++pp)
                         *reinterpret_cast<uint2 *>(Kx + (pp * kAttnKTile + row) * Shape::kRowK + d) =
                             make_uint2(kw[0][pp], kw[1][pp]);
+                    if constexpr (kChunksPerRow == 16) {
+                        // Lanes l16 + 16 q of a wave hold keys 4 w + q, dims 4 l16 .. + 3. A 4 x 4
+                        // transpose over (q, element) (permlane32_swap exchanges bit 1 of q with bit 1
+                        // of the element, permlane16_swap bit 0 with bit 0) leaves lane (l16, q) with
+                        // keys 4 w .. 4 w + 3 of dim 4 l16 + q: four adjacent V^T slots, one 8-byte
+                        // write per part.
+                        uint32_t e[4] = {__float_as_uint(vv[0]), __float_as_uint(vv[1]), __float_as_uint(vv[2]),
+                                         __float_as_uint(vv[3])};
 #pragma unroll
                         for (int j = 0; j < 2; ++j) {
-                            uint16_t *vcol = Vx + (pp * D + d + 2 * j) * Shape::kRowV + slot;
-                            vcol[0] = static_cast<uint16_t>(vw[j][pp]);
-                            vcol[Shape::kRowV] = static_cast<uint16_t>(vw[j][pp] >> 16);
+                            const auto sw = __builtin_amdgcn_permlane32_swap(e[j], e[2 + j], false, false);
+                            e[j] = sw[0];
+                            e[2 + j] = sw[1];
                         }
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            const auto sw = __builtin_amdgcn_permlane16_swap(e[2 * j], e[2 * j + 1], false, false);
+                            e[2 * j] = sw[0];
+                            e[2 * j + 1] = sw[1];
+                        }
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            split3x2(__uint_as_float(e[2 * j]), __uint_as_float(e[2 * j + 1]), vw[j][0], vw[j][1],
+                                     vw[j][2]);
+                        const int lane_q = (threadIdx.x % kWaveSize) / 16;
+                        const int key0 = row - lane_q, vd = d + lane_q; // keys key0 .. key0 + 3 of dim vd
+                        const int slot = x6_key_slot(key0);
+#pragma unroll
+                        for (int pp = 0; pp < 3; ++pp)
+                            *reinterpret_cast<uint2 *>(Vx + (pp * D + x6_vrow(vd)) * Shape::kRowV + slot) =
+                                make_uint2(vw[0][pp], vw[1][pp]);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            split3x2(vv[2 * j], vv[2 * j + 1], vw[j][0], vw[j][1], vw[j][2]);
+                        const int slot = x6_key_slot(row);
+#pragma unroll
+                        for (int pp = 0; pp < 3; ++pp)
+#pragma unroll
+                            for (int j = 0; j < 2; ++j) {
+                                Vx[(pp * D + x6_vrow(d + 2 * j)) * Shape::kRowV + slot] =
+                                    static_cast<uint16_t>(vw[j][pp]);
+                                Vx[(pp * D + x6_vrow(d + 2 * j + 1)) * Shape::kRowV + slot] =
+                                    static_cast<uint16_t>(vw[j][pp] >> 16);
+                            }
                     }
                 } else {
                     float *Ks = lds + buf * kStage;
@@ -533,7 +575,7 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
                         for (int pp = 0; pp < 3; ++pp)
                             vx[t][pp] = __builtin_bit_cast(
                                 bf16x8v, *reinterpret_cast<const u32x4 *>(
-                                             Vx + (pp * D + 16 * (t0 + t) + l16) * Shape::kRowV + 8 * g));
+                                             Vx + (pp * D + x6_vrow(16 * (t0 + t) + l16)) * Shape::kRowV + 8 * g));
 #pragma unroll
                     for (int term = 0; term < 6; ++term)
 #pragma unroll
