@@ -104,8 +104,9 @@ template <int kDT, int kWaves, int kTiles, bool kX6 = false> struct PrefillShape
     static constexpr int kPerThread = (kChunks + kThreads - 1) / kThreads;
     static constexpr int kQ = kD / 4;                          // Q values per lane = QK^T MFMA steps per block
     // kX6 stage: K as three bf16 parts [part][key][kRowK] and V transposed as three parts
-    // [part][dim][kRowV], each row padded by 16 bytes
-    static constexpr int kRowK = kD + 8, kRowV = kAttnKTile + 8;              // bf16 elements
+    // [part][dim][kRowV], rows unpadded with their 16-byte chunks XOR-swizzled (x6_k_chunk,
+    // x6_v_chunk)
+    static constexpr int kRowK = kD, kRowV = kAttnKTile;                     // bf16 elements
     static constexpr int kStageX6 = 3 * kAttnKTile * kRowK + 3 * kD * kRowV;  // bf16 elements per stage
     static constexpr int kLdsBytes = kX6 ? 2 * 2 * kStageX6 : 4 * 4 * kAttnKTile * kLd; // double buffered
 };
@@ -158,12 +159,21 @@ __device__ __forceinline__ f32x4 mfma_x6_term(int term, const bf16x8v (&a)[3], c
 // Key slot of V^T rows: lane group g's eight keys of a 32-key tile (16 (j / 4) + 4 g + j % 4,
 // the keys its S^T registers hold) sit at slots 8 g + j, so one 16-byte read fetches them.
 __device__ __forceinline__ int x6_key_slot(int key) { return 8 * ((key % 16) / 4) + 4 * (key / 16) + key % 4; }
-// Physical V^T row of head-dim d: within each block of 8 rows, d's low three bits XOR the next
-// three. With 80-byte rows (row p starts at 4-bank group 5p mod 8 of 32 banks) the fragment reads
-// (dims 16t + 0..7 and 16t + 8..15, one 16-byte block) hit 8 distinct bank groups, and the
-// staging writes of one 16-lane group (dims 4 l + q, l < 16, one 8-byte piece each) hit each bank
-// pair at most twice, against eight times for rows in dim order.
-__device__ __forceinline__ int x6_vrow(int d) { return (d & ~7) | ((d ^ (d >> 3)) & 7); }
+// LDS chunk swizzles of the three-part stages, for the fragment reads: lane (l16, g) reads the
+// 16-byte chunk of row l16 that g selects. Measured with the bank-conflict counter on an LDS
+// probe of these exact address patterns (SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE): rows padded
+// to 144 or 80 bytes ran 2-way, 128-byte rows with chunk c ^ 2 ((r / 4) mod 4) also 2-way, and the
+// two swizzles below conflict-free:
+//  * 128-byte rows (K at head_dim 64): chunk c of row r in c ^ ((r >> 1) & 7), the bf16 GEMM's;
+//  * 64-byte rows (V^T, and K at head_dim 32): chunk c of row r in c ^ 2 bit3(r) ^ bit4(r).
+// The staging writes (one 8-byte piece per lane) meet at most two-way conflicts.
+template <int kD> __device__ __forceinline__ int x6_k_chunk(int c, int r) {
+    if constexpr (kD == 64)
+        return c ^ ((r >> 1) & 7);
+    else
+        return c ^ (2 * ((r >> 3) & 1)) ^ ((r >> 4) & 1);
+}
+__device__ __forceinline__ int x6_v_chunk(int c, int d) { return c ^ (2 * ((d >> 3) & 1)) ^ ((d >> 4) & 1); }
 
 // Dispatch order of query tiles. Work per tile grows with its index (causal),
 // and the grid is the query tiles x kv heads (x head slices). Ranks go out in
@@ -390,9 +400,10 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
 #pragma unroll
                     for (int j = 0; j < 2; ++j)
                         split3x2(kv[2 * j], kv[2 * j + 1], kw[j][0], kw[j][1], kw[j][2]);
+                    const int kofs = row * Shape::kRowK + 8 * x6_k_chunk<D>(d / 8, row) + d % 8;
 #pragma unroll
                     for (int pp = 0; pp < 3; ++pp)
-                        *reinterpret_cast<uint2 *>(Kx + (pp * kAttnKTile + row) * Shape::kRowK + d) =
+                        *reinterpret_cast<uint2 *>(Kx + pp * kAttnKTile * Shape::kRowK + kofs) =
                             make_uint2(kw[0][pp], kw[1][pp]);
                     if constexpr (kChunksPerRow == 16) {
                         // Lanes l16 + 16 q of a wave hold keys 4 w + q, dims 4 l16 .. + 3. A 4 x 4
@@ -421,23 +432,23 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
                         const int lane_q = (threadIdx.x % kWaveSize) / 16;
                         const int key0 = row - lane_q, vd = d + lane_q; // keys key0 .. key0 + 3 of dim vd
                         const int slot = x6_key_slot(key0);
+                        const int vofs = vd * Shape::kRowV + 8 * x6_v_chunk(slot / 8, vd) + slot % 8;
 #pragma unroll
                         for (int pp = 0; pp < 3; ++pp)
-                            *reinterpret_cast<uint2 *>(Vx + (pp * D + x6_vrow(vd)) * Shape::kRowV + slot) =
+                            *reinterpret_cast<uint2 *>(Vx + pp * D * Shape::kRowV + vofs) =
                                 make_uint2(vw[0][pp], vw[1][pp]);
                     } else {
 #pragma unroll
                         for (int j = 0; j < 2; ++j)
                             split3x2(vv[2 * j], vv[2 * j + 1], vw[j][0], vw[j][1], vw[j][2]);
                         const int slot = x6_key_slot(row);
+                        auto vpos = [&](int dd) { return dd * Shape::kRowV + 8 * x6_v_chunk(slot / 8, dd) + slot % 8; };
 #pragma unroll
                         for (int pp = 0; pp < 3; ++pp)
 #pragma unroll
                             for (int j = 0; j < 2; ++j) {
-                                Vx[(pp * D + x6_vrow(d + 2 * j)) * Shape::kRowV + slot] =
-                                    static_cast<uint16_t>(vw[j][pp]);
-                                Vx[(pp * D + x6_vrow(d + 2 * j + 1)) * Shape::kRowV + slot] =
-                                    static_cast<uint16_t>(vw[j][pp] >> 16);
+                                Vx[pp * D * Shape::kRowV + vpos(d + 2 * j)] = static_cast<uint16_t>(vw[j][pp]);
+                                Vx[pp * D * Shape::kRowV + vpos(d + 2 * j + 1)] = static_cast<uint16_t>(vw[j][pp] >> 16);
                             }
                     }
                 } else {
@@ -484,7 +495,8 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
                         for (int pp = 0; pp < 3; ++pp)
                             kf[u][pp] = __builtin_bit_cast(
                                 bf16x8v, *reinterpret_cast<const u32x4 *>(
-                                             Kx + (pp * kAttnKTile + 16 * u + l16) * Shape::kRowK + 32 * c + 8 * g));
+                                             Kx + (pp * kAttnKTile + 16 * u + l16) * Shape::kRowK +
+                                             8 * x6_k_chunk<D>(4 * c + g, 16 * u + l16)));
                     // the two blocks' chains alternate, so consecutive MFMAs are independent
 #pragma unroll
                     for (int term = 0; term < 6; ++term)
@@ -575,7 +587,8 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
                         for (int pp = 0; pp < 3; ++pp)
                             vx[t][pp] = __builtin_bit_cast(
                                 bf16x8v, *reinterpret_cast<const u32x4 *>(
-                                             Vx + (pp * D + x6_vrow(16 * (t0 + t) + l16)) * Shape::kRowV + 8 * g));
+                                             Vx + (pp * D + 16 * (t0 + t) + l16) * Shape::kRowV +
+                                             8 * x6_v_chunk(g, 16 * (t0 + t) + l16)));
 #pragma unroll
                     for (int term = 0; term < 6; ++term)
 #pragma unroll
