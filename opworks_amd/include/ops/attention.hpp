@@ -28,9 +28,9 @@
 // keys) at half the MFMA work of a 32-query tile and give four resident
 // workgroups per CU; tiles are dispatched heaviest first in alternating passes
 // (prefill_tile_of_rank) so each CU's share of KV tiles is about equal.
-// Two-tile grids (long prompts) run the same products on bf16 MFMAs with every
-// operand split into three bf16 parts ("bf16x6", fp32 accuracy): K and V are
-// split once when staged, Q once per workgroup, P once per tile.
+// With head_dim 32 or 64 the same products run on bf16 MFMAs with every operand
+// split into three bf16 parts ("bf16x6", fp32 accuracy): K and V are split once
+// when staged, Q once per workgroup, P once per tile.
 //
 // ---- decode (split-KV) ---------------------------------------------------
 // One workgroup = one kv head x one chunk of kAttnChunk keys: the chunk's K/V
@@ -777,18 +777,13 @@ template <int kDT, int kWaves>
 inline void attention_prefill_tiles(const float *q, const float *k, const float *v, float *out, int T, int S,
                                     int q_offset, int kv_rep, int kvh, int cap, float scale, hipStream_t stream,
                                     const PrefillWorkspaceArgs *ws) {
-    // Two-tile grids take the bf16x6 products when head_dim allows (32 or 64): config 4 154 ->
-    // 136 us, T = 4096 569 -> 443 us, T = 8192 2197 -> 1685 us (workspace form). One-tile grids
-    // keep the fp32 MFMA kernel: the three-part stages take 58 KB of LDS per workgroup, which
-    // halves their resident workgroups (T = 512: 20.8 us against 22.2).
-    if (prefill_two_tiles<kDT, kWaves>(T, kv_rep, kvh)) {
-        if constexpr (kDT % 2 == 0)
-            attention_prefill_launch<kDT, kWaves, 2, true>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
-        else
-            attention_prefill_launch<kDT, kWaves, 2, false>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
-    } else {
-        attention_prefill_launch<kDT, kWaves, 1, false>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
-    }
+    // head_dim 32 or 64 takes the bf16x6 products (config 4 154 -> 109 us; T = 512 20.8 -> 18.0
+    // us and T = 4096 569 -> 377 us in the workspace form); 16 and 48 keep fp32 MFMAs.
+    constexpr bool kX6 = kDT % 2 == 0;
+    if (prefill_two_tiles<kDT, kWaves>(T, kv_rep, kvh))
+        attention_prefill_launch<kDT, kWaves, 2, kX6>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
+    else
+        attention_prefill_launch<kDT, kWaves, 1, kX6>(q, k, v, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, ws);
 }
 
 template <int kDT>
