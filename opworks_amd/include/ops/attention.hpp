@@ -886,18 +886,53 @@ __device__ __forceinline__ void decode_combine_head(const DecodeAttnArgs &a, int
     }
     // The first batch of output rows is loaded together with the (max, sum) pairs, so a
     // merge of up to kBatch chunks (1024 keys) costs one memory round trip (32 measured slower).
-    constexpr int kBatch = 16;
+    // Rows 16..63 (up to three more batches, long contexts) are issued right behind it, so they
+    // share that round trip instead of taking one each; past 64 rows, one batch per trip.
+    constexpr int kBatch = 16, kAhead = 3;
     float v[kBatch];
 #pragma unroll
     for (int j = 0; j < kBatch; ++j)
         v[j] = j < nchunks && lane < D ? record_load<kCoherent>(base + int64_t(j) * (D + 2) + 2 + lane) : 0.f;
+    // Uniform branches on the record count, and row and lane indices clamped (the extra values
+    // are multiplied by nothing), so no load sits under a per-lane condition.
+    float u[kAhead][kBatch];
+    const int dl = lane < D ? lane : D - 1;
+#pragma unroll
+    for (int b = 0; b < kAhead; ++b) {
+        if (nchunks > kBatch * (b + 1)) {
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const int c = kBatch * (b + 1) + j < nchunks ? kBatch * (b + 1) + j : nchunks - 1;
+                u[b][j] = record_load<kCoherent>(base + int64_t(c) * (D + 2) + 2 + dl);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j)
+                u[b][j] = 0.f;
+        }
+    }
     const float M = wave::max(fmaxf(m0, m1));
     const float w0 = lane < nchunks ? expf(m0 - M) : 0.f;
     const float w1 = lane + kWaveSize < nchunks ? expf(m1 - M) : 0.f;
     const float L = wave::sum(l0 * w0 + l1 * w1);
     float acc = 0.f;
-    for (int c0 = 0; c0 < nchunks; c0 += kBatch) {
-        if (c0 > 0) {
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+        const float wc = wave::readlane(w0, j);
+        acc = j < nchunks ? fmaf(v[j], wc, acc) : acc;
+    }
+#pragma unroll
+    for (int b = 0; b < kAhead; ++b)
+        if (nchunks > kBatch * (b + 1)) {
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                const int c = kBatch * (b + 1) + j;
+                const float wc = wave::readlane(w0, c);
+                acc = c < nchunks ? fmaf(u[b][j], wc, acc) : acc;
+            }
+        }
+    for (int c0 = kBatch * (kAhead + 1); c0 < nchunks; c0 += kBatch) {
+        {
 #pragma unroll
             for (int j = 0; j < kBatch; ++j)
                 v[j] = c0 + j < nchunks && lane < D
