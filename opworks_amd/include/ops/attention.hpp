@@ -697,15 +697,15 @@ struct PrefillSplitPlan {
     int64_t rec_floats = 0, counter_ints = 0;
 };
 
-// Automatic threshold, from a sweep of thresholds and orders at 32 q / 8 kv heads, D = 64:
+// Automatic threshold, from sweeps of thresholds and orders at 32 q / 8 kv heads, D = 64:
 //  * one-tile grids (at most 3 workgroups per CU): every group past 2 K/V tiles splits and the
-//    units go out in alternating passes, so a CU holds heavy and light halves (T = 512:
-//    25.9 -> 20.8 us; T = 1024: 49.6 -> 47.7 us);
-//  * two-tile grids of one round (T = 2048, config 4: 512 workgroups, two per CU) do not split:
+//    units go out in alternating passes, so a CU holds heavy and light halves (bf16x6 products:
+//    T = 512 24.3 -> 18.0 us, T = 1024 44.2 -> 41.4 us);
+//  * two-tile grids do not split. In one round (T = 2048, config 4: 512 workgroups, two per CU)
 //    the alternating passes already pair each heavy group with a light one on its CU, and every
-//    split form measured slower (155 against 162-175 us);
-//  * two-tile grids of several rounds split past 2 tiles in descending order, so the long halves
-//    start first (T = 4096: 603 -> 570 us).
+//    split form measured slower (fp32 products: 155 against 162-175 us). Over several rounds the
+//    split paid with fp32 products (T = 4096 603 -> 570 us) but not with bf16x6 ones (T = 4096
+//    381 against 387 us, T = 8192 1416 against 1431).
 // The threshold then rises until the records and counters fit the caller's memory.
 template <int kDT, int kWaves, int kTiles>
 inline PrefillSplitPlan prefill_split_plan(int T, int S, int q_offset, int kv_rep, int kvh, int thr_req,
@@ -720,10 +720,7 @@ inline PrefillSplitPlan prefill_split_plan(int T, int S, int q_offset, int kv_re
     if (thr_req >= 0) {
         p.thr = thr_req;
     } else {
-        // resident workgroups per CU: 4 waves per SIMD at kWaves >= 4 (128 registers), else 2
-        const int per_cu = std::max(1, (kWaves >= 4 ? 16 : 8) / (kTiles * kWaves));
-        const int64_t one_round = int64_t(cu_count()) * per_cu;
-        p.thr = kTiles == 2 && int64_t(ngroups) * per_tile <= one_round ? INT32_MAX : 2;
+        p.thr = kTiles == 2 ? INT32_MAX : 2;
     }
     const int64_t rec_per_group = int64_t(per_tile) * 2 * (2 + 4 * kDT) * Shape::kThreads;
     const int64_t ctr_per_group = int64_t(per_tile) * kAttnCounterStride;
