@@ -59,10 +59,20 @@ constexpr int kBfThreads = 512;
 // 256 x 256 tiles leave CUs idle or force deep split-K. The small shape exists on the direct
 // path only (bf16 A, 16-byte aligned operands).
 struct BfBig {
-    static constexpr int BM = 256, BN = 256, kThreads = 512, WM = 2, WN = 4;
+    static constexpr int BM = 256, BN = 256, kThreads = 512, WM = 2, WN = 4, kStages = 2;
 };
 struct BfSmall {
-    static constexpr int BM = 128, BN = 128, kThreads = 256, WM = 2, WN = 2;
+    static constexpr int BM = 128, BN = 128, kThreads = 256, WM = 2, WN = 2, kStages = 2;
+};
+// Tall: 128 x 256 outputs, 8 waves in 2 x 4 (64 x 64 each), three LDS stages (144 KB, one
+// workgroup per CU), so two K tiles are in flight while one is multiplied. For short-M products
+// from 256 rows (the prefill projections). At 512 rows, against two 128 x 128 workgroups per CU
+// on two stages (same outputs, bit for bit): gate/up 56-60 -> 43-45 us, down (8 splits) 28-33 ->
+// 25-26, qkv 16.0-16.2 -> 14.2-14.9, o_proj 13.9-14.3 -> 13.4-13.6. The third stage is what pays:
+// a 256 x 128 tile on two stages ran as slowly as the small tiles (57-59 us for gate/up), on three
+// 44-49 us.
+struct BfTall {
+    static constexpr int BM = 128, BN = 256, kThreads = 512, WM = 2, WN = 4, kStages = 3;
 };
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
@@ -84,8 +94,10 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_bf16_mfma_kernel(const T
     constexpr bool kDirect = kVec && !kF32A;
     constexpr int kBM = Shape::BM, kBN = Shape::BN, kT = Shape::kThreads;
     constexpr int kWTM = kBM / Shape::WM, kWTN = kBN / Shape::WN; // outputs per wave
-    static_assert(std::is_same_v<Shape, BfBig> || kDirect, "the small tile runs on the direct path only");
-    static_assert(kBM == kBN, "square workgroup tiles: both operands stage the same rows per thread");
+    static_assert(std::is_same_v<Shape, BfBig> || kDirect, "the small and tall tiles run on the direct path only");
+    static_assert(kBM == kBN || kDirect, "register staging: both operands stage the same rows per thread");
+    constexpr int kStages = Shape::kStages;
+    static_assert(kStages == 2 || kDirect, "register staging is double buffered");
     // LDS rows: a direct load writes 1 KB of consecutive bytes, so its rows are unpadded, with
     // chunk c of row r in slot c ^ ((r >> 1) & 7). The LDS serves 256 bytes a cycle, 16 lanes of
     // a 16-byte read, and the reads of 16 consecutive rows at one k then fall on 16 different
@@ -94,9 +106,10 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_bf16_mfma_kernel(const T
     // read offset a compile-time constant (the swizzle took the fp32-A kernel past 256 registers).
     constexpr int kRowE = kDirect ? BK : BK + 8;       // bf16 elements per LDS row
     constexpr int kCPR = BK / 8;                       // 16-byte chunks (8 k) per tile row
-    constexpr int kPer = kBM * kCPR / kT;              // chunks per thread per operand
+    constexpr int kPer = kBM * kCPR / kT;              // chunks per thread of A (and of B when square)
+    constexpr int kPerB = kBN * kCPR / kT;             // chunks per thread of B
     constexpr int kStage = (kBM + kBN) * kRowE;        // uint16 elements per stage
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * kStage];
+    __shared__ __attribute__((aligned(16))) uint16_t lds[kStages * kStage];
 
     const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
     int tm, tn;
@@ -116,7 +129,7 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_bf16_mfma_kernel(const T
         return row * kRowE + ((kDirect ? chunk ^ ((row >> 1) & 7) : chunk) << 3);
     };
 
-    // Register staging: chunk tid + kT * i of each operand tile (kBM rows x BK k),
+    // Register staging: chunk tid + kT * i of each operand tile (kBM or kBN rows x BK k),
     // row (tid + kT * i) / kCPR. The vector path loads unconditionally from clamped
     // addresses into raw registers (fp32 A is rounded to bf16 only when staged): a load under
     // a branch makes the compiler wait for every load in flight before the next one. Rows past
@@ -124,8 +137,9 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_bf16_mfma_kernel(const T
     // K tail is zeroed when staged.
     using AStage = std::conditional_t<kF32A, f32x4, u32x4>;
     constexpr int kAParts = kF32A ? 2 : 1;
+    constexpr int kPerMax = kPer > kPerB ? kPer : kPerB; // chunks i < kPer of A, i < kPerB of B
     AStage ra[kPer][kAParts];
-    u32x4 rb[kPer];
+    u32x4 rb[kPerB];
     auto chunk_row = [&](int i) { return (tid + kT * i) / kCPR; };
     auto chunk_k = [&](int i) { return ((tid + kT * i) % kCPR) * 8; };
     auto load_chunk_bf16 = [&](const uint16_t *src, int row, int rows_total, int k) -> u32x4 {
@@ -140,20 +154,20 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_bf16_mfma_kernel(const T
     auto global_load = [&](int kt, bool with_a, bool with_b) {
         const int k0 = kt * BK;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
+        for (int i = 0; i < kPerMax; ++i) {
             const int r = chunk_row(i), k = k0 + chunk_k(i);
             if constexpr (kVec) {
                 const int ar = m0 + r < M ? m0 + r : M - 1, br = n0 + r < N ? n0 + r : N - 1;
                 const int kc = k < K ? k : K - 8;
-                if (with_a) {
+                if (with_a && i < kPer) {
 #pragma unroll
                     for (int p = 0; p < kAParts; ++p)
                         ra[i][p] = *reinterpret_cast<const AStage *>(A + int64_t(ar) * K + kc + 4 * p);
                 }
-                if (with_b)
+                if (with_b && i < kPerB)
                     rb[i] = *reinterpret_cast<const u32x4 *>(W + int64_t(br) * K + kc);
             } else {
-                if (with_a) {
+                if (with_a && i < kPer) {
                     if constexpr (kF32A) {
 #pragma unroll
                         for (int p = 0; p < 2; ++p)
@@ -166,7 +180,7 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_bf16_mfma_kernel(const T
                         ra[i][0] = load_chunk_bf16(A, m0 + r, M, k);
                     }
                 }
-                if (with_b)
+                if (with_b && i < kPerB)
                     rb[i] = load_chunk_bf16(W, n0 + r, N, k);
             }
         }
@@ -176,14 +190,15 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_bf16_mfma_kernel(const T
         uint16_t *Bs = As + kBM * kRowE;
         const int k0 = kt * BK;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
+        for (int i = 0; i < kPerMax; ++i) {
             const int k = k0 + chunk_k(i);
-            u32x4 av, bv = rb[i];
+            const int ia = i < kPer ? i : 0, ib = i < kPerB ? i : 0; // in range; unused when i is past
+            u32x4 av, bv = rb[ib];
             if constexpr (kF32A)
-                av = u32x4{pack_bf16x2(ra[i][0][0], ra[i][0][1]), pack_bf16x2(ra[i][0][2], ra[i][0][3]),
-                           pack_bf16x2(ra[i][1][0], ra[i][1][1]), pack_bf16x2(ra[i][1][2], ra[i][1][3])};
+                av = u32x4{pack_bf16x2(ra[ia][0][0], ra[ia][0][1]), pack_bf16x2(ra[ia][0][2], ra[ia][0][3]),
+                           pack_bf16x2(ra[ia][1][0], ra[ia][1][1]), pack_bf16x2(ra[ia][1][2], ra[ia][1][3])};
             else
-                av = ra[i][0];
+                av = ra[ia][0];
             if (zero_tail) { // the partial last K tile only: k >= K contributes nothing
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -192,9 +207,9 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_bf16_mfma_kernel(const T
                 }
             }
             const int off = swz(chunk_row(i), chunk_k(i) / 8);
-            if (with_a)
+            if (with_a && i < kPer)
                 *reinterpret_cast<u32x4 *>(As + off) = av;
-            if (with_b)
+            if (with_b && i < kPerB)
                 *reinterpret_cast<u32x4 *>(Bs + off) = bv;
         }
     };
@@ -208,11 +223,35 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_bf16_mfma_kernel(const T
         uint16_t *As = lds + buf * kStage;
         uint16_t *Bs = As + kBM * kRowE;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
+        for (int i = 0; i < (kPer > kPerB ? kPer : kPerB); ++i) {
             const int block = 8 * wave + (kT / 8) * i, r = block + d_row;
             const int ar = m0 + r < M ? m0 + r : M - 1, br = n0 + r < N ? n0 + r : N - 1;
-            load_lds16(A + int64_t(ar) * K + k0, As + block * kRowE);
-            load_lds16(W + int64_t(br) * K + k0, Bs + block * kRowE);
+            if (i < kPer)
+                load_lds16(A + int64_t(ar) * K + k0, As + block * kRowE);
+            if (i < kPerB)
+                load_lds16(W + int64_t(br) * K + k0, Bs + block * kRowE);
+        }
+    };
+    // s_waitcnt operand for vmcnt(n), expcnt and lgkmcnt at their maxima (gfx9: vmcnt bits 3:0
+    // and 15:14): waits until at most n of the wave's vector memory accesses are outstanding.
+    constexpr int kLoadsPerStage = kPer + kPerB; // direct loads per thread per stage
+    constexpr int kInFlight = (kStages - 2) * kLoadsPerStage;
+    static_assert(kInFlight < 64, "vmcnt holds 6 bits");
+    constexpr int kWaitOlderStages = kWaitVmcnt0Only | (kInFlight & 15) | ((kInFlight >> 4) << 14);
+    // __syncthreads() waits for every outstanding direct load (the compiler's workgroup fence
+    // drains vmcnt), which would take the younger stages' loads out of flight. With more than two
+    // stages the loop syncs with a bare barrier instead, after this wave's older stages landed
+    // (vmcnt) and its LDS reads returned (lgkmcnt(0): no wave overwrites a stage another wave may
+    // still be reading). The sched_barrier fences keep the compiler from moving LDS accesses
+    // across it.
+    auto stage_sync = [] {
+        if constexpr (kStages == 2) {
+            __syncthreads();
+        } else {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(kWaitOlderStages & ~0x0F00); // the same vmcnt, lgkmcnt(0)
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -332,29 +371,38 @@ __global__ __launch_bounds__(Shape::kThreads) void gemm_bf16_mfma_kernel(const T
         // between. The idle stage was last read before the previous tile's barrier.
         // (4096^3, bf16 A, on one box: 123-126 us with a barrier at the end of each tile on
         // 32x32x16 tiles, 112-114 us with this barrier, 102.5-104 us on 16x16x32 tiles.)
-        direct_load(0, kt_begin);
-        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0Only);
-        __syncthreads();
+        // With kStages stages the loads run kStages - 1 tiles ahead: tile kt + kStages - 1 goes
+        // into the stage tile kt - 1 used, which no wave reads after the previous barrier, and
+        // the wait before each barrier leaves the younger tiles' loads (kInFlight) outstanding.
+        for (int s = 0; s + 1 < kStages; ++s)
+            direct_load(s, kt_begin + s < kt_full ? kt_begin + s : kt_full - 1);
+        __builtin_amdgcn_s_waitcnt(kWaitOlderStages);
+        stage_sync();
         read16(0, 0, 0);
         for (int kt = kt_begin; kt < kt_full; ++kt) {
-            const int buf = (kt - kt_begin) & 1;
+            const int j = kt - kt_begin;
+            const int buf = kStages == 2 ? (j & 1) : j % kStages;
+            const int nbuf = kStages == 2 ? (buf ^ 1) : (buf + 1 == kStages ? 0 : buf + 1);
+            const int lbuf = kStages == 2 ? (buf ^ 1) : (buf == 0 ? kStages - 1 : buf - 1);
             // past the last tile: a reload of a valid tile into the idle stage, never read (a
             // peeled last tile without it took the residual epilogue into spills)
-            const int next = kt + 1 < kt_full ? kt + 1 : kt;
-            direct_load(buf ^ 1, next);
+            const int next = kt + kStages - 1 < kt_full ? kt + kStages - 1 : kt_full - 1;
+            direct_load(lbuf, next);
             __builtin_amdgcn_sched_barrier(0); // the loads stay at the top, in flight during the MFMAs
             read16(buf, 1, 1);
             mfma16(0);
             interleave16();
             __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0Only); // this wave's loads of the next tile landed
-            __syncthreads();
+            __builtin_amdgcn_s_waitcnt(kWaitOlderStages); // this wave's loads of the next tile landed
+            stage_sync();
             __builtin_amdgcn_sched_barrier(0);
-            read16(buf ^ 1, 0, 0);
+            read16(nbuf, 0, 0);
             mfma16(1);
             interleave16();
             __builtin_amdgcn_sched_barrier(0);
         }
+        if constexpr (kInFlight > 0) // the reloads past the end land before the stages are reused
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0Only);
       }
     } else if (kt_begin < kt_full) {
         // Each K tile: the next tile's loads are issued first into registers, stored halfway
@@ -496,7 +544,8 @@ void gemm_bf16_launch(const TA *A, const uint16_t *W, const float *bias, float *
 }
 
 // Floats of split-K workspace any launch planned by splitk_factor(tiles, ., 256) needs (the
-// small-tile plans below stay within it: splits x tiles <= 512 tiles of a quarter the size).
+// small- and tall-tile plans below stay within it: splits x tiles <= 512 tiles of a quarter the
+// size, or <= 256 of half).
 constexpr int64_t kSplitKWorkspaceBf16 = int64_t(256) * kBfBM * kBfBN;
 
 // Split-K form of gemm_bf16_launch for store / residual outputs (see
@@ -518,12 +567,13 @@ void gemm_bf16_launch_splitk(const TA *A, const uint16_t *W, const float *bias, 
 }
 
 // bf16 A on the direct path (both operands straight into LDS), for any M: 256 x 256 tiles when
-// they fill the GPU's 256 CUs, else 128 x 128 tiles, and for store / residual outputs K split
-// across workgroups toward two per CU, at least 8 K tiles of 64 per split, the partial tiles
+// they fill the GPU's 256 CUs, else 128 x 256 three-stage tiles from 256 rows (one workgroup per
+// CU) and 128 x 128 tiles below (two per CU), and for store / residual outputs K split across
+// workgroups toward one round of the GPU, at least 8 K tiles of 64 per split, the partial tiles
 // summed in split order by splitk_reduce_kernel. At M = 512 (a 512-token prefill) the 256 x 256
 // tiles gave gate/up 128 workgroups and qkv, o_proj and down 8-way splits on 16-24 tiles.
 // `reduce` as in gemm_f32_launch_splitk: called as reduce(ws, splits) in place of the reduction
-// kernel when K is split (small tiles only). Returns true when it was.
+// kernel when K is split (small and tall tiles only). Returns true when it was.
 template <typename Epi, GemmStore kStore, typename Reduce = std::nullptr_t>
 bool gemm_bf16_launch_direct(const uint16_t *A, const uint16_t *W, const float *bias, float *C, int M, int N, int K,
                              Epi epi, float *ws, int64_t ws_floats, hipStream_t stream, Reduce reduce = nullptr) {
@@ -538,22 +588,29 @@ bool gemm_bf16_launch_direct(const uint16_t *A, const uint16_t *W, const float *
             gemm_bf16_launch_splitk<uint16_t, Epi, kStore>(A, W, bias, C, M, N, K, epi, ws, ws_floats, stream);
         return false;
     }
-    using S = BfSmall;
-    const int tiles = static_cast<int>(blocks_for64(M, S::BM) * blocks_for64(N, S::BN));
-    int splits = 1;
-    if constexpr (!kSwiglu) {
-        splits = splitk_factor(tiles, static_cast<int>(blocks_for64(K, 64)), 512);
-        if (N % 4 != 0 || !ws || int64_t(splits) * M * N > ws_floats || !aligned16(C) || (bias && !aligned16(bias)))
-            splits = 1;
-    }
-    if (splits == 1) {
-        launch_async(stream, gemm_bf16_mfma_kernel<uint16_t, true, Epi, kStore, S>, dim3(tiles, 1), S::kThreads, A, W,
-                     bias, C, M, N, K, epi);
+    // One workgroup per CU for the tall tiles, two for the small ones: split toward that many.
+    auto run = [&](auto shape, int target) {
+        using S = decltype(shape);
+        const int tiles = static_cast<int>(blocks_for64(M, S::BM) * blocks_for64(N, S::BN));
+        int splits = 1;
+        if constexpr (!kSwiglu) {
+            splits = splitk_factor(tiles, static_cast<int>(blocks_for64(K, 64)), target);
+            if (N % 4 != 0 || !ws || int64_t(splits) * M * N > ws_floats || !aligned16(C) ||
+                (bias && !aligned16(bias)))
+                splits = 1;
+        }
+        if (splits == 1)
+            launch_async(stream, gemm_bf16_mfma_kernel<uint16_t, true, Epi, kStore, S>, dim3(tiles, 1), S::kThreads,
+                         A, W, bias, C, M, N, K, epi);
+        else
+            launch_async(stream, gemm_bf16_mfma_kernel<uint16_t, true, IdentityEpilogue, GemmStore::partial, S>,
+                         dim3(tiles, splits), S::kThreads, A, W, static_cast<const float *>(nullptr), ws, M, N, K,
+                         IdentityEpilogue{});
+        return splits;
+    };
+    const int splits = M >= 256 ? run(BfTall{}, 256) : run(BfSmall{}, 512);
+    if (splits == 1)
         return false;
-    }
-    launch_async(stream, gemm_bf16_mfma_kernel<uint16_t, true, IdentityEpilogue, GemmStore::partial, S>,
-                 dim3(tiles, splits), S::kThreads, A, W, static_cast<const float *>(nullptr), ws, M, N, K,
-                 IdentityEpilogue{});
     if constexpr (!kSwiglu) {
         if constexpr (std::is_same_v<Reduce, std::nullptr_t>)
             launch_async(stream, splitk_reduce_kernel<Epi, kStore>, stream_grid(int64_t(M) * N / 4), 256, ws, splits,

@@ -31,7 +31,10 @@ def test_convert_bits_match_oracle(ow, orc):
 
 
 SHAPES = [(1, 8, 1), (16, 64, 64), (100, 200, 300), (256, 256, 256), (300, 2048, 520), (512, 1024, 3072),
-          (257, 40, 513), (3, 4104, 7)]  # a full K tile + an 8-wide tail; tiles one row/column past 256
+          (257, 40, 513), (3, 4104, 7),  # a full K tile + an 8-wide tail; tiles one row/column past 256
+          # the three-stage 128 x 256 tiles (from 256 rows) with 1, 2 and 3 full K tiles, tails and
+          # partial row and column tiles
+          (260, 72, 300), (512, 128, 512), (300, 200, 600)]
 
 
 @pytest.mark.parametrize("rows,in_f,out_f", SHAPES)
