@@ -102,6 +102,17 @@ __device__ __forceinline__ int block_lane_flat() {
 }
 __device__ __forceinline__ int block_lanes_flat() { return static_cast<int>(blockDim.x * blockDim.y * blockDim.z); }
 
+// Workgroup barrier that orders LDS accesses only. __syncthreads() fences every address space,
+// which compiles to s_waitcnt vmcnt(0) lgkmcnt(0): each wave waits for all of its outstanding
+// global loads before the barrier. With the fences restricted to LDS only lgkmcnt(0) is waited
+// for, so loads issued earlier (GEMV weights, K/V rows) stay in flight across the barrier. Use
+// it where the barrier protects LDS data only.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 inline bool launch_dims_positive(dim3 grid, dim3 block) {
     return grid.x != 0 && grid.y != 0 && grid.z != 0 && block.x != 0 && block.y != 0 && block.z != 0;
 }

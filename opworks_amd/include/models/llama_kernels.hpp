@@ -70,6 +70,12 @@ template <typename WT> constexpr int kRowScale = std::is_same_v<WT, bf16> ? 2 : 
 // H = 256 * kV. The input vector is staged once per workgroup: its loads are
 // issued first, then every weight pack of the wave, so with in-order vmcnt
 // accounting the RMS statistics are computed while the weights stream in.
+// That holds only while the loads are straight-line code: a load under a
+// branch (a per-lane bound, a wave that has no row) leaves the compiler
+// unable to count what is outstanding at the join, and it waits for every
+// load before the first use. So every load is issued, from a valid address
+// (the callers give inactive waves a valid row), the barriers order LDS only,
+// and the copy of x is stored after the dot products.
 // The (optionally RMS-normalised) vector goes to LDS and each wave reads its
 // kV packs from there. Waves with active == false still take part in the
 // barriers. xn = x * rsqrtf(mean(x^2) + eps) * gamma, ops::rms_norm's order.
@@ -102,21 +108,17 @@ __device__ __forceinline__ void block_gemv(const XT *__restrict__ x, const float
     f32x4 xv[kX], gv[kX];
 #pragma unroll
     for (int i = 0; i < kX; ++i) {
-        const int c = tid + kBlock * i;
-        if (c < kPacks) {
-            xv[i] = load_x4(x, c);
-            if (gamma)
-                gv[i] = g4[c];
-        }
+        const int c = tid + kBlock * i, cc = c < kPacks ? c : kPacks - 1;
+        xv[i] = load_x4(x, cc);
+        if (gamma) // uniform
+            gv[i] = g4[cc];
     }
     typename WPack<WT>::type w[kR][kP];
-    if (active) {
 #pragma unroll
-        for (int r = 0; r < kR; ++r)
+    for (int r = 0; r < kR; ++r)
 #pragma unroll
-            for (int u = 0; u < kP; ++u)
-                w[r][u] = load_wpack(W + int64_t(row[r]) * H, lane + kWaveSize * u);
-    }
+        for (int u = 0; u < kP; ++u)
+            w[r][u] = load_wpack(W + int64_t(row[r]) * H, lane + kWaveSize * u);
     __builtin_amdgcn_sched_barrier(0);
     float inv = 1.f;
     if (gamma) {
@@ -130,15 +132,13 @@ __device__ __forceinline__ void block_gemv(const XT *__restrict__ x, const float
         ss = wave::sum(ss);
         if (lane == 0)
             red[wave] = ss;
-        __syncthreads();
+        detail::lds_barrier(); // the weight loads stay in flight
         inv = rsqrtf(((red[0] + red[1]) + (red[2] + red[3])) / H + eps);
     }
 #pragma unroll
     for (int i = 0; i < kX; ++i) {
         const int c = tid + kBlock * i;
         if (c < kPacks) {
-            if (copy_x_to)
-                reinterpret_cast<f32x4 *>(copy_x_to)[c] = xv[i];
             f32x4 v = xv[i];
             if (gamma)
 #pragma unroll
@@ -147,21 +147,29 @@ __device__ __forceinline__ void block_gemv(const XT *__restrict__ x, const float
             *reinterpret_cast<f32x4 *>(&xs[4 * c]) = v;
         }
     }
-    __syncthreads();
-    if (!active)
-        return;
+    detail::lds_barrier(); // each dot product waits for its own weight pack only
+    if (active) {
 #pragma unroll
-    for (int r = 0; r < kR; ++r) {
-        float acc = 0.f;
+        for (int r = 0; r < kR; ++r) {
+            float acc = 0.f;
 #pragma unroll
-        for (int u = 0; u < kP; ++u) {
-            f32x4 xl[E / 4];
+            for (int u = 0; u < kP; ++u) {
+                f32x4 xl[E / 4];
 #pragma unroll
-            for (int q = 0; q < E / 4; ++q)
-                xl[q] = *reinterpret_cast<const f32x4 *>(&xs[E * (lane + kWaveSize * u) + 4 * q]);
-            acc = dot_wpack<WT>(w[r][u], xl, acc);
+                for (int q = 0; q < E / 4; ++q)
+                    xl[q] = *reinterpret_cast<const f32x4 *>(&xs[E * (lane + kWaveSize * u) + 4 * q]);
+                acc = dot_wpack<WT>(w[r][u], xl, acc);
+            }
+            y[r] = wave::sum(acc);
         }
-        y[r] = wave::sum(acc);
+    }
+    if (copy_x_to) { // uniform; after the dot products, so no store sits between the weight loads and their uses
+#pragma unroll
+        for (int i = 0; i < kX; ++i) {
+            const int c = tid + kBlock * i;
+            if (c < kPacks)
+                reinterpret_cast<f32x4 *>(copy_x_to)[c] = xv[i];
+        }
     }
 }
 

@@ -1027,17 +1027,32 @@ __device__ __forceinline__ bool decode_attention_chunk_rb(const DecodeAttnArgs &
     const f32x4 *vh = reinterpret_cast<const f32x4 *>(a.vcache + (int64_t(kvh) * a.cap + k0) * D);
     const f32x4 *q4 = reinterpret_cast<const f32x4 *>(a.q + int64_t(kvh) * rep * D);
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    // q, then K, then V: the scores wait for q and K only, and V keeps arriving through the
+    // scores and the softmax (their barriers order LDS only). Every load is issued, from a valid
+    // clamped address (the cache row len - 1, the last pack of a row, head 0 of the group), and
+    // what lies outside is zeroed afterwards: a load under a per-lane branch would make the
+    // compiler wait for all of them before the first score.
     f32x4 kv[kPer], vv[kPer], qv[kWaves];
+    const int dqc = dq_ok ? dq : P - 1;
+#pragma unroll
+    for (int h = 0; h < kWaves; ++h) {
+        const f32x4 x = q4[(h < rep ? h : 0) * P + dqc];
+        qv[h] = dq_ok && h < rep ? x : zero;
+    }
+    auto clamped = [&](int key) { return (k0 + key < len ? key : len - 1 - k0) * P + dqc; };
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
         const int key = row + kRowStep * i;
-        const bool ok = dq_ok && key < n;
-        kv[i] = ok ? kh[key * P + dq] : zero;
-        vv[i] = ok ? vh[key * P + dq] : zero;
+        const f32x4 x = kh[clamped(key)];
+        kv[i] = dq_ok && key < n ? x : zero;
     }
 #pragma unroll
-    for (int h = 0; h < kWaves; ++h)
-        qv[h] = dq_ok && h < rep ? q4[h * P + dq] : zero;
+    for (int i = 0; i < kPer; ++i) {
+        const int key = row + kRowStep * i;
+        const f32x4 x = vh[clamped(key)];
+        vv[i] = dq_ok && key < n ? x : zero;
+    }
+    __builtin_amdgcn_sched_barrier(0);
     __shared__ float Ss[kSub][kWaves][C];                        // scaled scores, [head][key]
     __shared__ __attribute__((aligned(16))) float Ps[kSub][C][kWaves]; // probabilities, [key][head]
     __shared__ __attribute__((aligned(16))) float Os[kSub][kWaves][16 * kOStride]; // per-wave P V partials
@@ -1075,7 +1090,7 @@ __device__ __forceinline__ bool decode_attention_chunk_rb(const DecodeAttnArgs &
         if (h < rep)
             Ss[sub][h][key] = key < n ? v[0] * a.scale : kNegInf;
     }
-    __syncthreads();
+    lds_barrier();
     // softmax of head `wave` over the chunk's keys (lane = key); an empty chunk leaves m = -inf
     const bool head_ok = wave < rep;
     const int h = kvh * rep + (head_ok ? wave : 0);
@@ -1090,7 +1105,7 @@ __device__ __forceinline__ bool decode_attention_chunk_rb(const DecodeAttnArgs &
         }
         Ps[sub][lane][wave] = pr;
     }
-    __syncthreads();
+    lds_barrier();
     // P V: this thread's slots for every head of the group
     float o[kOut];
 #pragma unroll
