@@ -229,47 +229,51 @@ def wl_layernorm(stream, steps, warmup):
 # from a process where this library's runtime already holds it.
 LIBRARY_REFERENCE_CHILD = r"""
 import json, sys, torch
-kind, n, calls, seed = sys.argv[1], int(sys.argv[2]), int(sys.argv[3]), int(sys.argv[4])
+kind, m, n, k, calls, seed, copies = sys.argv[1], *map(int, sys.argv[2:8])
 dev = torch.device("cuda", 0)
 g = torch.Generator(device=dev).manual_seed(seed)
-# kinds: f32 (A @ B), f32nk (X @ W^T), bf16 (A @ W^T, bf16 result), bf16f32 (A @ W^T, fp32 result)
+# kinds: f32 (A @ B), f32nk (X @ W^T), bf16 (A @ W^T, bf16 result), bf16f32 (A @ W^T, fp32 result);
+# A is m x k, the right operand n x k (k x n for f32), rotated over `copies` distinct tensors
 dt = torch.bfloat16 if kind.startswith("bf16") else torch.float32
-a = (torch.randn(n, n, device=dev, generator=g) / 64).to(dt)
-b = (torch.randn(n, n, device=dev, generator=g) / 64).to(dt)
-rhs = b if kind == "f32" else b.t()
-out = torch.empty(n, n, device=dev, dtype=torch.float32 if kind == "bf16f32" else dt)
+a = (torch.randn(m, k, device=dev, generator=g) / 64).to(dt)
+bs = [(torch.randn(k, n, device=dev, generator=g) if kind == "f32" else
+       torch.randn(n, k, device=dev, generator=g)).div_(64).to(dt) for _ in range(copies)]
+rhs = [b if kind == "f32" else b.t() for b in bs]
+out = torch.empty(m, n, device=dev, dtype=torch.float32 if kind == "bf16f32" else dt)
 if kind == "bf16f32":
-    def call():
-        torch.mm(a, rhs, torch.float32, out=out)
+    def call(i):
+        torch.mm(a, rhs[i % copies], torch.float32, out=out)
 else:
-    def call():
-        torch.matmul(a, rhs, out=out)
+    def call(i):
+        torch.matmul(a, rhs[i % copies], out=out)
 import time
 t_end = time.perf_counter() + 0.3  # back-to-back calls past the clock ramp, as this library's workloads get
 while time.perf_counter() < t_end:
-    for _ in range(10):
-        call()
+    for i in range(10):
+        call(i)
     torch.cuda.synchronize()
 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 e0.record()
-for _ in range(calls):
-    call()
+for i in range(calls):
+    call(i)
 e1.record()
 torch.cuda.synchronize()
 print(json.dumps({"ms": e0.elapsed_time(e1) / calls, "torch": torch.__version__}))
 """
 
 
-def library_reference(kind, n=4096, calls=50):
+def library_reference(kind, n=4096, calls=50, shape=None, copies=1):
     """The vendor library on the same problem, for comparison only (opt-in, --library-reference):
-    torch.matmul (hipBLASLt on ROCm) on n^3 N(0, 1/64) operands, `calls` back-to-back calls
-    between two events after 0.3 s of untimed ones (the clock ramp). kind "f32": fp32 A @ B; "bf16": bf16 A @ W^T with
-    a bf16 result (half the output bytes of this library's fp32 result); "bf16f32": bf16 A @ W^T with an fp32
+    torch.matmul (hipBLASLt on ROCm) on N(0, 1/64) operands (n^3, or shape = (m, n, k)), `calls`
+    back-to-back calls between two events after 0.3 s of untimed ones (the clock ramp), the right
+    operand rotated over `copies` tensors. kind "f32": fp32 A @ B; "bf16": bf16 A @ W^T with a bf16
+    result (half the output bytes of this library's fp32 result); "bf16f32": bf16 A @ W^T with an fp32
     result (torch.mm's out_dtype, this library's problem); "f32nk": fp32 X @ W^T."""
     import subprocess
 
-    proc = subprocess.run([sys.executable, "-c", LIBRARY_REFERENCE_CHILD, kind, str(n), str(calls), str(SEED)],
-                          capture_output=True, text=True, timeout=600)
+    m, nn, k = shape if shape else (n, n, n)
+    proc = subprocess.run([sys.executable, "-c", LIBRARY_REFERENCE_CHILD, kind, str(m), str(nn), str(k), str(calls),
+                           str(SEED), str(copies)], capture_output=True, text=True, timeout=600)
     if proc.returncode != 0:
         return {"impl": "torch.matmul", "error": proc.stderr.strip().splitlines()[-1:]}
     r = json.loads(proc.stdout.strip().splitlines()[-1])
@@ -277,7 +281,24 @@ def library_reference(kind, n=4096, calls=50):
     desc = {"f32": "fp32, A @ B", "f32nk": "fp32, X @ W^T", "bf16": "bf16 in/out, A @ W^T",
             "bf16f32": "bf16 in, fp32 out, A @ W^T"}[kind]
     return {"impl": f"torch {r['torch']} matmul ({desc})",
-            "ms": round(ms, 5), "value": round(2.0 * n ** 3 / ms / 1e9, 2), "unit": "TFLOP/s"}
+            "ms": round(ms, 5), "value": round(2.0 * m * nn * k / ms / 1e9, 2), "unit": "TFLOP/s"}
+
+
+def library_reference_prefill(prompt_len=512):
+    """hipBLASLt (torch.mm, bf16 operands, fp32 result) on the bf16 Llama prefill's four projection
+    shapes at prompt_len rows, the weights rotated over enough copies (>= 600 MB) that they come
+    from HBM as the model's 16 layers' do; microseconds per call."""
+    from opworks_amd.llama import LLAMA_3_2_1B as c
+
+    H, I = c["hidden_size"], c["intermediate_size"]
+    qkv = (c["num_attention_heads"] + 2 * c["num_key_value_heads"]) * c["head_dim"]
+    out = {}
+    for name, (n, k) in {"qkv": (qkv, H), "o_proj": (H, c["num_attention_heads"] * c["head_dim"]),
+                         "gate_up": (2 * I, H), "down": (H, I)}.items():
+        copies = max(2, int(6e8 // (n * k * 2)))
+        ref = library_reference("bf16f32", calls=100, shape=(prompt_len, n, k), copies=copies)
+        out[name] = round(ref["ms"] * 1e3, 2) if "ms" in ref else ref
+    return {"impl": "torch.mm (bf16 in, fp32 out), weights rotated over copies", "rows": prompt_len, "us": out}
 
 
 def wl_gemm(stream, steps, warmup):
@@ -738,7 +759,8 @@ def main() -> int:
     ap.add_argument("--workload", default="all", help="all | " + " | ".join(WORKLOADS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--library-reference", action="store_true",
-                    help="also time torch.matmul (hipBLASLt) beside the gemm and gemm_bf16 workloads")
+                    help="also time torch.matmul (hipBLASLt) beside the gemm, gemm_bf16 and linear workloads, "
+                         "and on the bf16 prefill's projection shapes beside llama_bf16")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -762,6 +784,10 @@ def main() -> int:
                     ref["ratio"] = round(results[name]["value"] / ref["value"], 4)  # this library / the vendor's
                 results[name][key] = ref
                 print(f"[bench] {name} {key}: {ref.get('value', ref.get('error'))}", file=sys.stderr, flush=True)
+        if "llama_bf16" in results:  # the prefill's projection GEMMs against the library's
+            results["llama_bf16"]["library_reference_prefill"] = library_reference_prefill()
+            print(f"[bench] llama_bf16 library_reference_prefill: "
+                  f"{results['llama_bf16']['library_reference_prefill']['us']}", file=sys.stderr, flush=True)
     if not args.no_cpu:  # the oracle on this host beside every GPU figure (bounded samples)
         for name in names:
             if name != headline and name in CPU_SAMPLES:
