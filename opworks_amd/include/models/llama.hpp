@@ -849,24 +849,29 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
             const LayerWeights<WT> &lw = w_.layers[static_cast<size_t>(l)];
             if (!input_normed)
                 norm(lw.input_norm.data());
-            if (xb)
-                direct(StoreTag{}, xbits, lw.qkv_proj.data(), s.workspace.qkv.data(), qkvw, H);
-            else
-                project(s, normed, lw.qkv_proj.data(), s.workspace.qkv.data(), n, qkvw, H, st);
-            launch_async(st, llama::rope_split_kernel, detail::stream_grid(int64_t(n) * (qh + 2 * kvh) * (D / 2)),
-                         256, s.workspace.qkv.data(), w_.rope_inv_freq.data(), s.workspace.q_heads.data(), layer_k(s, l), layer_v(s, l), n, qh,
-                         kvh, D, s.cache.max_seq_len, 0);
+            // RoPE + head split + KV append; when the qkv projection splits K, this pass sums the
+            // partial tiles itself in place of the split-K reduction
+            auto rope_split = [&](const float *src, int splits) {
+                launch_async(st, llama::rope_split_kernel, detail::stream_grid(int64_t(n) * (qh + 2 * kvh) * (D / 2)),
+                             256, src, splits, w_.rope_inv_freq.data(), s.workspace.q_heads.data(), layer_k(s, l),
+                             layer_v(s, l), n, qh, kvh, D, s.cache.max_seq_len, 0);
+            };
+            auto rope_from_partials = [&](float *ws, int splits) { rope_split(ws, splits); };
+            const bool qkv_split =
+                xb ? detail::gemm_bf16_launch_direct<IdentityEpilogue, GemmStore::store>(
+                         xbits, reinterpret_cast<const uint16_t *>(lw.qkv_proj.data()), nullptr, s.workspace.qkv.data(),
+                         n, qkvw, H, IdentityEpilogue{}, s.workspace.splitk.data(), s.workspace.splitk.size(), st,
+                         rope_from_partials)
+                   : project(s, normed, lw.qkv_proj.data(), s.workspace.qkv.data(), n, qkvw, H, st, rope_from_partials);
+            if (!qkv_split)
+                rope_split(s.workspace.qkv.data(), 0);
+            // the attention writes its rows with the heads merged, [T][qh * D], as o_proj reads them
+            // (bf16 bits for the bf16 GEMM), so no separate merge pass runs
             ops::attention_prefill_ws(s.workspace.q_heads.data(), layer_k(s, l), layer_v(s, l),
-                                      s.workspace.attn_heads.data(), n, n, 0, qh, cfg_.kv_rep(), D, s.cache.max_seq_len,
-                                      s.workspace.attn_split.data(), s.workspace.attn_split.size(),
-                                      s.workspace.attn_split_counters.data(), s.workspace.attn_split_counters.size(),
-                                      -1, st);
-            if (xb)
-                launch_async(st, llama::merge_heads_kernel<uint16_t>, detail::stream_grid(int64_t(n) * qh * D), 256,
-                             s.workspace.attn_heads.data(), xbits, n, qh, D);
-            else
-                launch_async(st, llama::merge_heads_kernel<float>, detail::stream_grid(int64_t(n) * qh * D), 256,
-                             s.workspace.attn_heads.data(), s.workspace.attn_out.data(), n, qh, D);
+                                      xb ? reinterpret_cast<float *>(xbits) : s.workspace.attn_out.data(), n, n, 0, qh,
+                                      cfg_.kv_rep(), D, s.cache.max_seq_len, s.workspace.attn_split.data(),
+                                      s.workspace.attn_split.size(), s.workspace.attn_split_counters.data(),
+                                      s.workspace.attn_split_counters.size(), -1, st, true, xb);
             if (!residual_then_norm(s.workspace.attn_out.data(), xbits, lw.o_proj.data(), qh * D, lw.post_norm.data()))
                 norm(lw.post_norm.data());
             if (xb)

@@ -590,7 +590,10 @@ __global__ __launch_bounds__(256) void embed_token_kernel(const WT *__restrict__
 
 // qkv [T][(qh + 2 kvh) D] -> RoPE(q) into q_heads [qh][T][D]; RoPE(k) and v
 // appended to the caches at positions pos_start + t. One thread per rotary pair.
-__global__ __launch_bounds__(256) static void rope_split_kernel(const float *__restrict__ qkv,
+// splits > 0: qkv holds the split-K partials of the projection instead, `splits`
+// slices of [T][width], summed here in split order and then + 0.f, exactly as
+// splitk_reduce_kernel would have stored them (one pass and one launch fewer).
+__global__ __launch_bounds__(256) static void rope_split_kernel(const float *__restrict__ qkv, int splits,
                                                                 const float *__restrict__ inv_freq,
                                                                 float *__restrict__ q_heads, float *__restrict__ kcache,
                                                                 float *__restrict__ vcache, int T, int qh, int kvh,
@@ -598,6 +601,7 @@ __global__ __launch_bounds__(256) static void rope_split_kernel(const float *__r
     const int half = D / 2;
     const int slots = qh + 2 * kvh;
     const int width = slots * D;
+    const int64_t slice = int64_t(T) * width;
     OPWORKS_GRID_LOOP(i, int64_t(T) * slots * half) {
         const int j = static_cast<int>(i % half);
         const int slot = static_cast<int>((i / half) % slots);
@@ -605,6 +609,14 @@ __global__ __launch_bounds__(256) static void rope_split_kernel(const float *__r
         const int pos = pos_start + t;
         const float *src = qkv + int64_t(t) * width + slot * D;
         float lo = src[j], hi = src[j + half];
+        if (splits > 0) { // uniform
+            for (int sp = 1; sp < splits; ++sp) {
+                lo = lo + src[sp * slice + j];
+                hi = hi + src[sp * slice + j + half];
+            }
+            lo = lo + 0.f;
+            hi = hi + 0.f;
+        }
         if (slot < qh + kvh) {
             const float freq = static_cast<float>(pos) * inv_freq[j];
             float s, c;
@@ -622,23 +634,6 @@ __global__ __launch_bounds__(256) static void rope_split_kernel(const float *__r
             dst = vcache + (int64_t(slot - qh - kvh) * cap + pos) * D;
         dst[j] = lo;
         dst[j + half] = hi;
-    }
-}
-
-// attn_heads [qh][T][D] -> packed rows [T][qh * D]; OT = uint16_t rounds each value to bf16
-// (nearest-even) as it is stored, the input of a bf16 o_proj GEMM.
-template <typename OT = float>
-__global__ __launch_bounds__(256) void merge_heads_kernel(const float *__restrict__ in, OT *__restrict__ out, int T,
-                                                          int qh, int D) {
-    OPWORKS_GRID_LOOP(i, int64_t(T) * qh * D) {
-        const int d = static_cast<int>(i % D);
-        const int h = static_cast<int>((i / D) % qh);
-        const int t = static_cast<int>(i / (int64_t(D) * qh));
-        const float v = in[(int64_t(h) * T + t) * D + d];
-        if constexpr (std::is_same_v<OT, float>)
-            out[i] = v;
-        else
-            out[i] = float_to_bf16_rne(v);
     }
 }
 

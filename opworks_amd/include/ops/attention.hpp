@@ -44,6 +44,7 @@
 #include <cstdint>
 #include <type_traits>
 
+#include "../core/bf16.hpp"
 #include "../core/hip_utils.hpp"
 #include "../core/wave.hpp"
 #include "elementwise.hpp"
@@ -267,6 +268,15 @@ struct PrefillSplit {
     int alternate; // nonzero: units go out in passes of alternating direction, not in descending order
 };
 
+// Where output row q of head h goes: element h * head_stride + q * row_stride, then head_dim
+// consecutive values, fp32 or (bf16 != 0) rounded to bf16 nearest-even. The reference's layout
+// [qh][T][D] is head_stride T * D, row_stride D; [T][qh * D] (the heads merged, as the output
+// projection reads them) is head_stride D, row_stride qh * D.
+struct PrefillOut {
+    int64_t head_stride, row_stride;
+    int bf16;
+};
+
 // amdgpu_waves_per_eu: with four or more waves per workgroup the register budget is 128
 // (four resident waves per SIMD, as many as the LDS allows); the bound also makes the
 // compiler keep the MFMA accumulators in VGPRs rather than AGPRs. kSplit: the workspace form
@@ -277,7 +287,7 @@ __global__ __launch_bounds__(kTiles *kWaves *kWaveSize)
 __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) void attention_prefill_kernel(
     const float *__restrict__ q_heads, const float *__restrict__ kcache, const float *__restrict__ vcache,
     float *__restrict__ out, int T, int S, int q_offset, int kv_rep, int num_kv_heads, int cap, float qscale,
-    int pass_width, PrefillSplit sp) {
+    int pass_width, PrefillSplit sp, PrefillOut ol) {
     using Shape = PrefillShape<kDT, kWaves, kTiles, kX6>;
     constexpr int D = Shape::kD, kLd = Shape::kLd, kQ = Shape::kQ;
     static_assert(!kX6 || kDT % 2 == 0, "the bf16x6 path needs head_dim 32 or 64");
@@ -667,14 +677,19 @@ __attribute__((amdgpu_waves_per_eu(kWaves >= 4 ? 4 : 2, kWaves >= 4 ? 4 : 2))) v
     }
     const float inv = l > 0.f ? 1.f / l : 0.f;
     if (head_ok && tile_ok && q < T) {
-        float *orow = out + (int64_t(h) * T + q) * D;
+        const int64_t orow = int64_t(h) * ol.head_stride + int64_t(q) * ol.row_stride;
 #pragma unroll
         for (int t = 0; t < kDT; ++t) {
             f32x4 o;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
                 o[r] = oacc[t][r] * inv;
-            *reinterpret_cast<f32x4 *>(orow + 16 * t + 4 * g) = o;
+            if (ol.bf16) // uniform
+                *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(out) + orow + 16 * t + 4 * g) =
+                    uint2{uint32_t(float_to_bf16_rne(o[0])) | (uint32_t(float_to_bf16_rne(o[1])) << 16),
+                          uint32_t(float_to_bf16_rne(o[2])) | (uint32_t(float_to_bf16_rne(o[3])) << 16)};
+            else
+                *reinterpret_cast<f32x4 *>(out + orow + 16 * t + 4 * g) = o;
         }
     }
 }
@@ -688,6 +703,8 @@ struct PrefillWorkspaceArgs {
     int *counters = nullptr;
     int64_t counter_ints = 0;
     int thr = -1;
+    bool merged_heads = false; // output [T][qh * D] instead of [qh][T][D]
+    bool out_bf16 = false;     // output rounded to bf16 (nearest-even)
 };
 
 // Workspace form on the host: the threshold, how many groups split, and what that needs.
@@ -745,6 +762,9 @@ inline void attention_prefill_launch(const float *q, const float *k, const float
     const int64_t ngroups = blocks_for64(blocks_for64(T, kAttnQTile), kTiles);
     require(ngroups * per_tile <= INT32_MAX, "attention_prefill: grid too large");
     const int pass_width = cu_count() / per_tile > 0 ? cu_count() / per_tile : 1;
+    const int D = 16 * kDT, qh = kvh * kv_rep;
+    const PrefillOut ol = ws && ws->merged_heads ? PrefillOut{D, int64_t(qh) * D, ws->out_bf16 ? 1 : 0}
+                                                 : PrefillOut{int64_t(T) * D, D, ws && ws->out_bf16 ? 1 : 0};
     if (ws) {
         const PrefillSplitPlan p = prefill_split_plan<kDT, kWaves, kTiles>(T, S, q_offset, kv_rep, kvh, ws->thr,
                                                                            ws->rec_floats, ws->counter_ints);
@@ -753,13 +773,13 @@ inline void attention_prefill_launch(const float *q, const float *k, const float
             launch_async_lds(stream, Shape::kLdsBytes, attention_prefill_kernel<kDT, kWaves, kTiles, true, kX6>,
                              static_cast<int>((ngroups + p.nsplit) * per_tile), Shape::kThreads, q, k, v, out, T, S,
                              q_offset, kv_rep, kvh, cap, scale * kLog2e, pass_width,
-                             PrefillSplit{ws->rec, ws->counters, p.thr, p.alternate});
+                             PrefillSplit{ws->rec, ws->counters, p.thr, p.alternate}, ol);
             return;
         }
     }
     launch_async_lds(stream, Shape::kLdsBytes, attention_prefill_kernel<kDT, kWaves, kTiles, false, kX6>,
                      static_cast<int>(ngroups * per_tile), Shape::kThreads, q, k, v, out, T, S, q_offset, kv_rep, kvh,
-                     cap, scale * kLog2e, pass_width, PrefillSplit{nullptr, nullptr, 0, 0});
+                     cap, scale * kLog2e, pass_width, PrefillSplit{nullptr, nullptr, 0, 0}, ol);
 }
 
 // Two query tiles per workgroup when the one-tile grid would fill every CU's four
@@ -1519,7 +1539,7 @@ inline void attention_prefill_workspace_size(int T, int S, int q_offset, int num
 inline void attention_prefill_ws(const float *q_heads, const float *kcache, const float *vcache, float *out, int T,
                                  int S, int q_offset, int num_q_heads, int kv_rep, int head_dim, int cap, float *rec,
                                  int64_t rec_floats, int *counters, int64_t counter_ints, int thr = -1,
-                                 hipStream_t stream = nullptr) {
+                                 hipStream_t stream = nullptr, bool merged_heads = false, bool out_bf16 = false) {
     detail::require(T > 0 && S >= T && q_offset == S - T, "attention_prefill: bad shape/offset");
     detail::require(num_q_heads > 0 && kv_rep > 0 && num_q_heads % kv_rep == 0, "attention_prefill: bad head shape");
     detail::require(head_dim > 0 && head_dim <= detail::kAttnMaxD && head_dim % 16 == 0,
@@ -1530,7 +1550,9 @@ inline void attention_prefill_ws(const float *q_heads, const float *kcache, cons
                     "attention_prefill_ws: bad workspace");
     const float scale = 1.f / std::sqrt(static_cast<float>(head_dim));
     const int kvh = num_q_heads / kv_rep;
-    const detail::PrefillWorkspaceArgs ws{rec, rec_floats, counters, counter_ints, thr};
+    detail::require(!(merged_heads || out_bf16) || reinterpret_cast<uintptr_t>(out) % 8 == 0,
+                    "attention_prefill_ws: merged or bf16 output needs 8-byte alignment");
+    const detail::PrefillWorkspaceArgs ws{rec, rec_floats, counters, counter_ints, thr, merged_heads, out_bf16};
     switch (head_dim / 16) {
     case 1: detail::attention_prefill_dispatch<1>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, &ws); break;
     case 2: detail::attention_prefill_dispatch<2>(q_heads, kcache, vcache, out, T, S, q_offset, kv_rep, kvh, cap, scale, stream, &ws); break;

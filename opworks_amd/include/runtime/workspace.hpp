@@ -3,14 +3,16 @@
 // Per-session scratch of the Llama runtime (reference: include/runtime/
 // workspace.cuh:10-55), allocated once when the session is created and reused
 // by every prefill and decode step. Buffers with a counterpart in the
-// reference keep its name (tokens, hidden, normed, q_heads, attn_heads,
-// attn_out, logits); the others serve this build's fused kernels: the fused
-// [q;k;v] projection output, the SwiGLU product, split-K partial tiles, the
-// bf16 copy of the gate/up GEMM input (bf16-weight models), the prefill
-// attention's split records and counters, the one-row buffers of the decode
-// step, the decode attention's chunk records
-// and arrival counters, the LM head's per-workgroup argmax records, the
-// device step state and the tokens a chained greedy decode produces.
+// reference keep its name (tokens, hidden, normed, q_heads, attn_out,
+// logits). The reference's attn_heads is not needed: the prefill attention
+// writes its rows with the heads merged, straight into attn_out (or, for
+// bf16 weights, into the bf16 input copy). The others serve this build's
+// fused kernels: the fused [q;k;v] projection output, the SwiGLU product,
+// split-K partial tiles, the bf16 copy of each projection's input (bf16-weight
+// models), the prefill attention's split records and counters, the one-row
+// buffers of the decode step, the decode attention's chunk records and
+// arrival counters, the LM head's per-workgroup argmax records, the device
+// step state and the tokens a chained greedy decode produces.
 
 #include <algorithm>
 #include <cstdint>
@@ -40,7 +42,6 @@ struct Workspace {
     TypedDeviceBuffer<float> normed;     // [T, H]
     TypedDeviceBuffer<float> qkv;        // [T, (qh + 2 kvh) D] fused projection output
     TypedDeviceBuffer<float> q_heads;    // [qh, T, D]
-    TypedDeviceBuffer<float> attn_heads; // [qh, T, D]
     TypedDeviceBuffer<float> attn_out;   // [T, qh D]
     TypedDeviceBuffer<float> act;        // [T, I] silu(gate) * up
     TypedDeviceBuffer<float> splitk;     // split-K partial tiles
@@ -73,7 +74,6 @@ struct Workspace {
         normed = TypedDeviceBuffer<float>(T * H);
         qkv = TypedDeviceBuffer<float>(T * cfg.qkv_width());
         q_heads = TypedDeviceBuffer<float>(T * qw);
-        attn_heads = TypedDeviceBuffer<float>(T * qw);
         attn_out = TypedDeviceBuffer<float>(T * qw);
         act = TypedDeviceBuffer<float>(T * I);
         if (T >= 2) { // only a multi-row prefill runs the GEMMs
