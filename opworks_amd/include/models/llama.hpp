@@ -773,13 +773,13 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
         } else if constexpr (kBf16) {
             detail::gemm_bf16_launch<float, IdentityEpilogue, kStore>(A, Wb, nullptr, C, M, N, K, IdentityEpilogue{},
                                                                       st);
-        } else if constexpr (kSplittable) {
+        } else if constexpr (kSplittable) { // fp32 MFMA kernels: the oracle parity of the logits
             return detail::gemm_f32_launch_splitk<detail::BLayout::nk, IdentityEpilogue, kStore>(
                 A, W, nullptr, C, M, N, K, IdentityEpilogue{}, s.workspace.splitk.data(), s.workspace.splitk.size(), st,
                 reduce);
         } else {
             detail::gemm_f32_launch<detail::BLayout::nk, IdentityEpilogue, kStore>(A, W, nullptr, C, M, N, K,
-                                                                                  IdentityEpilogue{}, st);
+                                                                                  IdentityEpilogue{}, st, 1, false);
         }
         return false;
     }

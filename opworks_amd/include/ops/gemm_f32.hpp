@@ -40,6 +40,7 @@
 // k-ascending fmaf chain only by summation order.
 
 #include <cstddef>
+#include <cstdlib>
 #include <cstdint>
 #include <type_traits>
 
@@ -484,6 +485,36 @@ void gemm_f32_launch_shape(const float *A, const TB *B, const float *bias, float
                      B, bias, C, M, N, K, epi);
 }
 
+} // namespace opworks::detail
+
+#include "gemm_x6.hpp"
+
+namespace opworks::detail {
+
+// The nk-layout fp32 products that the bf16x6 kernel takes: fp32 operands, A row-major, 16-byte
+// aligned, K a multiple of 8, and enough work to fill its 128 x 256 tiles (at 4096^3 nk: 1003 ->
+// 673 us, 1.30 of the fp32 MFMA peak; 512 x 16384 x 2048: 279 -> 179 us), for plain stores (the
+// operator API's products). Callers that need the fp32 MFMA kernels' summation (the Llama runtime,
+// held to the oracle's logits at 1e-5, whose config-5 run read 1.05e-5 through bf16x6 against 9.27e-6)
+// pass allow_x6 = false; the split-K form (the runtime's) never takes it.
+// OPWORKS_GEMM_X6=0 in the environment keeps every product on the fp32 MFMA kernels.
+inline bool gemm_x6_enabled() {
+    static const bool enabled = [] {
+        const char *v = std::getenv("OPWORKS_GEMM_X6");
+        return !(v && v[0] == '0' && v[1] == '\0');
+    }();
+    return enabled;
+}
+template <BLayout kB, GemmStore kStore, typename TB, ALayout kAL>
+inline bool gemm_use_x6(const float *A, const TB *B, int M, int N, int K) {
+    if constexpr (kB == BLayout::nk && std::is_same_v<TB, float> && kAL == ALayout::mk &&
+                  kStore == GemmStore::store) {
+        return M >= 16 && int64_t(M) * N * K >= (int64_t(1) << 26) && gemm_x6_ok(A, B, K) && gemm_x6_enabled();
+    } else {
+        return false;
+    }
+}
+
 // Enqueues C[M][N] = epi(A[M][K] B + bias) (written per kStore). K == 0 writes epi(bias or 0).
 // When K is not split: GemmBig when its tiles alone cover every CU, else GemmMid when its
 // 256 x 128 tiles do (the prefill gate/up projection at 512 rows: 280 -> 262 us against
@@ -491,8 +522,15 @@ void gemm_f32_launch_shape(const float *A, const TB *B, const float *bias, float
 template <BLayout kB, typename Epi, GemmStore kStore = GemmStore::store, typename TB = float,
           ALayout kAL = ALayout::mk>
 void gemm_f32_launch(const float *A, const TB *B, const float *bias, float *C, int M, int N, int K, Epi epi,
-                     hipStream_t stream, int splits = 1) {
+                     hipStream_t stream, int splits = 1, bool allow_x6 = true) {
     require(kStore != GemmStore::swiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
+    if constexpr (kB == BLayout::nk && std::is_same_v<TB, float> && kAL == ALayout::mk &&
+                  kStore == GemmStore::store) {
+        if (allow_x6 && gemm_use_x6<kB, kStore, TB, kAL>(A, B, M, N, K)) {
+            gemm_x6_launch<Epi, kStore>(A, B, bias, C, M, N, K, epi, stream, splits);
+            return;
+        }
+    }
     const int64_t big_tiles = blocks_for64(M, GemmBig::BM) * blocks_for64(N, GemmBig::BN);
     const int64_t mid_tiles = blocks_for64(M, GemmMid::BM) * blocks_for64(N, GemmMid::BN);
     if (splits == 1 && big_tiles >= 256)
@@ -529,7 +567,7 @@ bool gemm_f32_launch_splitk(const float *A, const TB *B, const float *bias, floa
                                                       ktiles, 512);
     if (splits == 1 || N % 4 != 0 || !ws || int64_t(splits) * M * N > ws_floats || !aligned16(C) ||
         (bias && !aligned16(bias))) {
-        gemm_f32_launch<kB, Epi, kStore, TB>(A, B, bias, C, M, N, K, epi, stream);
+        gemm_f32_launch<kB, Epi, kStore, TB>(A, B, bias, C, M, N, K, epi, stream, 1, false); // fp32 MFMA
         return false;
     }
     if (mid_splits > 1)

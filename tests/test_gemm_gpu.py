@@ -121,6 +121,26 @@ def test_linear_matches_oracle(ow, orc, rows, in_f, out_f):
         check_kscaled(got[0], orc.gemv(X, W, in_f, out_f), absdot[0])
 
 
+@pytest.mark.parametrize("rows,in_f,out_f", [(512, 2048, 3072), (300, 1000, 600), (1024, 8192, 512)])
+def test_linear_bf16x6_path_has_fp32_accuracy(ow, rows, in_f, out_f):
+    """ops::linear with fp32 weights at these sizes runs the bf16x6 kernel (three bf16 parts per
+    operand, six MFMAs per product). Against float64 on sampled rows its error stays at fp32's
+    level, 2e-6 of sum_k |x w| (the fp32 MFMA kernel's worst on the same data is of the same
+    order), far inside the 1e-4 bar; ragged tiles (300 x 600) and a K tail (1000 = 31 x 32 + 8)."""
+    rng = np.random.default_rng(SEED + rows)
+    X = rng.standard_normal((rows, in_f)).astype(np.float32)
+    W = (rng.standard_normal((out_f, in_f)) * 0.02).astype(np.float32)
+    Y = ow.DeviceBuffer.empty(rows * out_f)
+    dX, dW = upload(ow, X.ravel()), upload(ow, W.ravel())
+    ow.ops.linear(dX, dW, Y, rows, in_f, out_f)
+    got = Y.to_host().reshape(rows, out_f)
+    sample = np.unique(np.concatenate([np.arange(0, rows, 37), [rows - 1]]))
+    Xs, W64 = X[sample].astype(np.float64), W.astype(np.float64)
+    ref = Xs @ W64.T
+    absdot = np.abs(Xs) @ np.abs(W64).T
+    check_kscaled(got[sample], ref, absdot, tol=2e-6, floor=0.0)
+
+
 @pytest.mark.slow
 def test_config3_full_size_sampled(ow, orc):
     """Config 3: C = relu(A @ B + bias), M = N = K = 4096, A, B ~ N(0, 1/64), bias ~ U[-0.1, 0.1];
