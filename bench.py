@@ -125,7 +125,7 @@ def roofline(achieved: float, peak: float, unit: str, bound: str, traffic=None) 
 
 TRAFFIC_FILES = (ROOT / "profiles" / "llama_decode_traffic.md", ROOT / "profiles" / "stream_ops_traffic.md",
                  ROOT / "profiles" / "scan_transpose_gather_traffic.md", ROOT / "profiles" / "gemm_attention_traffic.md",
-                 ROOT / "profiles" / "gemm_x6_linear.md")
+                 ROOT / "profiles" / "gemm_x6_linear_and_config3.md")
 
 
 def profiled_traffic(stage: str):
@@ -315,9 +315,17 @@ def wl_gemm(stream, steps, warmup):
                                                                          stream)), steps, warmup)
     flop = 2.0 * n ** 3
     tf = flop / ms / 1e9
+    executed = 6.0 * flop / ms / 1e9  # bf16x6 products, as the linear workload's
     return {"workload": "gemm_f32_relu_bias_4096^3", "unit": "TFLOP/s", "value": tf, "ms": ms, "flop": flop,
-            "kernel": "gemm_f32_mfma_kernel<kn>",
-            "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma", traffic=profiled_traffic("gemm"))}
+            "kernel": "gemm_x6_kernel<kn> (bf16x6 products)",
+            "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma", traffic=profiled_traffic("gemm_x6")),
+            "mfma_executed": {"dtype": "bf16", "flop_per_launch": 6.0 * flop, "achieved": round(executed, 2),
+                              "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                              "frac": round(executed / BF16_PEAK_TFLOPS, 4)},
+            "note": "fp32-accurate products on bf16 MFMAs (three bf16 parts per operand, six MFMAs per product; "
+                    "B [K][N] transposed while staged): roofline.frac prices the algorithmic fp32 flops against the "
+                    "fp32 MFMA peak and can exceed 1; mfma_executed prices the issued bf16 work against the bf16 "
+                    "peak. OPWORKS_GEMM_X6=0 runs the fp32 MFMA kernel instead"}
 
 
 def wl_gemm_bf16(stream, steps, warmup):

@@ -491,9 +491,9 @@ void gemm_f32_launch_shape(const float *A, const TB *B, const float *bias, float
 
 namespace opworks::detail {
 
-// The nk-layout fp32 products that the bf16x6 kernel takes: fp32 operands, A row-major, 16-byte
-// aligned, K a multiple of 8, and enough work to fill its 128 x 256 tiles (at 4096^3 nk: 1003 ->
-// 673 us, 1.30 of the fp32 MFMA peak; 512 x 16384 x 2048: 279 -> 179 us), for plain stores (the
+// The fp32 products that the bf16x6 kernel takes: fp32 operands, A row-major, 16-byte aligned,
+// K a multiple of 8 (and N of 4 for a kn-layout B), and enough work to fill its 128 x 256 tiles
+// (at 4096^3 nk: 1003 -> 673 us, 1.30 of the fp32 MFMA peak; 512 x 16384 x 2048: 279 -> 179 us), for plain stores (the
 // operator API's products). Callers that need the fp32 MFMA kernels' summation (the Llama runtime,
 // held to the oracle's logits at 1e-5, whose config-5 run read 1.05e-5 through bf16x6 against 9.27e-6)
 // pass allow_x6 = false; the split-K form (the runtime's) never takes it.
@@ -507,9 +507,9 @@ inline bool gemm_x6_enabled() {
 }
 template <BLayout kB, GemmStore kStore, typename TB, ALayout kAL>
 inline bool gemm_use_x6(const float *A, const TB *B, int M, int N, int K) {
-    if constexpr (kB == BLayout::nk && std::is_same_v<TB, float> && kAL == ALayout::mk &&
-                  kStore == GemmStore::store) {
-        return M >= 16 && int64_t(M) * N * K >= (int64_t(1) << 26) && gemm_x6_ok(A, B, K) && gemm_x6_enabled();
+    if constexpr (std::is_same_v<TB, float> && kAL == ALayout::mk && kStore == GemmStore::store) {
+        return M >= 16 && int64_t(M) * N * K >= (int64_t(1) << 26) && gemm_x6_ok<kB>(A, B, N, K) &&
+               gemm_x6_enabled();
     } else {
         return false;
     }
@@ -524,10 +524,9 @@ template <BLayout kB, typename Epi, GemmStore kStore = GemmStore::store, typenam
 void gemm_f32_launch(const float *A, const TB *B, const float *bias, float *C, int M, int N, int K, Epi epi,
                      hipStream_t stream, int splits = 1, bool allow_x6 = true) {
     require(kStore != GemmStore::swiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
-    if constexpr (kB == BLayout::nk && std::is_same_v<TB, float> && kAL == ALayout::mk &&
-                  kStore == GemmStore::store) {
+    if constexpr (std::is_same_v<TB, float> && kAL == ALayout::mk && kStore == GemmStore::store) {
         if (allow_x6 && gemm_use_x6<kB, kStore, TB, kAL>(A, B, M, N, K)) {
-            gemm_x6_launch<Epi, kStore>(A, B, bias, C, M, N, K, epi, stream, splits);
+            gemm_x6_launch<kB, Epi, kStore>(A, B, bias, C, M, N, K, epi, stream, splits);
             return;
         }
     }

@@ -1,8 +1,9 @@
 #pragma once
 
 // fp32 GEMM on bf16 MFMAs with three-part operands ("bf16x6", core/bf16x6.hpp):
-//   C[m][n] = epi(sum_k A[m][k] W[n][k] + bias[n]),   A fp32 [M][K], W fp32 [N][K] (nk),
-// both k-contiguous, 16-byte aligned, K a multiple of 8. Every fp32 operand value splits
+//   C[m][n] = epi(sum_k A[m][k] B(k, n) + bias[n]),   A fp32 [M][K] k-contiguous, and B either
+// W [N][K] (nk, the HF weight layout) or B [K][N] (kn, the reference's mat_mul); 16-byte aligned,
+// K a multiple of 8, and N a multiple of 4 for kn. Every fp32 operand value splits
 // exactly into three bf16 parts and each product keeps the six terms x_i y_j with i + j <= 2,
 // accumulated in fp32 by the MFMA: the products carry fp32's error (the dropped terms are below
 // 2^-24 of |x y|), on 16-cycle 16x16x32 bf16 MFMAs. Per 16x16x32 block of products that is
@@ -11,11 +12,12 @@
 // Kernel shape (gfx950): 128 x 256 outputs per workgroup, 512 lanes as 2 x 4 waves of 64 x 64
 // (4 x 4 16x16 accumulator tiles); K steps of 32. Each step's fp32 tiles are loaded into
 // registers one step ahead, split, and written as three bf16 planes per operand into the idle
-// LDS stage (72 KB per stage, two stages, one workgroup per CU). Plane rows are 64 bytes with
+// LDS stage (72 KB per stage, two stages, one workgroup per CU); a kn-layout B is transposed on the
+// way (each thread holds 4 k x 4 n and writes 8-byte pieces of n-major rows). Plane rows are 64 bytes with
 // their 16-byte chunks swizzled (x6_k_chunk<32>, measured conflict-free for these reads). A
 // wave reads its 3 x (4 + 4) fragments of a step and issues 6 x 16 MFMAs, smallest terms first.
 
-// Included by gemm_f32.hpp ahead of its launchers, which send nk-layout fp32 products here; it
+// Included by gemm_f32.hpp ahead of its launchers, which send fp32 products here; it
 // uses that header's GemmStore, gemm_tile_of and IdentityEpilogue. Include gemm_f32.hpp, not this.
 
 #include <cstdint>
@@ -30,7 +32,7 @@ struct GemmX6Shape {
     static constexpr int BM = 128, BN = 256, BK = 32, kThreads = 512, WM = 2, WN = 4;
 };
 
-template <typename Epi, GemmStore kStore>
+template <BLayout kB, typename Epi, GemmStore kStore>
 __global__ __launch_bounds__(GemmX6Shape::kThreads) void gemm_x6_kernel(const float *__restrict__ A,
                                                                        const float *__restrict__ W,
                                                                        const float *__restrict__ bias,
@@ -60,20 +62,36 @@ __global__ __launch_bounds__(GemmX6Shape::kThreads) void gemm_x6_kernel(const fl
     // are zeroed, so every load is issued unconditionally.
     const int kc = tid % 4, srow = tid / 4;
     const float *arow = A + int64_t(m0 + srow < M ? m0 + srow : M - 1) * K;
-    const float *brow0 = W + int64_t(n0 + srow < N ? n0 + srow : N - 1) * K;
-    const float *brow1 = W + int64_t(n0 + srow + 128 < N ? n0 + srow + 128 : N - 1) * K;
-    f32x4 ra[2], rb[2][2];
+    // nk: B rows srow and srow + 128 of the tile. kn: thread (q, o) = (tid % 64, tid / 64) holds
+    // columns 4q .. 4q + 3 of the tile at k 4o .. 4o + 3 (a wave reads 1 KB of one k row per load);
+    // columns past N read the last four (N % 4 == 0), rows past K read row K - 1 and are zeroed.
+    const float *brow0 = W + (kB == BLayout::nk ? int64_t(n0 + srow < N ? n0 + srow : N - 1) * K : 0);
+    const float *brow1 = W + (kB == BLayout::nk ? int64_t(n0 + srow + 128 < N ? n0 + srow + 128 : N - 1) * K : 0);
+    const int bq = tid % 64, bo = tid / 64;
+    const int bcol = n0 + 4 * bq + 3 < N ? n0 + 4 * bq : N - 4;
+    f32x4 ra[2], rb[2][2], rk[4];
     bool kin = true;
+    int kin_rows = 0; // kn: bit i set when row k 4o + i of the step lies inside K
     auto gload = [&](int kt) {
         const int k = kt * BK + 8 * kc;
         kin = k < K;
         const int kl = kin ? k : K - 8;
         ra[0] = *reinterpret_cast<const f32x4 *>(arow + kl);
         ra[1] = *reinterpret_cast<const f32x4 *>(arow + kl + 4);
-        rb[0][0] = *reinterpret_cast<const f32x4 *>(brow0 + kl);
-        rb[0][1] = *reinterpret_cast<const f32x4 *>(brow0 + kl + 4);
-        rb[1][0] = *reinterpret_cast<const f32x4 *>(brow1 + kl);
-        rb[1][1] = *reinterpret_cast<const f32x4 *>(brow1 + kl + 4);
+        if constexpr (kB == BLayout::nk) {
+            rb[0][0] = *reinterpret_cast<const f32x4 *>(brow0 + kl);
+            rb[0][1] = *reinterpret_cast<const f32x4 *>(brow0 + kl + 4);
+            rb[1][0] = *reinterpret_cast<const f32x4 *>(brow1 + kl);
+            rb[1][1] = *reinterpret_cast<const f32x4 *>(brow1 + kl + 4);
+        } else {
+            kin_rows = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kr = kt * BK + 4 * bo + i;
+                kin_rows |= (kr < K ? 1 : 0) << i;
+                rk[i] = *reinterpret_cast<const f32x4 *>(W + int64_t(kr < K ? kr : K - 1) * N + bcol);
+            }
+        }
     };
     auto slot = [](int row, int chunk) { return row * BK + 8 * x6_k_chunk<32>(chunk, row); };
     auto put = [&](uint16_t *plane0, int plane_elems, int row, const f32x4 (&x)[2]) {
@@ -92,8 +110,27 @@ __global__ __launch_bounds__(GemmX6Shape::kThreads) void gemm_x6_kernel(const fl
     auto commit = [&](int buf) {
         uint16_t *st = lds + buf * kStage;
         put(st, kPlaneA, srow, ra);
-        put(st + 3 * kPlaneA, kPlaneB, srow, rb[0]);
-        put(st + 3 * kPlaneA, kPlaneB, srow + 128, rb[1]);
+        if constexpr (kB == BLayout::nk) {
+            put(st + 3 * kPlaneA, kPlaneB, srow, rb[0]);
+            put(st + 3 * kPlaneA, kPlaneB, srow + 128, rb[1]);
+        } else { // column 4q + j: its four k values, split, as 8-byte pieces of the n-major rows
+            uint16_t *pb = st + 3 * kPlaneA;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    v[i] = (kin_rows >> i) & 1 ? rk[i][j] : 0.f;
+                uint32_t w[3][2];
+                split3x2(v[0], v[1], w[0][0], w[1][0], w[2][0]);
+                split3x2(v[2], v[3], w[0][1], w[1][1], w[2][1]);
+                const int row = 4 * bq + j;
+                const int off = row * BK + 8 * x6_k_chunk<32>(bo / 2, row) + 4 * (bo % 2);
+#pragma unroll
+                for (int p = 0; p < 3; ++p)
+                    *reinterpret_cast<uint2 *>(pb + p * kPlaneB + off) = uint2{w[p][0], w[p][1]};
+            }
+        }
     };
 
     f32x4 acc[FM][FN];
@@ -223,21 +260,24 @@ __global__ __launch_bounds__(GemmX6Shape::kThreads) void gemm_x6_kernel(const fl
         store_tile(std::true_type{});
 }
 
-// Whether the bf16x6 kernel takes this product: both operands 16-byte aligned and k-contiguous
-// in chunks of 8.
-inline bool gemm_x6_ok(const float *A, const float *W, int K) { return aligned16(A) && aligned16(W) && K % 8 == 0 && K > 0; }
+// Whether the bf16x6 kernel takes this product: both operands 16-byte aligned, A's rows in chunks
+// of 8 k, and for a kn-layout B whole groups of 4 columns.
+template <BLayout kB> inline bool gemm_x6_ok(const float *A, const float *B, int N, int K) {
+    return aligned16(A) && aligned16(B) && K % 8 == 0 && K > 0 && (kB == BLayout::nk || (N % 4 == 0 && N >= 4));
+}
 
-template <typename Epi, GemmStore kStore>
-void gemm_x6_launch(const float *A, const float *W, const float *bias, float *C, int M, int N, int K, Epi epi,
+template <BLayout kB, typename Epi, GemmStore kStore>
+void gemm_x6_launch(const float *A, const float *B, const float *bias, float *C, int M, int N, int K, Epi epi,
                     hipStream_t stream, int splits = 1) {
     static_assert(kStore != GemmStore::swiglu_bf16, "the bf16x6 GEMM stores fp32");
     require((kStore != GemmStore::swiglu) || N % 2 == 0, "swiglu epilogue needs an even number of columns");
-    require(gemm_x6_ok(A, W, K), "gemm_x6: operands must be 16-byte aligned with K a multiple of 8");
+    require(gemm_x6_ok<kB>(A, B, N, K), "gemm_x6: operands must be 16-byte aligned with K a multiple of 8 "
+                                        "(and N a multiple of 4 for a kn-layout B)");
     using S = GemmX6Shape;
     const int64_t tiles = blocks_for64(M, S::BM) * blocks_for64(N, S::BN);
     require(tiles <= INT32_MAX && splits >= 1, "gemm_x6: grid too large");
-    launch_async(stream, gemm_x6_kernel<Epi, kStore>, dim3(static_cast<unsigned>(tiles), splits), S::kThreads, A, W,
-                 bias, C, M, N, K, epi);
+    launch_async(stream, gemm_x6_kernel<kB, Epi, kStore>, dim3(static_cast<unsigned>(tiles), splits), S::kThreads, A,
+                 B, bias, C, M, N, K, epi);
 }
 
 } // namespace opworks::detail

@@ -141,6 +141,23 @@ def test_linear_bf16x6_path_has_fp32_accuracy(ow, rows, in_f, out_f):
     check_kscaled(got[sample], ref, absdot, tol=2e-6, floor=0.0)
 
 
+@pytest.mark.parametrize("M,N,K", [(512, 2048, 3072), (300, 1000, 604), (1024, 8192, 512)])
+def test_matmul_bf16x6_kn_path_has_fp32_accuracy(ow, M, N, K):
+    """ops::mat_mul with B as [N][K] (the reference's layout; inner dimension N here) runs the bf16x6
+    kernel with B transposed while staged; same fp32-level bar as the nk form, ragged tiles and a
+    tail of the inner dimension (1000 = 31 x 32 + 8)."""
+    rng = np.random.default_rng(SEED + M + 1)
+    A = rng.standard_normal((M, N)).astype(np.float32)
+    B = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    C = ow.DeviceBuffer.empty(M * K)
+    dA, dB = upload(ow, A.ravel()), upload(ow, B.ravel())
+    ow.ops.mat_mul(dA, dB, C, M, N, K)
+    got = C.to_host().reshape(M, K)
+    sample = np.unique(np.concatenate([np.arange(0, M, 37), [M - 1]]))
+    As, B64 = A[sample].astype(np.float64), B.astype(np.float64)
+    check_kscaled(got[sample], As @ B64, np.abs(As) @ np.abs(B64), tol=2e-6, floor=0.0)
+
+
 @pytest.mark.slow
 def test_config3_full_size_sampled(ow, orc):
     """Config 3: C = relu(A @ B + bias), M = N = K = 4096, A, B ~ N(0, 1/64), bias ~ U[-0.1, 0.1];
