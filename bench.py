@@ -363,7 +363,7 @@ def wl_linear(stream, steps, warmup):
     # flops against the fp32 MFMA peak, `mfma_executed` the bf16 MFMA work actually issued.
     executed = 6.0 * flop / ms / 1e9
     return {"workload": "linear_f32_4096^3_hf_weights", "unit": "TFLOP/s", "value": tf, "ms": ms, "flop": flop,
-            "kernel": "gemm_x6_kernel (bf16x6 products)",
+            "kernel": "gemm_x6_kernel<nk> (bf16x6 products)",
             "roofline": roofline(tf, FP32_PEAK_TFLOPS, "TFLOP/s", "mfma", traffic=profiled_traffic("linear_x6")),
             "mfma_executed": {"dtype": "bf16", "flop_per_launch": 6.0 * flop, "achieved": round(executed, 2),
                               "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
