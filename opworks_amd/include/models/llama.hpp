@@ -777,9 +777,9 @@ template <typename WT> class LlamaModelT final : public LlamaRuntime {
             return detail::gemm_f32_launch_splitk<detail::BLayout::nk, IdentityEpilogue, kStore>(
                 A, W, nullptr, C, M, N, K, IdentityEpilogue{}, s.workspace.splitk.data(), s.workspace.splitk.size(), st,
                 reduce);
-        } else {
-            detail::gemm_f32_launch<detail::BLayout::nk, IdentityEpilogue, kStore>(A, W, nullptr, C, M, N, K,
-                                                                                  IdentityEpilogue{}, st, 1, false);
+        } else { // the gate/up projection (SwiGLU store) on bf16x6 products, the others fp32 MFMA
+            detail::gemm_f32_launch<detail::BLayout::nk, IdentityEpilogue, kStore>(
+                A, W, nullptr, C, M, N, K, IdentityEpilogue{}, st, 1, kStore == detail::GemmStore::swiglu);
         }
         return false;
     }

@@ -493,10 +493,11 @@ namespace opworks::detail {
 
 // The fp32 products that the bf16x6 kernel takes: fp32 operands, A row-major, 16-byte aligned,
 // K a multiple of 8 (and N of 4 for a kn-layout B), and enough work to fill its 128 x 256 tiles
-// (at 4096^3 nk: 1003 -> 673 us, 1.30 of the fp32 MFMA peak; 512 x 16384 x 2048: 279 -> 179 us), for plain stores (the
-// operator API's products). Callers that need the fp32 MFMA kernels' summation (the Llama runtime,
-// held to the oracle's logits at 1e-5, whose config-5 run read 1.05e-5 through bf16x6 against 9.27e-6)
-// pass allow_x6 = false; the split-K form (the runtime's) never takes it.
+// (at 4096^3 nk: 1003 -> 673 us, 1.30 of the fp32 MFMA peak; 512 x 16384 x 2048: 279 -> 179 us), for plain
+// and SwiGLU stores. Callers that need the fp32 MFMA kernels' summation pass allow_x6 = false; the
+// split-K form never takes it. The Llama runtime, held to the oracle's logits at NRMSE 1e-5, takes
+// it for the gate/up projection only: config 5's worst step read 9.27e-6 on fp32 MFMAs, 9.94e-6 with
+// gate/up on bf16x6 (fp32 TTFT 9.57 -> 8.10 ms), 1.05e-5 with every projection on it.
 // OPWORKS_GEMM_X6=0 in the environment keeps every product on the fp32 MFMA kernels.
 inline bool gemm_x6_enabled() {
     static const bool enabled = [] {
@@ -507,7 +508,8 @@ inline bool gemm_x6_enabled() {
 }
 template <BLayout kB, GemmStore kStore, typename TB, ALayout kAL>
 inline bool gemm_use_x6(const float *A, const TB *B, int M, int N, int K) {
-    if constexpr (std::is_same_v<TB, float> && kAL == ALayout::mk && kStore == GemmStore::store) {
+    if constexpr (std::is_same_v<TB, float> && kAL == ALayout::mk &&
+                  (kStore == GemmStore::store || kStore == GemmStore::swiglu)) {
         return M >= 16 && int64_t(M) * N * K >= (int64_t(1) << 26) && gemm_x6_ok<kB>(A, B, N, K) &&
                gemm_x6_enabled();
     } else {
@@ -524,7 +526,8 @@ template <BLayout kB, typename Epi, GemmStore kStore = GemmStore::store, typenam
 void gemm_f32_launch(const float *A, const TB *B, const float *bias, float *C, int M, int N, int K, Epi epi,
                      hipStream_t stream, int splits = 1, bool allow_x6 = true) {
     require(kStore != GemmStore::swiglu || N % 2 == 0, "swiglu epilogue needs an even number of columns");
-    if constexpr (std::is_same_v<TB, float> && kAL == ALayout::mk && kStore == GemmStore::store) {
+    if constexpr (std::is_same_v<TB, float> && kAL == ALayout::mk &&
+                  (kStore == GemmStore::store || kStore == GemmStore::swiglu)) {
         if (allow_x6 && gemm_use_x6<kB, kStore, TB, kAL>(A, B, M, N, K)) {
             gemm_x6_launch<kB, Epi, kStore>(A, B, bias, C, M, N, K, epi, stream, splits);
             return;
