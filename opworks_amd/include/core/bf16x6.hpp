@@ -14,10 +14,10 @@ namespace opworks::detail {
 // An fp32 value splits exactly into three bf16 parts, x = x0 + x1 + x2 (each round to nearest
 // of the remaining residual; 3 x 8 significand bits cover fp32's 24). A product keeps the six
 // terms with i + j <= 2, x_i y_j, each exact in fp32, accumulated by the MFMA in fp32; the
-// dropped terms are below 2^-24 of |x y|. Dot products then carry fp32's error (checked in
-// float64 against fp32 sums of length 64: the same worst case, 6.7e-8 of sum |x y|), at 16
-// cycles per 16x16x32 bf16 MFMA against 32 per 16x16x4 fp32 one: per 16x16x64 block, 12 x 16
-// against 16 x 32 cycles.
+// dropped terms x1 y2, x2 y1 (each at most 2^-24 of |x y|) and x2 y2 stay within 2^-23. Dot
+// products then carry fp32's error (checked in float64 against fp32 sums of length 64: the same
+// worst case, 6.7e-8 of sum |x y|), at 16 cycles per 16x16x32 bf16 MFMA against 32 per 16x16x4
+// fp32 one: per 16x16x64 block, 12 x 16 against 16 x 32 cycles.
 using bf16x8v = __bf16 __attribute__((ext_vector_type(8)));
 using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
 

@@ -5,8 +5,8 @@
 // W [N][K] (nk, the HF weight layout) or B [K][N] (kn, the reference's mat_mul); 16-byte aligned,
 // K a multiple of 8, and N a multiple of 4 for kn. Every fp32 operand value splits
 // exactly into three bf16 parts and each product keeps the six terms x_i y_j with i + j <= 2,
-// accumulated in fp32 by the MFMA: the products carry fp32's error (the dropped terms are below
-// 2^-24 of |x y|), on 16-cycle 16x16x32 bf16 MFMAs. Per 16x16x32 block of products that is
+// accumulated in fp32 by the MFMA: the products carry fp32's error (each dropped term is at most
+// 2^-24 of |x y|, 2^-23 together), on 16-cycle 16x16x32 bf16 MFMAs. Per 16x16x32 block of products that is
 // 6 x 16 = 96 matrix-core cycles against 8 x 32 = 256 on 16x16x4 fp32 MFMAs.
 //
 // Kernel shape (gfx950): 128 x 256 outputs per workgroup, 512 lanes as 2 x 4 waves of 64 x 64
