@@ -6,8 +6,8 @@
 // K a multiple of 8, and N a multiple of 4 for kn. Every fp32 operand value splits
 // exactly into three bf16 parts and each product keeps the six terms x_i y_j with i + j <= 2,
 // accumulated in fp32 by the MFMA: the products carry fp32's error (each dropped term is at most
-// 2^-24 of |x y|, 2^-23 together), on 16-cycle 16x16x32 bf16 MFMAs. Per 16x16x32 block of products that is
-// 6 x 16 = 96 matrix-core cycles against 8 x 32 = 256 on 16x16x4 fp32 MFMAs.
+// 2^-24 of |x y|, 2^-23 together), on 16-cycle 16x16x32 bf16 MFMAs. Per 16x16x32 block of
+// products that is 6 x 16 = 96 matrix-core cycles against 8 x 32 = 256 on 16x16x4 fp32 MFMAs.
 //
 // Kernel shape (gfx950): 128 x 256 outputs per workgroup, 512 lanes as 2 x 4 waves of 64 x 64
 // (4 x 4 16x16 accumulator tiles); K steps of 32. Each step's fp32 tiles are loaded into
@@ -16,7 +16,7 @@
 // way (each thread holds 4 k x 4 n and writes 8-byte pieces of n-major rows). Plane rows are 64 bytes with
 // their 16-byte chunks swizzled (x6_k_chunk<32>, measured conflict-free for these reads). A
 // wave reads its 3 x (4 + 4) fragments of a step and issues 6 x 16 MFMAs, smallest terms first,
-// with the next step's split and LDS writes issued among the last two terms.
+// with the next step's split and LDS writes interleaved with the last two terms' MFMAs.
 
 // Included by gemm_f32.hpp ahead of its launchers, which send fp32 products here; it
 // uses that header's GemmStore, gemm_tile_of and IdentityEpilogue. Include gemm_f32.hpp, not this.
@@ -176,18 +176,30 @@ __global__ __launch_bounds__(GemmX6Shape::kThreads) void gemm_x6_kernel(const fl
 #pragma unroll
         for (int bn = 0; bn < FN; ++bn)
             rb16(2, bn);
+        auto terms = [&](int t0, int t1) {
 #pragma unroll
-        for (int term = 0; term < 6; ++term) {
-            if (term == 4)
-                mid();
+            for (int term = t0; term < t1; ++term)
 #pragma unroll
-            for (int bm = 0; bm < FM; ++bm)
+                for (int bm = 0; bm < FM; ++bm)
 #pragma unroll
-                for (int bn = 0; bn < FN; ++bn) {
-                    const bf16x8v a[3] = {fa[0][bm], fa[1][bm], fa[2][bm]};
-                    const bf16x8v b[3] = {fb[0][bn], fb[1][bn], fb[2][bn]};
-                    acc[bm][bn] = mfma_x6_term(term, a, b, acc[bm][bn]);
-                }
+                    for (int bn = 0; bn < FN; ++bn) {
+                        const bf16x8v a[3] = {fa[0][bm], fa[1][bm], fa[2][bm]};
+                        const bf16x8v b[3] = {fb[0][bn], fb[1][bn], fb[2][bn]};
+                        acc[bm][bn] = mfma_x6_term(term, a, b, acc[bm][bn]);
+                    }
+        };
+        terms(0, 4);
+        // The last two terms' 2 x 16 MFMAs interleaved with `mid`'s split (VALU) and LDS writes:
+        // a wave issues in order, so without this its MFMAs wait behind the whole split (4096^3:
+        // kn 209 -> 218-220 TFLOP/s, nk 223 -> 230; the same from the fourth term on).
+        __builtin_amdgcn_sched_barrier(0);
+        mid();
+        terms(4, 6);
+#pragma unroll
+        for (int i = 0; i < 2 * FM * FN; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0); // up to five VALU
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0); // up to one LDS write
         }
     };
 
